@@ -1,0 +1,198 @@
+// Row softmax over the last dimension for gfx950 (reference.py:14-17).
+//
+// HBM-bound: each row is read once into registers (as fp32), reduced for its
+// max and for sum(exp(x - max)) with wave64 DPP reductions, then normalised
+// and written once. Rows up to 64*8 16-byte vectors are owned by one wave
+// (no barriers), wider rows by a 256- or 1024-thread workgroup. Rows are
+// indexed with 64-bit arithmetic and every row gets its own owner, so there
+// is no grid-size cap on the row count.
+//
+// -inf logits give exp2(-inf) = 0 exactly; a row with a single finite entry
+// returns exactly 1.0 there. The file is built without fast-math so those
+// IEEE special cases are honoured.
+#include "ak_common.h"
+
+namespace ak {
+namespace {
+
+template <typename T, int VPT, int TPR>
+__global__ void __launch_bounds__(TPR >= 256 ? TPR : 256)
+softmax_vec_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
+                   int64_t ld_x, int64_t ld_y) {
+  constexpr int VE = Vec16<T>::VE;
+  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_WG + threadIdx.x / TPR;
+  if (TPR == 64 && row >= rows) return;
+  const int nvec = cols / VE;
+  const T* xr = x + row * ld_x;
+
+  float v[VPT][VE];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int c = t + k * TPR;
+    if (c < nvec) {
+      Vec16<T> xv = load16(xr + (int64_t)c * VE);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        v[k][e] = to_f32(xv.e[e]);
+        m = fmaxf(m, v[k][e]);
+      }
+    }
+  }
+  m = wave_max(m);
+  __shared__ float part[TPR > 64 ? TPR / 64 : 1];
+  if constexpr (TPR > 64) {
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = m;
+    __syncthreads();
+    m = part[0];
+#pragma unroll
+    for (int i = 1; i < TPR / 64; ++i) m = fmaxf(m, part[i]);
+    __syncthreads();
+  }
+
+  // exp(x - m): the max element gives exp2(0) = 1 exactly.
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int c = t + k * TPR;
+    if (c < nvec) {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        v[k][e] = fast_exp(v[k][e] - m);
+        s += v[k][e];
+      }
+    }
+  }
+  s = wave_sum(s);
+  if constexpr (TPR > 64) {
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = s;
+    __syncthreads();
+    s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPR / 64; ++i) s += part[i];
+  }
+  const float inv = 1.0f / s;
+
+  T* yr = y + row * ld_y;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int c = t + k * TPR;
+    if (c < nvec) {
+      Vec16<T> o;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) o.e[e] = from_f32<T>(v[k][e] * inv);
+      store16(yr + (int64_t)c * VE, o);
+    }
+  }
+}
+
+// Online (max, sum) state: sum is relative to max.
+struct MaxSum {
+  float m, s;
+};
+
+__device__ __forceinline__ MaxSum combine(MaxSum a, MaxSum b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return {m, 0.0f};
+  const float sa = a.m == -INFINITY ? 0.0f : a.s * fast_exp(a.m - m);
+  const float sb = b.m == -INFINITY ? 0.0f : b.s * fast_exp(b.m - m);
+  return {m, sa + sb};
+}
+
+// Any width / alignment: one 256-thread workgroup per row, two passes over
+// global memory (online max/sum, then normalise).
+template <typename T>
+__global__ void __launch_bounds__(256)
+softmax_generic_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
+                       int64_t ld_x, int64_t ld_y) {
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ld_x;
+  MaxSum st{-INFINITY, 0.0f};
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    const float v = to_f32(xr[c]);
+    if (v > st.m) {
+      // exp(v - v) is 1, or NaN for v = +inf, as in the reference op.
+      st.s = st.s * fast_exp(st.m - v) + fast_exp(v - v);
+      st.m = v;
+    } else if (v != v) {
+      st = {v, v};  // NaN poisons the row
+    } else if (v != -INFINITY) {
+      st.s += fast_exp(v - st.m);
+    }
+  }
+  // wave-level combine through shuffles
+  for (int off = 1; off < 64; off <<= 1) {
+    MaxSum o{__shfl_xor(st.m, off, 64), __shfl_xor(st.s, off, 64)};
+    st = (st.m != st.m || o.m != o.m) ? MaxSum{NAN, NAN} : combine(st, o);
+  }
+  __shared__ MaxSum part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = st;
+  __syncthreads();
+  st = part[0];
+  for (int i = 1; i < 4; ++i) {
+    st = (st.m != st.m || part[i].m != part[i].m) ? MaxSum{NAN, NAN} : combine(st, part[i]);
+  }
+  const float inv = 1.0f / st.s;
+  T* yr = y + row * ld_y;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    yr[c] = from_f32<T>(fast_exp(to_f32(xr[c]) - st.m) * inv);
+  }
+}
+
+template <typename T, int VPT, int TPR>
+void launch_vec(const T* x, T* y, int64_t rows, int cols, int64_t ld_x, int64_t ld_y,
+                hipStream_t s) {
+  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
+  const int64_t grid = (rows + ROWS_PER_WG - 1) / ROWS_PER_WG;
+  softmax_vec_kernel<T, VPT, TPR><<<dim3((unsigned)grid), dim3(TPR * ROWS_PER_WG), 0, s>>>(
+      x, y, rows, cols, ld_x, ld_y);
+}
+
+template <typename T>
+int dispatch(const void* xv, void* yv, int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_y,
+             hipStream_t s) {
+  const T* x = static_cast<const T*>(xv);
+  T* y = static_cast<T*>(yv);
+  constexpr int VE = Vec16<T>::VE;
+  const bool vec_ok = cols % VE == 0 && ld_x % VE == 0 && ld_y % VE == 0 && aligned16(x) &&
+                      aligned16(y);
+  const int64_t nvec = cols / VE;
+  const int c = (int)cols;
+  if (vec_ok && nvec <= 64 * 8) {
+    if (nvec <= 64) launch_vec<T, 1, 64>(x, y, rows, c, ld_x, ld_y, s);
+    else if (nvec <= 128) launch_vec<T, 2, 64>(x, y, rows, c, ld_x, ld_y, s);
+    else if (nvec <= 256) launch_vec<T, 4, 64>(x, y, rows, c, ld_x, ld_y, s);
+    else launch_vec<T, 8, 64>(x, y, rows, c, ld_x, ld_y, s);
+  } else if (vec_ok && nvec <= 256 * 8) {
+    if (nvec <= 256 * 4) launch_vec<T, 4, 256>(x, y, rows, c, ld_x, ld_y, s);
+    else launch_vec<T, 8, 256>(x, y, rows, c, ld_x, ld_y, s);
+  } else if (vec_ok && nvec <= 1024 * 8) {
+    launch_vec<T, 8, 1024>(x, y, rows, c, ld_x, ld_y, s);
+  } else {
+    softmax_generic_kernel<T><<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, y, rows, c, ld_x, ld_y);
+  }
+  return ak_check_launch("ak_softmax_fwd");
+}
+
+}  // namespace
+}  // namespace ak
+
+extern "C" int ak_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, int64_t ld_x,
+                              int64_t ld_y, int dtype, void* stream) {
+  const char* name = "ak_softmax_fwd";
+  if (ak_dtype_size(dtype) == 0) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", name, dtype);
+  if (rows < 0 || cols <= 0 || cols > (int64_t)1 << 30)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape rows=%lld cols=%lld", name, (long long)rows, (long long)cols);
+  if (rows > 0xFFFFFFFFll) return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld exceeds 2^32-1", name, (long long)rows);
+  if (ld_x < cols || ld_y < cols) return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  if (rows == 0) return AK_OK;
+  if (!x || !y) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  hipStream_t s = ak_stream(stream);
+  switch (dtype) {
+    case AK_DTYPE_F32: return ak::dispatch<float>(x, y, rows, cols, ld_x, ld_y, s);
+    case AK_DTYPE_F16: return ak::dispatch<ak::f16>(x, y, rows, cols, ld_x, ld_y, s);
+    default: return ak::dispatch<ak::bf16>(x, y, rows, cols, ld_x, ld_y, s);
+  }
+}

@@ -1,0 +1,261 @@
+"""Loader for the prebuilt gfx950 kernel library (``libautokernel_gfx950.so``).
+
+Replaces the reference's JIT loader ``kernels/hip/_compile.py:210-369``
+(``compile_hip`` -> ``torch.utils.cpp_extension.load_inline``): the kernels
+are compiled ahead of time for gfx950 only (``csrc/Makefile``) and reached
+through the C ABI declared in ``include/autokernel_mi355x.h``.
+
+The library is opened after ``import torch`` so that its ``libamdhip64.so.7``
+dependency resolves to the HIP runtime torch has already loaded: kernels
+launch on torch's current stream and use torch's device memory.
+
+Every launcher here takes torch tensors, checks shapes and devices on the
+host, and forwards raw pointers, element pitches and the current stream to
+one ``extern "C"`` entry point. A non-zero return raises ``RuntimeError``
+carrying ``ak_last_error()``. There is no CPU or PyTorch fallback: a missing
+library or a non-GPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+LIB_NAME = "libautokernel_gfx950.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+CSRC_DIR = os.path.normpath(os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "..", "csrc"))
+
+AK_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+FLOAT_DTYPES = tuple(AK_DTYPE)
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+_SIGNATURES = {
+    "ak_last_error": [],
+    "ak_abi_version": [],
+    "ak_target_arch": [],
+    "ak_rmsnorm_fwd": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
+    "ak_fused_add_rmsnorm_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                                 _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
+    "ak_softmax_fwd": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
+    "ak_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                  _i64, _i64, _i64, _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
+    "ak_ce_bwd_tiny": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                       _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
+    "ak_lmhead_ce_workspace_bytes": [_i64, _i64],
+    "ak_lmhead_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                         _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                         _c_void_p],
+    "ak_selective_scan_fwd": [_c_void_p] * 10 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
+    "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
+}
+_RESTYPES = {
+    "ak_last_error": ctypes.c_char_p,
+    "ak_target_arch": ctypes.c_char_p,
+    "ak_lmhead_ce_workspace_bytes": ctypes.c_size_t,
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+class HipExtensionMissing(RuntimeError):
+    """The gfx950 kernel library has not been built."""
+
+
+def lib_path() -> str:
+    return os.environ.get("AUTOKERNEL_GFX950_LIB", LIB_PATH)
+
+
+def load() -> ctypes.CDLL:
+    """Open the kernel library (once) and declare every entry point."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = lib_path()
+            if not os.path.exists(path):
+                raise HipExtensionMissing(
+                    f"{path} is missing: build it with `make -C {CSRC_DIR}` "
+                    "or `python -c 'import __graft_entry__ as g; g.build()'`")
+            handle = ctypes.CDLL(path)
+            for name, argtypes in _SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = handle
+    return _lib
+
+
+def is_available() -> bool:
+    return os.path.exists(lib_path())
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().ak_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_device(*tensors: Optional[torch.Tensor]) -> None:
+    """Raise unless every given tensor lives on one GPU."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "autokernel gfx950 kernels need GPU tensors (got a tensor on "
+                f"{t.device}); there is no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return AK_DTYPE[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected one of float32, float16, bfloat16")
+
+
+def _rows_view(t: torch.Tensor, name: str) -> int:
+    """Row pitch (elements) of a 2-D view whose last dim is contiguous."""
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.size(1) > 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+    return max(t.stride(0), t.size(1)) if t.size(0) > 1 else t.size(1)
+
+
+# ---------------------------------------------------------------------------
+# Launchers (tensor-level). Outputs are preallocated by the caller.
+# ---------------------------------------------------------------------------
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor, eps: float) -> None:
+    require_device(x, weight, y)
+    rows, cols = x.shape
+    with torch.cuda.device(x.device):
+        rc = load().ak_rmsnorm_fwd(_ptr(x), _ptr(weight), _ptr(y), rows, cols,
+                                   _rows_view(x, "x"), _rows_view(y, "y"), float(eps),
+                                   dtype_code(x.dtype), _stream(x))
+    _check(rc, "ak_rmsnorm_fwd")
+
+
+def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                      new_residual: Optional[torch.Tensor], y: torch.Tensor, eps: float) -> None:
+    require_device(x, residual, weight, new_residual, y)
+    rows, cols = x.shape
+    ld_nr = _rows_view(new_residual, "new_residual") if new_residual is not None else cols
+    with torch.cuda.device(x.device):
+        rc = load().ak_fused_add_rmsnorm_fwd(
+            _ptr(x), _ptr(residual), _ptr(weight), _ptr(new_residual), _ptr(y), rows, cols,
+            _rows_view(x, "x"), _rows_view(residual, "residual"), ld_nr, _rows_view(y, "y"),
+            float(eps), dtype_code(x.dtype), _stream(x))
+    _check(rc, "ak_fused_add_rmsnorm_fwd")
+
+
+def softmax(x: torch.Tensor, y: torch.Tensor) -> None:
+    require_device(x, y)
+    rows, cols = x.shape
+    with torch.cuda.device(x.device):
+        rc = load().ak_softmax_fwd(_ptr(x), _ptr(y), rows, cols, _rows_view(x, "x"),
+                                   _rows_view(y, "y"), dtype_code(x.dtype), _stream(x))
+    _check(rc, "ak_softmax_fwd")
+
+
+def ce_fwd(logits: torch.Tensor, targets: torch.Tensor, losses: torch.Tensor, lse: torch.Tensor,
+           row_max: Optional[torch.Tensor], row_sum: Optional[torch.Tensor],
+           grad: Optional[torch.Tensor], softcap: float, ignore_index: int,
+           label_smoothing: float, scale_grad: float) -> None:
+    require_device(logits, targets, losses, lse, row_max, row_sum, grad)
+    rows, vocab = logits.shape
+    ld_g = _rows_view(grad, "grad") if grad is not None else vocab
+    with torch.cuda.device(logits.device):
+        rc = load().ak_ce_fwd(_ptr(logits), _ptr(targets), _ptr(losses), _ptr(lse), _ptr(row_max),
+                              _ptr(row_sum), _ptr(grad), rows, vocab, _rows_view(logits, "logits"),
+                              ld_g, float(softcap), int(ignore_index), float(label_smoothing),
+                              float(scale_grad), dtype_code(logits.dtype), _stream(logits))
+    _check(rc, "ak_ce_fwd")
+
+
+def ce_bwd_tiny(logits: torch.Tensor, targets: torch.Tensor, row_max: torch.Tensor,
+                row_sum: torch.Tensor, grad: torch.Tensor, softcap: float, ignore_index: int,
+                label_smoothing: float, scale_grad: float) -> None:
+    require_device(logits, targets, row_max, row_sum, grad)
+    rows, vocab = logits.shape
+    with torch.cuda.device(logits.device):
+        rc = load().ak_ce_bwd_tiny(_ptr(logits), _ptr(targets), _ptr(row_max), _ptr(row_sum),
+                                   _ptr(grad), rows, vocab, _rows_view(logits, "logits"),
+                                   _rows_view(grad, "grad"), float(softcap), int(ignore_index),
+                                   float(label_smoothing), float(scale_grad),
+                                   dtype_code(logits.dtype), _stream(logits))
+    _check(rc, "ak_ce_bwd_tiny")
+
+
+def lmhead_ce_workspace_bytes(n_rows: int, vocab: int) -> int:
+    return int(load().ak_lmhead_ce_workspace_bytes(n_rows, vocab))
+
+
+def lmhead_ce(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+              loss: torch.Tensor, lse: torch.Tensor, losses: Optional[torch.Tensor],
+              n_valid: Optional[torch.Tensor], workspace: torch.Tensor, ignore_index: int) -> None:
+    require_device(hidden, weight, targets, loss, lse, losses, n_valid, workspace)
+    n_rows, d = hidden.shape
+    vocab = weight.shape[0]
+    with torch.cuda.device(hidden.device):
+        rc = load().ak_lmhead_ce_fwd(
+            _ptr(hidden), _ptr(weight), _ptr(targets), _ptr(loss), _ptr(lse), _ptr(losses),
+            _ptr(n_valid), _ptr(workspace), workspace.numel() * workspace.element_size(),
+            n_rows, vocab, d, _rows_view(hidden, "hidden"), _rows_view(weight, "weight"),
+            int(ignore_index), dtype_code(hidden.dtype), _stream(hidden))
+    _check(rc, "ak_lmhead_ce_fwd")
+
+
+def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool) -> None:
+    """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l]; A [d, n]."""
+    require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state)
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    ngroups = B.shape[1]
+    zs = (z.stride(0), z.stride(1)) if z is not None else (0, 0)
+    with torch.cuda.device(u.device):
+        rc = load().ak_selective_scan_fwd(
+            _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(delta_bias),
+            _ptr(out), _ptr(last_state),
+            batch, dim, seqlen, dstate, ngroups,
+            u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
+            B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),
+            zs[0], zs[1], out.stride(0), out.stride(1),
+            int(bool(delta_softplus)), dtype_code(u.dtype), dtype_code(delta.dtype),
+            dtype_code(B.dtype), _stream(u))
+    _check(rc, "ak_selective_scan_fwd")
+
+
+def diag_scan(dA, dBx, C, D, x, y) -> None:
+    require_device(dA, dBx, C, D, x, y)
+    batch, seqlen, d_inner = dA.shape
+    with torch.cuda.device(dA.device):
+        rc = load().ak_diag_scan_fwd(_ptr(dA), _ptr(dBx), _ptr(C), _ptr(D), _ptr(x), _ptr(y),
+                                     batch, seqlen, d_inner, _stream(dA))
+    _check(rc, "ak_diag_scan_fwd")

@@ -1,0 +1,175 @@
+"""Linear (lm-head) + cross-entropy without materialised logits, gfx950.
+
+Drop-in for the reference module ``kernels/hip/chunked_linear_cross_entropy.py``
+(``ChunkedLinearCrossEntropyLoss`` :178-229, ``_ChunkedLinearCrossEntropy``
+:50-175): same constructor arguments, same ``forward(hidden, weight,
+targets)`` contract, autograd for ``hidden`` and ``weight``.
+
+Forward (plain CE, bf16/fp16, ``d % 64 == 0``): one fused kernel,
+``ak_lmhead_ce_fwd`` (``csrc/lmhead_ce.hip``), computes ``hidden @ weight^T``
+tile by tile on the matrix cores and folds each tile into an online
+logsumexp, so the ``[N, V]`` logits never exist in memory and there is no
+host synchronisation. It returns the mean loss over non-ignored rows and
+the per-row logsumexp (used by the z-loss and by the backward).
+
+With ``softcap`` or ``label_smoothing`` set, or for fp32 / unaligned inputs,
+the forward runs the reference's row-chunked algorithm: per ``chunk_size``
+rows a GEMM (``torch.nn.functional.linear``) feeds the gfx950 CE row kernel.
+
+Backward: per row chunk the logits are recomputed with a GEMM and turned
+into ``dL/dlogits`` by the CE row kernel from the saved logsumexp, then
+``grad_hidden = dlogits @ W`` and ``grad_W += dlogits^T @ h`` (fp32
+accumulation), as in the reference (``:97-132``). As in the reference, the
+z-loss term contributes to the returned loss only, not to the gradient.
+
+``chunk_size`` is the row-chunk of the GEMM paths; the fused forward tiles
+the vocabulary itself. Inputs keep their dtype (the reference coerced
+everything to fp16).
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from kernels.hip import _lib
+
+
+def _fused_ok(hidden: torch.Tensor, weight: torch.Tensor, softcap: float,
+              label_smoothing: float) -> bool:
+    return (softcap == 0.0 and label_smoothing == 0.0
+            and hidden.dtype in (torch.bfloat16, torch.float16) and weight.dtype == hidden.dtype
+            and hidden.shape[1] % 64 == 0
+            and hidden.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                      ignore_index: int = -100, return_losses: bool = False):
+    """Fused forward: returns ``(loss, lse, n_valid)`` (+ per-row losses).
+
+    ``loss`` is a 0-d fp32 tensor (mean over non-ignored rows), ``lse`` fp32
+    ``[N]``, ``n_valid`` a 1-element int64 tensor. No host synchronisation.
+    """
+    _lib.require_device(hidden, weight, targets)
+    hidden = hidden.contiguous()
+    weight = weight.contiguous()
+    targets = targets.contiguous().to(torch.int64)
+    n = hidden.shape[0]
+    dev = hidden.device
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    lse = torch.empty(n, dtype=torch.float32, device=dev)
+    n_valid = torch.empty(1, dtype=torch.int64, device=dev)
+    losses = torch.empty(n, dtype=torch.float32, device=dev) if return_losses else None
+    ws = torch.empty(_lib.lmhead_ce_workspace_bytes(n, weight.shape[0]), dtype=torch.uint8, device=dev)
+    _lib.lmhead_ce(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index)
+    if return_losses:
+        return loss, lse, n_valid, losses
+    return loss, lse, n_valid
+
+
+def _chunked_forward(hidden, weight, targets, chunk_size, softcap, ignore_index, label_smoothing):
+    """Row-chunked GEMM + CE row kernel; returns (loss_sum, lse, n_valid float tensor)."""
+    from kernels.ce_fused import _get_fwd_module
+    mod = _get_fwd_module()
+    n = hidden.shape[0]
+    lse = torch.empty(n, dtype=torch.float32, device=hidden.device)
+    loss_sum = torch.zeros((), dtype=torch.float32, device=hidden.device)
+    for start in range(0, n, chunk_size):
+        end = min(start + chunk_size, n)
+        logits = F.linear(hidden[start:end], weight)
+        t = targets[start:end]
+        losses, lse_c, _, _, _ = mod.cross_entropy_fwd_hip(
+            logits, t, float(softcap), int(ignore_index), float(label_smoothing), 0, 0, 1.0)
+        lse[start:end] = lse_c
+        loss_sum = loss_sum + (losses * (t != ignore_index).to(torch.float32)).sum()
+    n_valid = (targets != ignore_index).sum().to(torch.float32).clamp(min=1.0)
+    return loss_sum / n_valid, lse, n_valid
+
+
+class _ChunkedLinearCrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, targets, chunk_size, softcap, ignore_index,
+                label_smoothing, z_loss_weight):
+        targets = targets.contiguous().to(torch.int64)
+        if _fused_ok(hidden, weight, softcap, label_smoothing):
+            loss, lse, n_valid_i = lmhead_ce_forward(hidden, weight, targets, ignore_index)
+            n_valid = n_valid_i.to(torch.float32).clamp(min=1.0).reshape(())
+        else:
+            loss, lse, n_valid = _chunked_forward(hidden.contiguous(), weight.contiguous(), targets,
+                                                  chunk_size, softcap, ignore_index,
+                                                  label_smoothing)
+        if z_loss_weight > 0:
+            valid = (targets != ignore_index).to(torch.float32)
+            loss = loss + z_loss_weight * ((lse * valid).pow(2).sum() / n_valid)
+        ctx.save_for_backward(hidden, weight, targets, lse, n_valid)
+        ctx.chunk_size = int(chunk_size)
+        ctx.softcap = float(softcap)
+        ctx.ignore_index = int(ignore_index)
+        ctx.label_smoothing = float(label_smoothing)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        from kernels.ce_fused import _get_bwd_module
+        hidden, weight, targets, lse, n_valid = ctx.saved_tensors
+        need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        grad_hidden = torch.empty_like(hidden) if need_h else None
+        grad_weight = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device) if need_w else None
+        if need_h or need_w:
+            # one host sync for the scalar scale, as in the reference (:160)
+            scale = float(grad_output.item()) / float(n_valid.item())
+            ones = torch.ones_like(lse)
+            bwd = _get_bwd_module()
+            w = weight.contiguous()
+            h = hidden.contiguous()
+            n = h.shape[0]
+            for start in range(0, n, ctx.chunk_size):
+                end = min(start + ctx.chunk_size, n)
+                logits = F.linear(h[start:end], w)
+                # softmax = exp(x - lse) / 1: pass lse as the row max and 1 as the row sum
+                glog = bwd.cross_entropy_bwd_tiny_hip(
+                    logits, targets[start:end], lse[start:end], ones[start:end], ctx.softcap,
+                    ctx.ignore_index, ctx.label_smoothing, scale)
+                if need_h:
+                    grad_hidden[start:end] = glog @ w
+                if need_w:
+                    grad_weight.addmm_(glog.t().to(torch.float32), h[start:end].to(torch.float32))
+            if need_w:
+                grad_weight = grad_weight.to(weight.dtype)
+        return grad_hidden, grad_weight, None, None, None, None, None, None
+
+
+class ChunkedLinearCrossEntropyLoss(nn.Module):
+    """Drop-in for ``nn.Linear`` + ``nn.CrossEntropyLoss`` without materialised logits.
+
+    Args:
+        chunk_size: rows per chunk for the GEMM-based paths (backward, and the
+            forward when softcap / label smoothing are on).
+        softcap: logit softcap (0 = off).
+        ignore_index: target value to mask (default -100).
+        label_smoothing: alpha (0 = off).
+        z_loss_weight: if > 0, adds ``z * mean(lse^2)`` over non-ignored rows.
+    """
+
+    def __init__(self, chunk_size: int = 512, softcap: float = 0.0, ignore_index: int = -100,
+                 label_smoothing: float = 0.0, z_loss_weight: float = 0.0):
+        super().__init__()
+        self.chunk_size = int(chunk_size)
+        self.softcap = float(softcap)
+        self.ignore_index = int(ignore_index)
+        self.label_smoothing = float(label_smoothing)
+        self.z_loss_weight = float(z_loss_weight)
+
+    def forward(self, hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+        if hidden.dim() == 3:
+            b, t, d = hidden.shape
+            hidden = hidden.reshape(b * t, d)
+        if targets.dim() == 2:
+            targets = targets.reshape(-1)
+        _lib.require_device(hidden, weight, targets)
+        if weight.dtype != hidden.dtype:
+            weight = weight.to(hidden.dtype)
+        return _ChunkedLinearCrossEntropy.apply(
+            hidden, weight, targets, self.chunk_size, self.softcap, self.ignore_index,
+            self.label_smoothing, self.z_loss_weight)

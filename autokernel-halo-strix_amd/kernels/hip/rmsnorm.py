@@ -1,0 +1,48 @@
+"""AutoKernel -- RMSNorm on gfx950 (MI355X).
+
+Drop-in for the reference module ``kernels/hip/rmsnorm.py`` (``kernel_fn``
+at :156-177, launcher ``rmsnorm_hip`` at :119-143). The kernel is
+``ak_rmsnorm_fwd`` in ``csrc/rownorm.hip``: one wave64 (or one workgroup for
+very wide rows) owns a row, reads it once with 16-byte loads, reduces the
+sum of squares in fp32 with DPP, and writes ``(x / rms) * weight`` once.
+
+Differences from the reference, all deliberate:
+  * fp32, fp16 and bf16 run natively (the reference runs fp16 only; fp32
+    fell back to PyTorch and bf16 was round-tripped through fp16).
+  * ``eps`` is a keyword argument (default 1e-6, the reference constant).
+  * arithmetic is fp32 with one final rounding, following
+    ``reference.py:25-29`` with the fp32 accumulation of ``:71-78``.
+"""
+
+import os
+
+import torch
+
+from kernels.hip import _lib
+
+KERNEL_TYPE = "rmsnorm"
+BACKEND = "hip"
+
+# Location of the kernel source (the reference held the source text here).
+HIP_SRC = os.path.join(_lib.CSRC_DIR, "rownorm.hip")
+
+DEFAULT_EPS = 1e-6
+
+
+def kernel_fn(x: torch.Tensor, weight: torch.Tensor, eps: float = DEFAULT_EPS) -> torch.Tensor:
+    """RMSNorm over the last dimension. Matches ``reference.rmsnorm_ref``."""
+    _lib.require_device(x, weight)
+    _lib.dtype_code(x.dtype)
+    if weight.dim() != 1 or weight.numel() != x.shape[-1]:
+        raise ValueError(f"weight shape {tuple(weight.shape)} does not match last dim {x.shape[-1]}")
+    if weight.dtype != x.dtype:
+        weight = weight.to(x.dtype)
+    weight = weight.contiguous()
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    y = torch.empty(shape, dtype=x.dtype, device=x.device)
+    if y.numel():
+        _lib.rmsnorm(x2, weight, y.view(-1, shape[-1]), eps)
+    return y

@@ -1,0 +1,140 @@
+"""AutoKernel -- selective scans on gfx950 (MI355X).
+
+Two entry points, both drop-ins:
+
+* ``kernel_fn(dA, dBx, C, D, x)`` -- the reference's diagonal recurrence
+  (``kernels/hip/selective_scan.py:214-241``)::
+
+      state[t] = dA[t] * state[t-1] + dBx[t];   y[t] = C[t] * state[t] + D * x[t]
+
+  over fp32 ``[batch, seq, d_inner]`` tensors (``ak_diag_scan_fwd``).
+
+* ``selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+  delta_softplus=False, return_last_state=False)`` -- the Mamba-1 forward
+  with the signature of ``mamba_ssm.ops.selective_scan_interface``
+  (``external/mamba/mamba_ssm/ops/selective_scan_interface.py:106-112``),
+  computed by ``ak_selective_scan_fwd`` with fp32 state. Results follow
+  ``selective_scan_ref`` (``:115-181``) except that ``silu(z)`` is evaluated
+  in fp32 rather than in ``z``'s dtype.
+
+  Accepted layouts: ``u, delta, z`` ``[batch, dim, seqlen]`` (last dim
+  contiguous), ``A`` real ``[dim, dstate]`` with ``dstate <= 16``, ``B`` / ``C``
+  ``[batch, dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``.
+  ``delta`` may be fp32 or ``u``'s dtype; ``B`` / ``C`` fp32 or ``u``'s dtype.
+  Complex ``A`` and input-independent (2-D) ``B`` / ``C`` raise
+  ``NotImplementedError``. The backward pass is not implemented on gfx950
+  (calling it raises).
+"""
+
+import os
+
+import torch
+
+from kernels.hip import _lib
+
+KERNEL_TYPE = "selective_scan"
+BACKEND = "hip"
+
+HIP_SRC = os.path.join(_lib.CSRC_DIR, "selective_scan.hip")
+
+
+def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Tensor,
+              x: torch.Tensor) -> torch.Tensor:
+    """Diagonal SSM scan over ``[batch, seq, d_inner]`` fp32 tensors."""
+    _lib.require_device(dA, dBx, C, D, x)
+    if dA.dtype != torch.float32:
+        raise TypeError("dA must be float32")
+    if dA.dim() != 3:
+        raise ValueError("dA must be 3-D [batch, seq, d_inner]")
+    shape = dA.shape
+    for name, t in (("dBx", dBx), ("C", C), ("x", x)):
+        if t.shape != shape:
+            raise ValueError(f"{name} shape {tuple(t.shape)} != dA shape {tuple(shape)}")
+    if D.numel() != shape[2]:
+        raise ValueError("D must have d_inner elements")
+    dA, dBx, C, x = (t.float().contiguous() for t in (dA, dBx, C, x))
+    D = D.float().contiguous()
+    y = torch.empty_like(dA)
+    _lib.diag_scan(dA, dBx, C, D, x, y)
+    return y
+
+
+def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last_state):
+    _lib.require_device(u, delta, A, B, C, D, z, delta_bias)
+    if A.is_complex():
+        raise NotImplementedError("complex A is not supported by the gfx950 selective scan")
+    if B.dim() < 3 or C.dim() < 3:
+        raise NotImplementedError("input-independent (2-D) B / C are not supported; pass [b, n, l] or [b, g, n, l]")
+    if u.dim() != 3:
+        raise ValueError("u must be [batch, dim, seqlen]")
+    batch, dim, seqlen = u.shape
+    if u.stride(-1) != 1:
+        u = u.contiguous()
+    if delta.stride(-1) != 1:
+        delta = delta.contiguous()
+    if delta.shape != u.shape:
+        raise ValueError("delta must have the shape of u")
+    if B.dim() == 3:
+        B = B.unsqueeze(1)
+    if C.dim() == 3:
+        C = C.unsqueeze(1)
+    if B.stride(-1) != 1:
+        B = B.contiguous()
+    if C.stride(-1) != 1:
+        C = C.contiguous()
+    dstate = A.shape[1]
+    if A.shape[0] != dim:
+        raise ValueError("A must be [dim, dstate]")
+    if B.shape[0] != batch or B.shape[2] != dstate or B.shape[3] != seqlen or C.shape != B.shape:
+        raise ValueError(f"B / C must be [batch, ngroups, dstate, seqlen], got {tuple(B.shape)}, {tuple(C.shape)}")
+    A = A.float()
+    if A.stride(1) != 1:
+        A = A.contiguous()
+    if D is not None:
+        D = D.float().contiguous()
+    if delta_bias is not None:
+        delta_bias = delta_bias.float().contiguous()
+    if z is not None:
+        if z.shape != u.shape:
+            raise ValueError("z must have the shape of u")
+        if z.dtype != u.dtype:
+            z = z.to(u.dtype)
+        if z.stride(-1) != 1:
+            z = z.contiguous()
+    if delta.dtype not in (torch.float32, u.dtype):
+        delta = delta.float()
+    if B.dtype not in (torch.float32, u.dtype):
+        B = B.float()
+    if C.dtype != B.dtype:
+        C = C.to(B.dtype)
+    out = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=u.device)
+    last_state = (torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device)
+                  if want_last_state else None)
+    _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus)
+    return out, last_state
+
+
+class SelectiveScanFn(torch.autograd.Function):
+    """Forward on gfx950; the backward pass is not available yet and raises."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                return_last_state=False):
+        out, last_state = _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
+                                        return_last_state)
+        if return_last_state:
+            ctx.mark_non_differentiable(last_state)
+            return out, last_state
+        return out
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            "selective_scan_fn backward is not implemented on gfx950 (forward only)")
+
+
+def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                      return_last_state=False):
+    """Mamba-1 selective scan. Returns ``out`` or ``(out, last_state)``."""
+    return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
+                                 return_last_state)

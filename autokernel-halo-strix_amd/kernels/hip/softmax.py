@@ -1,0 +1,43 @@
+"""AutoKernel -- row softmax on gfx950 (MI355X).
+
+Drop-in for the reference module ``kernels/hip/softmax.py`` (``kernel_fn``
+:339-360, launcher ``softmax_hip`` :273-326). ``ak_softmax_fwd`` in
+``csrc/softmax.hip`` reads each row once into registers, reduces max and
+sum(exp) in fp32 with wave64 DPP reductions and writes the row once.
+
+Differences from the reference, all deliberate:
+  * every row is written: the reference's block kernel caps its grid at
+    65,535 rows with no row loop (``softmax.py:293``, ``:175-176``), so rows
+    beyond that were left unwritten;
+  * IEEE semantics for -inf (the reference built with ``-ffast-math``);
+    masked entries come out as exact zeros;
+  * fp16, bf16 and fp32 all run on the GPU kernel.
+Semantics: ``reference.py:14-17`` (``F.softmax(x, -1)``), fp32 accumulation.
+"""
+
+import os
+
+import torch
+
+from kernels.hip import _lib
+
+KERNEL_TYPE = "softmax"
+BACKEND = "hip"
+
+HIP_SRC = os.path.join(_lib.CSRC_DIR, "softmax.hip")
+
+
+def kernel_fn(x: torch.Tensor) -> torch.Tensor:
+    """Softmax over the last dimension of ``x`` (any rank)."""
+    _lib.require_device(x)
+    _lib.dtype_code(x.dtype)
+    shape = x.shape
+    if x.dim() == 0:
+        raise ValueError("softmax needs at least one dimension")
+    x2 = x.reshape(-1, shape[-1]) if x.dim() != 2 else x
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    y = torch.empty(shape, dtype=x.dtype, device=x.device)
+    if y.numel():
+        _lib.softmax(x2, y.view(-1, shape[-1]))
+    return y

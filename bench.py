@@ -1,0 +1,348 @@
+"""Benchmark of the gfx950 kernel set on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1,c2,...] [--no-cpu]
+
+Prints ONE JSON line. The headline (``value``) is the HBM throughput of the
+configuration BASELINE.json's metric is quoted on at one GPU, configs[1]:
+the causal-masked fp16 row softmax [8, 12, 1024, 1024] (C2). A "step" is one
+launch of that kernel over one batch of synthetic input already resident in
+HBM; ``value`` = algorithmic bytes x K / wall-clock time of the K timed steps.
+``roofline`` gives the kernel's achieved bandwidth from HIP-event kernel
+durations against MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle on
+the GPU box's host on a bounded sample of the same workload. ``kernels``
+reports every configuration (C1..C5) the same way: time per launch, GB/s or
+TFLOP/s, roofline fraction, tokens/s and the CPU figure beside it.
+
+Inputs follow the seeded draw order of the survey (a CPU torch.Generator
+seeded 0, then copied to the GPU). Input sets are rotated so that each timed
+launch reads data not left in the 256 MB MALL by the previous launch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "autokernel-halo-strix_amd")
+if PKG not in sys.path:
+    sys.path.insert(0, PKG)
+
+import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, vendor spec
+ROTATE_BYTES = 640 * 2 ** 20   # > 2x the 256 MB MALL
+
+METRIC = "HBM GB/s (% of roofline) per kernel; selective-scan Mtok/s vs CPU ref"
+
+
+# ---------------------------------------------------------------------------
+# Synthetic inputs (seed 0, CPU generator, survey draw order)
+# ---------------------------------------------------------------------------
+
+def gen_c1():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2048, 768, generator=g)
+    w = 1 + 0.02 * torch.randn(768, generator=g)
+    return {"x": x, "w": w, "eps": 1e-6}
+
+
+def causal_mask(n):
+    return torch.triu(torch.ones(n, n, dtype=torch.bool), 1)
+
+
+def gen_c2(b=8, h=12, s=1024):
+    g = torch.Generator().manual_seed(0)
+    x = (3 * torch.randn(b, h, s, s, generator=g)).half()
+    return {"x": x.masked_fill(causal_mask(s), float("-inf"))}
+
+
+def gen_c3(rows=16384, cols=4096):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(rows, cols, generator=g).bfloat16()
+    r = torch.randn(rows, cols, generator=g).bfloat16()
+    w = (1 + 0.02 * torch.randn(cols, generator=g)).bfloat16()
+    return {"x": x, "r": r, "w": w, "eps": 1e-5}
+
+
+def gen_c4(n=8192, d=768, vocab=50304, tmax=50257, ignore_frac=0.05):
+    g = torch.Generator().manual_seed(0)
+    h = torch.randn(n, d, generator=g).bfloat16()
+    W = (0.02 * torch.randn(vocab, d, generator=g)).bfloat16()
+    t = torch.randint(0, tmax, (n,), generator=g)
+    t[torch.randperm(n, generator=g)[: int(ignore_frac * n)]] = -100
+    return {"h": h, "W": W, "t": t}
+
+
+def gen_c5(b=4, d=2048, l=4096, n=16):
+    g = torch.Generator().manual_seed(0)
+    u = torch.randn(b, d, l, generator=g).bfloat16()
+    delta = F.softplus(0.5 * torch.randn(b, d, l, generator=g) - 4.6)
+    A = -torch.arange(1, n + 1, dtype=torch.float32).expand(d, n).contiguous()
+    B = torch.randn(b, 1, n, l, generator=g).bfloat16()
+    C = torch.randn(b, 1, n, l, generator=g).bfloat16()
+    D = torch.ones(d)
+    z = torch.randn(b, d, l, generator=g).bfloat16()
+    return {"u": u, "delta": delta, "A": A, "B": B, "C": C, "D": D, "z": z}
+
+
+# Algorithmic work per launch (survey 8(d)).
+C1_BYTES = 2048 * 768 * 4 * 2 + 768 * 4
+C2_BYTES = 2 * 8 * 12 * 1024 * 1024 * 2
+C3_BYTES = 4 * 16384 * 4096 * 2 + 4096 * 2
+C4_FLOP = 2 * 8192 * 50304 * 768
+C4_MIN_BYTES = 8192 * 768 * 2 + 50304 * 768 * 2 + 8192 * 8 + 8192 * 4 + 4
+C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2 + 2048 * 16 * 4 + 2048 * 4
+
+
+# ---------------------------------------------------------------------------
+# GPU side: the product's C-ABI launchers with preallocated outputs
+# ---------------------------------------------------------------------------
+
+def _sets(nbytes):
+    return max(1, min(64, math.ceil(ROTATE_BYTES / max(1, nbytes))))
+
+
+def _replicate(tensors, k):
+    """k device copies of a dict of CPU tensors (first copy shares nothing with the CPU)."""
+    out = []
+    for _ in range(k):
+        out.append({n: (v.cuda() if torch.is_tensor(v) else v) for n, v in tensors.items()})
+    return out
+
+
+class Case:
+    """One configuration: device state, one launch per step, algorithmic work."""
+
+    def __init__(self, name, workload, bound, work, unit_tokens, launch, sets, kernel_name):
+        self.name, self.workload, self.bound, self.work = name, workload, bound, work
+        self.tokens, self.launch, self.sets, self.kernel_name = unit_tokens, launch, sets, kernel_name
+
+
+def make_case(name):
+    from kernels.hip import _lib
+    if name == "c1":
+        cpu = gen_c1()
+        k = _sets(C1_BYTES)
+        sets = _replicate(cpu, k)
+        for s in sets:
+            s["y"] = torch.empty_like(s["x"])
+        launch = lambda s: _lib.rmsnorm(s["x"], s["w"], s["y"], s["eps"])
+        return Case(name, "C1 RMSNorm fp32 [2048, 768]", "hbm", C1_BYTES, 2048, launch, sets,
+                    "rownorm_vec_kernel")
+    if name == "c2":
+        cpu = gen_c2()
+        k = _sets(C2_BYTES)
+        sets = _replicate(cpu, k)
+        for s in sets:
+            s["x2"] = s["x"].view(-1, 1024)
+            s["y"] = torch.empty_like(s["x2"])
+        launch = lambda s: _lib.softmax(s["x2"], s["y"])
+        return Case(name, "C2 causal softmax fp16 [8, 12, 1024, 1024]", "hbm", C2_BYTES, 98304,
+                    launch, sets, "softmax_vec_kernel")
+    if name == "c3":
+        cpu = gen_c3()
+        k = _sets(C3_BYTES)
+        sets = _replicate(cpu, k)
+        for s in sets:
+            s["nr"] = torch.empty_like(s["x"])
+            s["y"] = torch.empty_like(s["x"])
+        launch = lambda s: _lib.fused_add_rmsnorm(s["x"], s["r"], s["w"], s["nr"], s["y"], s["eps"])
+        return Case(name, "C3 fused residual + RMSNorm bf16 [16384, 4096]", "hbm", C3_BYTES, 16384,
+                    launch, sets, "rownorm_vec_kernel")
+    if name == "c4":
+        cpu = gen_c4()
+        sets = _replicate(cpu, 2)
+        wsb = _lib.lmhead_ce_workspace_bytes(8192, 50304)
+        for s in sets:
+            s["loss"] = torch.empty((), dtype=torch.float32, device="cuda")
+            s["lse"] = torch.empty(8192, dtype=torch.float32, device="cuda")
+            s["nv"] = torch.empty(1, dtype=torch.int64, device="cuda")
+            s["ws"] = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        launch = lambda s: _lib.lmhead_ce(s["h"], s["W"], s["t"], s["loss"], s["lse"], None, s["nv"],
+                                          s["ws"], -100)
+        return Case(name, "C4 lm-head + CE bf16 [8192, 768] x [50304, 768]", "mfma", C4_FLOP, 8192,
+                    launch, sets, "lmhead_ce_tile_kernel")
+    if name == "c5":
+        cpu = gen_c5()
+        k = _sets(C5_BYTES)
+        sets = _replicate(cpu, k)
+        for s in sets:
+            s["out"] = torch.empty_like(s["u"])
+        launch = lambda s: _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"],
+                                               s["z"], None, s["out"], None, False)
+        return Case(name, "C5 Mamba-1 selective scan B4 L4096 D2048 N16", "hbm", C5_BYTES, 4 * 4096,
+                    launch, sets, "mamba_scan_fwd_kernel")
+    raise ValueError(name)
+
+
+def time_case(case, steps, warmup):
+    """W untimed steps, then K timed steps (sync on both sides); per-launch HIP events."""
+    nset = len(case.sets)
+    for i in range(warmup):
+        case.launch(case.sets[i % nset])
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        case.launch(case.sets[i % nset])
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dur_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall, dur_ms
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle on a bounded sample, on the host's cores
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(name, budget_s=4.0):
+    """Returns (rate, unit, sample description) for the CPU oracle on a sample of ``name``."""
+    from oracle import ops
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+            if sum(ts) > budget_s:
+                break
+        return statistics.median(ts)
+
+    if name == "c1":
+        c = gen_c1()
+        t = timed(lambda: ops.rmsnorm_ref(c["x"], c["w"], c["eps"]), 5)
+        return C1_BYTES / t / 1e9, "GB/s", "full C1 (2048 x 768 fp32)"
+    if name == "c2":
+        c = gen_c2(b=1, h=2)
+        frac = 2 / 96
+        t = timed(lambda: ops.softmax_ref(c["x"]), 5)
+        return C2_BYTES * frac / t / 1e9, "GB/s", "2 of 96 (batch, head) planes of C2"
+    if name == "c3":
+        c = gen_c3(rows=1024)
+        t = timed(lambda: ops.fused_residual_add_rmsnorm_ref(c["x"], c["r"], c["w"], c["eps"]), 5)
+        return C3_BYTES * (1024 / 16384) / t / 1e9, "GB/s", "1024 of 16384 rows of C3"
+    if name == "c4":
+        c = gen_c4()
+        rows = 64
+        h, t_ = c["h"][:rows], c["t"][:rows]
+        t = timed(lambda: ops.lmhead_ce_ref(h, c["W"], t_), 3)
+        return 2 * rows * 50304 * 768 / t / 1e12, "TFLOP/s", f"{rows} of 8192 rows of C4 (fp32 GEMM per 4096-column vocab chunk)"
+    if name == "c5":
+        c = gen_c5(b=1, d=64)
+        t = timed(lambda: ops.selective_scan_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"],
+                                                 c["z"]), 1)
+        # tokens/s of the full problem = (channel-steps/s) / dim
+        return (64 * 4096) / t / 2048 / 1e6, "Mtok/s", "batch 1, 64 of 2048 channels, full L=4096"
+    raise ValueError(name)
+
+
+# ---------------------------------------------------------------------------
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    names = [n.strip() for n in args.only.split(",") if n.strip()]
+    if "c2" not in names:
+        names.insert(0, "c2")
+    kernels = {}
+    head = None
+    for name in names:
+        case = make_case(name)
+        wall, dur = time_case(case, args.steps, args.warmup)
+        mean_ms = statistics.fmean(dur)
+        med_ms = statistics.median(dur)
+        if case.bound == "hbm":
+            achieved = case.work / (mean_ms * 1e-3) / 1e9
+            peak, unit = HBM_PEAK_GBS, "GB/s"
+        else:
+            achieved = case.work / (mean_ms * 1e-3) / 1e12
+            peak, unit = BF16_PEAK_TFLOPS, "TFLOP/s"
+        rec = {
+            "workload": case.workload,
+            "kernel": case.kernel_name,
+            "us_per_launch_mean": round(mean_ms * 1e3, 2),
+            "us_per_launch_median": round(med_ms * 1e3, 2),
+            "achieved": round(achieved, 1),
+            "unit": unit,
+            "peak": peak,
+            "frac": round(achieved / peak, 4),
+            "tokens_per_s": round(case.tokens / (mean_ms * 1e-3), 1),
+            "input_sets": len(case.sets),
+            "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+        }
+        if name == "c5":
+            rec["Mtok_per_s"] = round(case.tokens / (mean_ms * 1e-3) / 1e6, 2)
+        if not args.no_cpu:
+            rate, cunit, sample = cpu_baseline(name)
+            rec["cpu"] = {"value": round(rate, 4), "unit": cunit, "sample": sample}
+            gpu_same_unit = rec.get("Mtok_per_s") if cunit == "Mtok/s" else achieved
+            rec["gpu_over_cpu"] = round(gpu_same_unit / rate, 1) if rate > 0 else None
+        kernels[name] = rec
+        if name == "c2":
+            head = (case, wall, mean_ms)
+        del case
+        torch.cuda.empty_cache()
+
+    case, wall, mean_ms = head
+    value = C2_BYTES * args.steps / wall / 1e9
+    h = kernels["c2"]
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seed-0 CPU generator, survey draw order)",
+        "config": {"workload": case.workload, "rows": 98304, "cols": 1024, "mask": "causal -inf",
+                   "accumulate": "fp32", "input_sets_rotated": len(case.sets)},
+        "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": h["frac"], "traffic": None},
+        "cpu_baseline": None,
+        "kernels": kernels,
+        "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+                 "cpu": platform.processor() or platform.machine(), "torch": torch.__version__,
+                 "gpu": torch.cuda.get_device_name(0)},
+    }
+    if "cpu" in h:
+        line["cpu_baseline"] = {"value": h["cpu"]["value"], "unit": "GB/s",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": h["cpu"]["sample"]}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,177 @@
+/*
+ * autokernel_mi355x.h -- C ABI of the gfx950 (MI355X / CDNA4) kernel library
+ * libautokernel_gfx950.so.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, element counts and element strides (row
+ *     pitches in ELEMENTS, not bytes) plus an opaque HIP stream (hipStream_t
+ *     passed as void*, NULL = the null stream);
+ *   - enqueues its kernels on that stream and returns without synchronising;
+ *   - never allocates or frees device memory (the caller owns every output
+ *     and workspace buffer);
+ *   - returns AK_OK (0) or a negative AK_ERR_* code; the message for the last
+ *     failure on the calling thread is returned by ak_last_error().
+ *
+ * Float element types are selected by an AK_DTYPE_* code. All reductions are
+ * carried in fp32 whatever the storage type.
+ *
+ * Each declaration names the reference interface (joelhenwang/autokernel-
+ * halo-strix, file:line) whose behaviour it replaces.
+ */
+#ifndef AUTOKERNEL_MI355X_H
+#define AUTOKERNEL_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AK_ABI_VERSION 1
+
+#define AK_DTYPE_F32 0
+#define AK_DTYPE_F16 1
+#define AK_DTYPE_BF16 2
+
+#define AK_OK 0
+#define AK_ERR_INVALID_ARG (-1)
+#define AK_ERR_UNSUPPORTED (-2)
+#define AK_ERR_LAUNCH (-3)
+#define AK_ERR_WORKSPACE (-4)
+
+/* Message describing the last non-zero return on the calling thread. */
+const char* ak_last_error(void);
+
+/* AK_ABI_VERSION of the loaded library. */
+int ak_abi_version(void);
+
+/* Name of the GPU architecture the library was built for ("gfx950"). */
+const char* ak_target_arch(void);
+
+/*
+ * RMSNorm: y[r, :] = (x[r, :] / sqrt(mean(x[r, :]^2) + eps)) * weight.
+ * Replaces kernels/hip/rmsnorm.py:119-143 (rmsnorm_hip) and the PyTorch
+ * fallback of kernels/hip/rmsnorm.py:156-177 (kernel_fn); semantics of
+ * reference.py:25-29 (rmsnorm_ref), computed in fp32 and rounded once.
+ */
+int ak_rmsnorm_fwd(const void* x, const void* weight, void* y,
+                   int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_y,
+                   float eps, int dtype, void* stream);
+
+/*
+ * Fused residual add + RMSNorm:
+ *   h = round_dtype(x + residual)            (written to new_residual if non-NULL)
+ *   y = round_dtype((h / sqrt(mean(h^2) + eps)) * weight)
+ * Replaces kernels/hip/fused_residual_add_rmsnorm.py:135-169
+ * (fused_residual_add_rmsnorm_hip) and :284-319 (..._dual_hip); semantics of
+ * reference.py:71-78 (fused_residual_add_rmsnorm_ref).
+ */
+int ak_fused_add_rmsnorm_fwd(const void* x, const void* residual, const void* weight,
+                             void* new_residual, void* y,
+                             int64_t rows, int64_t cols,
+                             int64_t ld_x, int64_t ld_r, int64_t ld_nr, int64_t ld_y,
+                             float eps, int dtype, void* stream);
+
+/*
+ * Row softmax over the last dimension with fp32 accumulation.
+ * Replaces kernels/hip/softmax.py:273-326 (softmax_hip); semantics of
+ * reference.py:14-17 (softmax_ref). -inf entries give exact zeros.
+ */
+int ak_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t ld_x, int64_t ld_y, int dtype, void* stream);
+
+/*
+ * Cross-entropy forward over materialised logits [rows, vocab].
+ * Replaces kernels/ce_fused.py:333-382 (cross_entropy_fwd_hip).
+ * Writes per-row loss and logsumexp; row_max / row_sum when non-NULL
+ * (tiny mode); grad_logits (same dtype as logits) when non-NULL (fused mode),
+ * pre-multiplied by scale_grad. softcap <= 0 disables the logit softcap,
+ * label_smoothing <= 0 disables smoothing. Rows whose target equals
+ * ignore_index get loss 0 and a zero gradient row; a target outside
+ * [0, vocab) that is not ignore_index yields loss NaN.
+ */
+int ak_ce_fwd(const void* logits, const int64_t* targets,
+              float* losses, float* lse, float* row_max, float* row_sum,
+              void* grad_logits,
+              int64_t rows, int64_t vocab, int64_t ld_logits, int64_t ld_grad,
+              float softcap, int64_t ignore_index, float label_smoothing,
+              float scale_grad, int dtype, void* stream);
+
+/*
+ * Cross-entropy backward from saved row max / row sum (tiny mode).
+ * Replaces kernels/ce_fused.py:490-522 (cross_entropy_bwd_tiny_hip).
+ */
+int ak_ce_bwd_tiny(const void* logits, const int64_t* targets,
+                   const float* row_max, const float* row_sum, void* grad_logits,
+                   int64_t rows, int64_t vocab, int64_t ld_logits, int64_t ld_grad,
+                   float softcap, int64_t ignore_index, float label_smoothing,
+                   float scale_grad, int dtype, void* stream);
+
+/*
+ * Fused lm-head + cross-entropy forward: logits = hidden @ weight^T are
+ * produced tile by tile on the matrix cores and folded into an online
+ * logsumexp; they are never written to memory.
+ *   lse[i]    = logsumexp_j(hidden[i] . weight[j])          (all rows)
+ *   losses[i] = lse[i] - logit[i, target[i]]  or 0 if ignored (nullable)
+ *   loss[0]   = sum(losses) / max(1, #non-ignored rows)
+ *   n_valid[0]= #non-ignored rows (nullable, int64)
+ * Replaces the per-chunk F.linear + cross_entropy_fwd_hip loop of
+ * kernels/hip/chunked_linear_cross_entropy.py:55-148 (forward value and the
+ * logsumexp side output). Only dtype AK_DTYPE_BF16 and AK_DTYPE_F16 are
+ * accepted; d must be a multiple of 64 and the rows of hidden and weight
+ * 16-byte aligned. workspace must hold ak_lmhead_ce_workspace_bytes() bytes.
+ */
+size_t ak_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab);
+int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targets,
+                     float* loss, float* lse, float* losses, int64_t* n_valid,
+                     void* workspace, size_t workspace_bytes,
+                     int64_t n_rows, int64_t vocab, int64_t d,
+                     int64_t ld_h, int64_t ld_w, int64_t ignore_index,
+                     int dtype, void* stream);
+
+/*
+ * Mamba-1 selective scan forward (selective_scan_fn semantics).
+ * Replaces selective_scan_cuda.fwd, external/mamba/csrc/selective_scan/
+ * selective_scan.cpp:227-335, as called by
+ * external/mamba/mamba_ssm/ops/selective_scan_interface.py:23-56; results
+ * follow selective_scan_ref (selective_scan_interface.py:115-181) with fp32
+ * state.
+ *   u, z, out : [batch, dim, seqlen], element type u_dtype, last dim contiguous
+ *   delta     : [batch, dim, seqlen], element type delta_dtype
+ *   A         : [dim, dstate] fp32 (real)
+ *   B, C      : [batch, ngroups, dstate, seqlen], element type bc_dtype
+ *   D, delta_bias : [dim] fp32 or NULL;  z may be NULL
+ *   last_state: [batch, dim, dstate] fp32 or NULL
+ * Strides are in elements. dim must be a multiple of ngroups; dstate <= 16.
+ */
+int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
+                          const void* B, const void* C, const float* D,
+                          const void* z, const float* delta_bias,
+                          void* out, float* last_state,
+                          int64_t batch, int64_t dim, int64_t seqlen,
+                          int64_t dstate, int64_t ngroups,
+                          int64_t u_batch_stride, int64_t u_dim_stride,
+                          int64_t delta_batch_stride, int64_t delta_dim_stride,
+                          int64_t A_dim_stride,
+                          int64_t B_batch_stride, int64_t B_group_stride, int64_t B_state_stride,
+                          int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
+                          int64_t z_batch_stride, int64_t z_dim_stride,
+                          int64_t out_batch_stride, int64_t out_dim_stride,
+                          int delta_softplus,
+                          int u_dtype, int delta_dtype, int bc_dtype, void* stream);
+
+/*
+ * Diagonal linear recurrence over [batch, seqlen, d_inner] fp32 tensors:
+ *   s[t] = dA[t] * s[t-1] + dBx[t];  y[t] = C[t] * s[t] + D * x[t]
+ * Replaces kernels/hip/selective_scan.py:165-201 (selective_scan_hip).
+ */
+int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* C,
+                     const float* D, const float* x, float* y,
+                     int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AUTOKERNEL_MI355X_H */

@@ -1,0 +1,230 @@
+"""CPU oracle: restatements of the reference's arithmetic for the gfx950 kernels.
+
+TEST INFRASTRUCTURE ONLY. Nothing in the product (the package under
+``autokernel-halo-strix_amd/``) imports this module; only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use
+it, as the checker / CPU baseline, never as the thing measured or shipped.
+
+Every function restates one reference function (torch on the CPU, fp32
+unless stated) and cites the reference file:line it follows. Each is pinned
+by tests in ``tests/test_oracle.py`` against closed forms, invariants,
+float64 brute force on tiny inputs and the reference's own known-answer test
+(``scripts/test_griffin_scan_op.py:42-52``).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+# ---------------------------------------------------------------------------
+# Norms
+# ---------------------------------------------------------------------------
+
+
+def rmsnorm_ref(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``reference.py:25-29`` verbatim semantics: arithmetic in ``x``'s dtype."""
+    rms = torch.sqrt(torch.mean(x ** 2, dim=-1, keepdim=True) + eps)
+    return (x / rms) * weight
+
+
+def rmsnorm_f32_ref(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm computed in fp32 and rounded once to ``x.dtype``.
+
+    The fp32 path of ``reference.py:71-78`` applied without the residual; this
+    is what the gfx950 kernel computes for fp16 / bf16 inputs (for fp32 inputs
+    it equals :func:`rmsnorm_ref`).
+    """
+    xf = x.float()
+    rms = torch.sqrt(torch.mean(xf ** 2, dim=-1, keepdim=True) + eps)
+    return ((xf / rms) * weight.float()).to(x.dtype)
+
+
+def fused_residual_add_rmsnorm_ref(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                                   eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``reference.py:71-78`` plus the ``hidden`` output of ``kernel_fn_dual``.
+
+    hidden = x + residual in the input dtype (one rounding of the exact sum);
+    y = ((hidden_f / sqrt(mean(hidden_f^2) + eps)) * weight_f).to(dtype).
+    """
+    hidden = x + residual
+    hf = hidden.float()
+    rms = torch.sqrt(torch.mean(hf ** 2, dim=-1, keepdim=True) + eps)
+    return hidden, ((hf / rms) * weight.float()).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Softmax
+# ---------------------------------------------------------------------------
+
+
+def softmax_ref(x: torch.Tensor) -> torch.Tensor:
+    """``reference.py:14-17`` (``F.softmax(x, -1)``) with fp32 accumulation."""
+    return F.softmax(x.float(), dim=-1).to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy over materialised logits (kernels/ce_fused.py)
+# ---------------------------------------------------------------------------
+
+
+def _capped(logits: torch.Tensor, softcap: float) -> torch.Tensor:
+    x = logits.float()
+    if softcap > 0:
+        x = softcap * torch.tanh(x / softcap)
+    return x
+
+
+def ce_rows_ref(logits: torch.Tensor, targets: torch.Tensor, softcap: float = 0.0,
+                ignore_index: int = -100, label_smoothing: float = 0.0):
+    """Per-row ``(losses, lse, row_max, row_sum)`` of ``kernels/ce_fused.py:144-262``.
+
+    lse = max + log(sum(exp(x - max))) over the (softcapped) row; loss =
+    lse - x[t], or lse - (1-a) x[t] - a mean(x) with label smoothing a;
+    ignored rows: loss 0, lse still reported.
+    """
+    x = _capped(logits, softcap)
+    row_max = x.max(dim=-1).values
+    row_sum = torch.exp(x - row_max[:, None]).sum(-1)
+    lse = row_max + torch.log(row_sum)
+    t = targets.long()
+    ignored = t == ignore_index
+    tc = torch.where(ignored, torch.zeros_like(t), t)
+    xt = x.gather(1, tc[:, None]).squeeze(1)
+    if label_smoothing > 0:
+        loss = lse - (1 - label_smoothing) * xt - label_smoothing * x.mean(-1)
+    else:
+        loss = lse - xt
+    loss = torch.where(ignored, torch.zeros_like(loss), loss)
+    return loss, lse, row_max, row_sum
+
+
+def ce_grad_ref(logits: torch.Tensor, targets: torch.Tensor, softcap: float = 0.0,
+                ignore_index: int = -100, label_smoothing: float = 0.0,
+                scale: float = 1.0) -> torch.Tensor:
+    """Gradient rows of ``kernels/ce_fused.py:268-328`` (fp32).
+
+    g = softmax(x) - [i == t](1 - a) - a / V, times (1 - tanh^2) under the
+    softcap, times ``scale``; ignored rows are zero.
+    """
+    x = _capped(logits, softcap)
+    V = x.shape[-1]
+    p = torch.softmax(x, dim=-1)
+    t = targets.long()
+    ignored = t == ignore_index
+    tc = torch.where(ignored, torch.zeros_like(t), t)
+    onehot = F.one_hot(tc, V).float()
+    g = p - onehot * (1 - label_smoothing)
+    if label_smoothing > 0:
+        g = g - label_smoothing / V
+    if softcap > 0:
+        th = x / softcap
+        g = g * (1 - th * th)
+    g = g * scale
+    return torch.where(ignored[:, None], torch.zeros_like(g), g)
+
+
+def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int = -100) -> torch.Tensor:
+    """Mean over non-ignored rows, denominator clamped to 1 (``ce_fused.py:594-622``)."""
+    valid = (targets != ignore_index).float()
+    return (losses * valid).sum() / valid.sum().clamp(min=1.0)
+
+
+def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                  ignore_index: int = -100, vocab_chunk: int = 4096):
+    """Linear + CE without materialising all logits (fp32 arithmetic).
+
+    Follows ``kernels/hip/chunked_linear_cross_entropy.py:72-75`` (n_valid),
+    ``:135-140`` (loss = sum / n_valid) and ``kernels/ce_fused.py:236-260``
+    (per-row loss), streaming the vocabulary in ``vocab_chunk`` columns with an
+    online (max, sum) merge. Returns ``(loss, lse, losses)``.
+    """
+    h = hidden.float()
+    V = weight.shape[0]
+    n = h.shape[0]
+    m = torch.full((n,), -math.inf)
+    s = torch.zeros(n)
+    t = targets.long()
+    xt = torch.zeros(n)
+    for v0 in range(0, V, vocab_chunk):
+        v1 = min(V, v0 + vocab_chunk)
+        logits = h @ weight[v0:v1].float().t()
+        cm = logits.max(dim=-1).values
+        nm = torch.maximum(m, cm)
+        s = s * torch.exp(m - nm) + torch.exp(logits - nm[:, None]).sum(-1)
+        m = nm
+        inside = (t >= v0) & (t < v1)
+        if inside.any():
+            idx = inside.nonzero().squeeze(1)
+            xt[idx] = logits[idx, t[idx] - v0]
+    lse = m + torch.log(s)
+    ignored = t == ignore_index
+    losses = torch.where(ignored, torch.zeros_like(lse), lse - xt)
+    return ce_mean_ref(losses, t, ignore_index), lse, losses
+
+
+# ---------------------------------------------------------------------------
+# Scans
+# ---------------------------------------------------------------------------
+
+
+def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                       return_last_state=False, initial_state: Optional[torch.Tensor] = None,
+                       silu_fp32: bool = True):
+    """``external/mamba/mamba_ssm/ops/selective_scan_interface.py:115-181`` (real A).
+
+    fp32 state; B / C given as [b, n, l] or [b, g, n, l] (groups repeated over
+    dim). ``silu_fp32=True`` evaluates silu(z) in fp32 (the gfx950 kernel's
+    choice); ``False`` evaluates it in z's dtype as the reference does (:179).
+    ``initial_state`` [b, d, n] (fp32) starts the recurrence from a given
+    state; the reference starts from zeros.
+    """
+    dtype_in = u.dtype
+    u = u.float()
+    delta = delta.float()
+    if delta_bias is not None:
+        delta = delta + delta_bias[..., None].float()
+    if delta_softplus:
+        delta = F.softplus(delta)
+    batch, dim, dstate = u.shape[0], A.shape[0], A.shape[1]
+    Bf, Cf = B.float(), C.float()
+    if Bf.dim() == 3:
+        Bf = Bf.unsqueeze(1)
+    if Cf.dim() == 3:
+        Cf = Cf.unsqueeze(1)
+    Bf = Bf.repeat_interleave(dim // Bf.shape[1], dim=1)  # [b, d, n, l]
+    Cf = Cf.repeat_interleave(dim // Cf.shape[1], dim=1)
+    x = torch.zeros(batch, dim, dstate) if initial_state is None else initial_state.float().clone()
+    deltaA = torch.exp(delta[:, :, :, None] * A.float()[None, :, None, :])        # [b, d, l, n]
+    deltaB_u = (delta * u)[:, :, :, None] * Bf.permute(0, 1, 3, 2)                 # [b, d, l, n]
+    Cl = Cf.permute(0, 1, 3, 2)                                                   # [b, d, l, n]
+    ys = []
+    for i in range(u.shape[2]):
+        x = deltaA[:, :, i] * x + deltaB_u[:, :, i]
+        ys.append((x * Cl[:, :, i]).sum(-1))
+    y = torch.stack(ys, dim=2)
+    out = y if D is None else y + u * D.float()[:, None]
+    if z is not None:
+        gate = F.silu(z.float()) if silu_fp32 else F.silu(z).float()
+        out = out * gate
+    out = out.to(dtype_in)
+    return (out, x) if return_last_state else out
+
+
+def diag_scan_ref(dA, dBx, C, D, x):
+    """Diagonal recurrence of ``kernels/hip/selective_scan.py:1-20, :214-241``.
+
+    state[t] = dA[t] * state[t-1] + dBx[t];  y[t] = C[t] * state[t] + D * x[t]
+    over fp32 [batch, seq, d_inner].
+    """
+    dA, dBx, C, x = (t.float() for t in (dA, dBx, C, x))
+    batch, seqlen, d = dA.shape
+    s = torch.zeros(batch, d)
+    ys = []
+    for t in range(seqlen):
+        s = dA[:, t] * s + dBx[:, t]
+        ys.append(C[:, t] * s + D.float() * x[:, t])
+    return torch.stack(ys, dim=1)

@@ -1,0 +1,111 @@
+"""CPU stand-in for the gfx950 launchers, built on the oracle (tests only).
+
+``install(monkeypatch)`` replaces the tensor-level launchers in
+``kernels.hip._lib`` with functions that compute the same outputs on the CPU
+from ``oracle.ops`` and write them into the caller's output tensors, and
+relaxes the GPU-device check. This lets the host logic (shape handling,
+autograd wiring, the module registry) run in the CPU test tier. The product
+never imports this module.
+"""
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from oracle import ops
+
+
+def _rmsnorm(x, w, y, eps):
+    y.copy_(ops.rmsnorm_f32_ref(x, w, eps))
+
+
+def _fused(x, r, w, nr, y, eps):
+    hidden, out = ops.fused_residual_add_rmsnorm_ref(x, r, w, eps)
+    if nr is not None:
+        nr.copy_(hidden)
+    y.copy_(out)
+
+
+def _softmax(x, y):
+    y.copy_(ops.softmax_ref(x))
+
+
+def _bad_targets(targets, vocab, ignore_index):
+    t = targets.long()
+    return (t != ignore_index) & ((t < 0) | (t >= vocab))
+
+
+def _ce_fwd(logits, targets, losses, lse, row_max, row_sum, grad, softcap, ignore_index, ls, scale):
+    bad = _bad_targets(targets, logits.shape[1], ignore_index)
+    t = torch.where(bad, torch.full_like(targets, ignore_index), targets)
+    l, s, m, sm = ops.ce_rows_ref(logits, t, softcap, ignore_index, ls)
+    l = torch.where(bad, torch.full_like(l, math.nan), l)
+    losses.copy_(l)
+    lse.copy_(s)
+    if row_max is not None:
+        row_max.copy_(m)
+    if row_sum is not None:
+        row_sum.copy_(sm)
+    if grad is not None:
+        g = ops.ce_grad_ref(logits, t, softcap, ignore_index, ls, scale)
+        g[bad] = math.nan
+        grad.copy_(g)
+
+
+def _ce_bwd_tiny(logits, targets, row_max, row_sum, grad, softcap, ignore_index, ls, scale):
+    x = logits.float()
+    if softcap > 0:
+        x = softcap * torch.tanh(x / softcap)
+    V = x.shape[1]
+    p = torch.exp(x - row_max.float()[:, None]) / row_sum.float()[:, None]
+    t = targets.long()
+    ignored = t == ignore_index
+    tc = torch.where(ignored, torch.zeros_like(t), t)
+    g = p - F.one_hot(tc, V).float() * (1 - ls)
+    if ls > 0:
+        g = g - ls / V
+    if softcap > 0:
+        th = x / softcap
+        g = g * (1 - th * th)
+    g = torch.where(ignored[:, None], torch.zeros_like(g), g * scale)
+    grad.copy_(g)
+
+
+def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index):
+    lo, ls_, per = ops.lmhead_ce_ref(hidden, weight, targets, ignore_index)
+    bad = _bad_targets(targets, weight.shape[0], ignore_index)
+    per = torch.where(bad, torch.full_like(per, math.nan), per)
+    lo = ops.ce_mean_ref(per, targets, ignore_index)
+    loss.copy_(lo)
+    lse.copy_(ls_)
+    if losses is not None:
+        losses.copy_(per)
+    if n_valid is not None:
+        n_valid.copy_((targets != ignore_index).sum().reshape(1))
+
+
+def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus):
+    o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
+                                     return_last_state=True)
+    out.copy_(o)
+    if last_state is not None:
+        last_state.copy_(last)
+
+
+def _diag(dA, dBx, C, D, x, y):
+    y.copy_(ops.diag_scan_ref(dA, dBx, C, D, x))
+
+
+def install(monkeypatch):
+    from kernels.hip import _lib
+    monkeypatch.setattr(_lib, "require_device", lambda *tensors: None)
+    monkeypatch.setattr(_lib, "rmsnorm", _rmsnorm)
+    monkeypatch.setattr(_lib, "fused_add_rmsnorm", _fused)
+    monkeypatch.setattr(_lib, "softmax", _softmax)
+    monkeypatch.setattr(_lib, "ce_fwd", _ce_fwd)
+    monkeypatch.setattr(_lib, "ce_bwd_tiny", _ce_bwd_tiny)
+    monkeypatch.setattr(_lib, "lmhead_ce", _lmhead)
+    monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
+    monkeypatch.setattr(_lib, "selective_scan", _scan)
+    monkeypatch.setattr(_lib, "diag_scan", _diag)

@@ -1,0 +1,269 @@
+"""Host logic of the drop-in API on the CPU fake backend (CPU tier).
+
+The fake routes every launcher to the oracle, so these tests check what the
+Python layer does around the kernels: shapes, dtypes, argument handling,
+the ce_fused / chunked CE autograd contracts, the torch.library ops and the
+module-swap registry -- the same surfaces the reference's own scripts
+exercise (test_ce_features.py, test_chunked_ce.py, test_tier2_parity.py,
+test_autokernel_autograd_safety.py).
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import ops
+
+
+def test_no_cpu_fallback_without_gpu():
+    from kernels.hip import rmsnorm, softmax
+    x = torch.randn(4, 8)
+    with pytest.raises(RuntimeError, match="GPU"):
+        rmsnorm.kernel_fn(x, torch.ones(8))
+    with pytest.raises(RuntimeError, match="GPU"):
+        softmax.kernel_fn(x)
+
+
+def test_kernel_fns_shapes_and_dtypes(fake_backend):
+    from kernels.hip import fused_residual_add_rmsnorm as frn
+    from kernels.hip import rmsnorm, softmax
+    x = torch.randn(2, 3, 64).bfloat16()
+    r = torch.randn(2, 3, 64).bfloat16()
+    w = torch.ones(64)
+    y = rmsnorm.kernel_fn(x, w)
+    assert y.shape == x.shape and y.dtype == x.dtype
+    assert torch.equal(y, ops.rmsnorm_f32_ref(x, w.bfloat16()))
+    h, n = frn.kernel_fn_dual(x, r, w, eps=1e-5)
+    hr, nr_ = ops.fused_residual_add_rmsnorm_ref(x, r, w.bfloat16(), 1e-5)
+    assert torch.equal(h, hr) and torch.equal(n, nr_)
+    assert torch.equal(frn.kernel_fn(x, r, w, eps=1e-5), nr_)
+    s = softmax.kernel_fn(x)
+    assert s.shape == x.shape and s.dtype == x.dtype
+    with pytest.raises(TypeError):
+        rmsnorm.kernel_fn(x.double(), w.double())
+    with pytest.raises(ValueError):
+        rmsnorm.kernel_fn(x, torch.ones(63))
+    with pytest.raises(ValueError):
+        frn.kernel_fn(x, r[:, :2], w)
+
+
+def test_ce_fused_module_api(fake_backend):
+    import kernel
+    from kernels import ce_fused
+    assert kernel.KERNEL_TYPE == "cross_entropy" and kernel.BACKEND == "hip"
+    assert kernel.kernel_fn is ce_fused.kernel_fn
+    assert set(ce_fused.TOLERANCES) == {"float16", "bfloat16", "float32"}
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(16, 40, generator=g).half()
+    t = torch.randint(0, 40, (16,), generator=g)
+    t[2] = -100
+    out = ce_fused._get_fwd_module().cross_entropy_fwd_hip(logits, t, 0.0, -100, 0.0, 1, 1, 0.5)
+    assert len(out) == 5 and all(o is not None for o in out)
+    out = ce_fused._get_fwd_module().cross_entropy_fwd_hip(logits, t, 0.0, -100, 0.0, 0, 0, 1.0)
+    assert out[2] is None and out[3] is None and out[4] is None
+    loss = ce_fused.kernel_fn(logits, t)
+    assert torch.allclose(loss, F.cross_entropy(logits.float(), t), rtol=1e-5)
+
+
+@pytest.mark.parametrize("mode", ["fused", "tiny"])
+@pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (8.0, 0.1, 0.0), (0.0, 0.0, 1e-2)])
+def test_ce_full_autograd(fake_backend, mode, softcap, ls, zw):
+    from kernels.ce_fused import ce_full
+    g = torch.Generator().manual_seed(1)
+    base = 3 * torch.randn(12, 30, generator=g)
+    t = torch.randint(0, 30, (12,), generator=g)
+    t[[0, 4]] = -100
+    x = base.clone().requires_grad_()
+    loss, lse = ce_full(x, t, softcap=softcap, label_smoothing=ls, mode=mode, return_z=True,
+                        z_loss_weight=zw)
+    (2.0 * loss).backward()
+    xr = base.double().requires_grad_()
+    xc = softcap * torch.tanh(xr / softcap) if softcap > 0 else xr
+    ref = F.cross_entropy(xc, t, ignore_index=-100, label_smoothing=ls)
+    if zw > 0:
+        valid = (t != -100).double()
+        lse_r = torch.logsumexp(xc, -1)
+        ref = ref + zw * ((lse_r * valid) ** 2).sum() / valid.sum()
+    (2.0 * ref).backward()
+    assert torch.allclose(loss.double(), ref.detach(), rtol=1e-5)
+    assert torch.allclose(x.grad.double(), xr.grad, atol=1e-6, rtol=1e-4)
+    assert torch.allclose(lse.double(), torch.logsumexp(xc.detach(), -1), rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("softcap,zw", [(0.0, 0.0), (0.0, 1e-3), (10.0, 0.0)])
+def test_chunked_linear_ce(fake_backend, dtype, softcap, zw):
+    from kernels.hip.chunked_linear_cross_entropy import ChunkedLinearCrossEntropyLoss
+    g = torch.Generator().manual_seed(2)
+    h0 = torch.randn(2, 20, 64, generator=g)
+    W0 = 0.05 * torch.randn(300, 64, generator=g)
+    t = torch.randint(0, 300, (2, 20), generator=g)
+    t[0, :3] = -100
+    h = h0.to(dtype).clone().requires_grad_()
+    W = W0.to(dtype).clone().requires_grad_()
+    loss = ChunkedLinearCrossEntropyLoss(chunk_size=16, softcap=softcap, z_loss_weight=zw)(h, W, t)
+    loss.backward()
+    hr = h0.to(dtype).double().detach().requires_grad_()
+    Wr = W0.to(dtype).double().detach().requires_grad_()
+    logits = hr.reshape(-1, 64) @ Wr.t()
+    if softcap > 0:
+        logits = softcap * torch.tanh(logits / softcap)
+    ref = F.cross_entropy(logits, t.reshape(-1))
+    ref.backward()
+    if zw > 0:  # z-loss enters the value only (as in the reference module)
+        valid = (t.reshape(-1) != -100).double()
+        ref = ref + zw * ((torch.logsumexp(logits.detach(), -1) * valid) ** 2).sum() / valid.sum()
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    assert torch.allclose(loss.double(), ref.detach(), rtol=tol)
+    assert torch.allclose(h.grad.double(), hr.grad, atol=tol, rtol=tol)
+    assert torch.allclose(W.grad.double(), Wr.grad, atol=tol, rtol=tol)
+
+
+def test_torch_ops_registered_with_fake_and_autograd(fake_backend):
+    import kernels.hip._torch_ops  # noqa: F401
+    x = torch.randn(6, 32, requires_grad=True)
+    w = (1 + 0.1 * torch.randn(32)).requires_grad_()
+    y = torch.ops.autokernel.rmsnorm(x, w)
+    y.sum().backward()
+    xr = x.detach().double().requires_grad_()
+    wr = w.detach().double().requires_grad_()
+    (xr / torch.sqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6) * wr).sum().backward()
+    assert torch.allclose(x.grad.double(), xr.grad, atol=1e-5)
+    assert torch.allclose(w.grad.double(), wr.grad, atol=1e-5)
+    r = torch.randn(6, 32, requires_grad=True)
+    x.grad = None
+    h, n = torch.ops.autokernel.fused_res_rmsnorm(x, r, w, 1e-5)
+    (h.sum() + (n * n).sum()).backward()
+    assert x.grad is not None and torch.equal(x.grad, r.grad)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        fx = torch.empty(3, 16)
+        out = torch.ops.autokernel.fused_res_rmsnorm(fx, fx, torch.empty(16))
+        assert out[0].shape == (3, 16)
+    dA = torch.rand(2, 7, 3, requires_grad=True)
+    dBx = torch.randn(2, 7, 3, requires_grad=True)
+    C = torch.randn(2, 7, 3, requires_grad=True)
+    D = torch.randn(3, requires_grad=True)
+    xx = torch.randn(2, 7, 3, requires_grad=True)
+    torch.ops.autokernel.selective_scan(dA, dBx, C, D, xx).pow(2).sum().backward()
+    ins = [t.detach().double().requires_grad_() for t in (dA, dBx, C, D, xx)]
+    ops.diag_scan_ref(*ins).double().pow(2).sum().backward()
+    ref = [t for t in (dA, dBx, C, D, xx)]
+    # the oracle computes in fp32; compare against its autograd
+    ins32 = [t.detach().float().requires_grad_() for t in ref]
+    ops.diag_scan_ref(*ins32).pow(2).sum().backward()
+    for a, b in zip(ref, ins32):
+        assert torch.allclose(a.grad, b.grad, rtol=1e-4, atol=1e-4)
+
+
+def test_selective_scan_fn_api(fake_backend):
+    from kernels.hip.selective_scan import selective_scan_fn
+    g = torch.Generator().manual_seed(3)
+    u = torch.randn(2, 4, 20, generator=g)
+    delta = 0.5 * torch.rand(2, 4, 20, generator=g)
+    A = -torch.rand(4, 8, generator=g)
+    B = torch.randn(2, 8, 20, generator=g)
+    C = torch.randn(2, 8, 20, generator=g)
+    out, last = selective_scan_fn(u, delta, A, B, C, torch.ones(4), return_last_state=True)
+    ref, rl = ops.selective_scan_ref(u, delta, A, B, C, torch.ones(4), return_last_state=True)
+    assert torch.allclose(out, ref) and torch.allclose(last, rl)
+    with pytest.raises(NotImplementedError):
+        selective_scan_fn(u, delta, A, torch.randn(4, 8), C)
+    uu = u.clone().requires_grad_()
+    with pytest.raises(NotImplementedError):
+        selective_scan_fn(uu, delta, A, B, C).sum().backward()
+
+
+# ---------------------------------------------------------------------------
+# Registry
+# ---------------------------------------------------------------------------
+
+class RMSNorm(nn.Module):
+    def __init__(self, d, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(d))
+        self.eps = eps
+
+    def forward(self, x):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight
+
+
+class Attn(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.proj = nn.Linear(d, d, bias=False)
+
+    def forward(self, x, freqs_cis):
+        return self.proj(x)
+
+
+class Block(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.attention = Attn(d)
+        self.attention_norm = RMSNorm(d)
+        self.feed_forward = nn.Sequential(nn.Linear(d, 2 * d), nn.SiLU(), nn.Linear(2 * d, d))
+        self.ffn_norm = RMSNorm(d)
+
+    def forward(self, x, freqs_cis):
+        h = x + self.attention(self.attention_norm(x), freqs_cis)
+        return h + self.feed_forward(self.ffn_norm(h))
+
+
+class Tiny(nn.Module):
+    def __init__(self, d=32, n=2):
+        super().__init__()
+        self.layers = nn.ModuleList([Block(d) for _ in range(n)])
+        self.norm = RMSNorm(d)
+
+    def forward(self, x):
+        for b in self.layers:
+            x = b(x, None)
+        return self.norm(x)
+
+
+def test_registry_patterns_and_priorities():
+    import autokernel
+    from autokernel._patterns import ALL_PATTERNS
+    assert autokernel.list_patterns() == ["fused_residual_rmsnorm", "fused_griffin_block", "fused_qkv",
+                                          "rmsnorm", "fused_silu_gate_mul", "silu_gate_mul",
+                                          "rotary_embedding"]
+    prio = {p.name: p.priority for p in ALL_PATTERNS}
+    assert prio == {"fused_residual_rmsnorm": 100, "fused_griffin_block": 95, "fused_qkv": 90,
+                    "rmsnorm": 50, "fused_silu_gate_mul": 45, "silu_gate_mul": 40,
+                    "rotary_embedding": 30}
+
+
+def test_optimize_report_restore(fake_backend):
+    import autokernel
+    torch.manual_seed(0)
+    model = Tiny()
+    x = torch.randn(2, 5, 32)
+    ref = model(x)
+    orig_keys = set(model.state_dict())
+    model = autokernel.optimize(model, training=True)
+    rep = autokernel.report(model)
+    assert rep["status"] == "optimized"
+    assert rep["patterns"]["fused_residual_rmsnorm"]["modules_replaced"] == 2
+    assert rep["patterns"]["rmsnorm"]["modules_replaced"] >= 1
+    keys = set(model.state_dict())
+    assert "layers.0.ffn_norm_weight" in keys and "layers.0.ffn_norm.weight" not in keys
+    out = model(x)
+    assert torch.allclose(out, ref, atol=1e-5)
+    out.pow(2).mean().backward()
+    for name, p in model.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
+    autokernel.restore(model)
+    assert set(model.state_dict()) == orig_keys
+    assert autokernel.report(model)["status"] == "not optimized"
+
+
+def test_optimize_include_exclude(fake_backend):
+    import autokernel
+    m = autokernel.optimize(Tiny(), training=True, include=["rmsnorm"])
+    assert list(autokernel.report(m)["patterns"]) == ["rmsnorm"]
+    m = autokernel.optimize(Tiny(), training=True, exclude=["rmsnorm", "fused_residual_rmsnorm"])
+    assert autokernel.report(m)["patterns"] == {}

@@ -1,0 +1,73 @@
+"""The C-ABI library loads and exports every entry point the header declares (CPU tier).
+
+No compute entry point is called here (no GPU in this tier); only argument
+validation paths that return before any HIP call.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from kernels.hip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "autokernel_mi355x.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+(ak_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.is_available():
+        pytest.skip("libautokernel_gfx950.so not built")
+    return _lib.load()
+
+
+def test_header_declares_the_loader_signatures():
+    assert _declared() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_arch(lib):
+    assert lib.ak_abi_version() == 1
+    assert lib.ak_target_arch() == b"gfx950"
+
+
+def test_workspace_query(lib):
+    ws = _lib.lmhead_ce_workspace_bytes(8192, 50304)
+    n_vt = (50304 + 255) // 256
+    assert ws >= n_vt * 8192 * 8 + 2 * 8192 * 4
+    assert ws % 256 == 0
+    assert _lib.lmhead_ce_workspace_bytes(0, 10) == 0
+
+
+def test_argument_errors_return_codes(lib):
+    # unsupported dtype code, rejected before any HIP call
+    rc = lib.ak_rmsnorm_fwd(None, None, None, 4, 8, 8, 8, 1e-6, 7, None)
+    assert rc == -2 and b"dtype" in lib.ak_last_error()
+    rc = lib.ak_softmax_fwd(None, None, 4, 8, 4, 8, 0, None)   # pitch < cols
+    assert rc == -1 and b"pitch" in lib.ak_last_error()
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 100, 100, 100, -100, 2, None)
+    assert rc == -2 and b"multiple" in lib.ak_last_error()
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0, None)
+    assert rc == -2  # fp32 is not a matrix-core input type here
+    rc = _lib.load().ak_selective_scan_fwd(*([None] * 10), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
+    assert rc == -2 and b"dstate" in lib.ak_last_error()
+    # zero-size work is a no-op success
+    assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setenv("AUTOKERNEL_GFX950_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.HipExtensionMissing):
+        _lib.load()

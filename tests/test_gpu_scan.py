@@ -1,0 +1,139 @@
+"""GPU parity: Mamba-1 selective scan and the diagonal recurrence.
+
+Bars: the reference's selective-scan test grid and tolerances
+(external/mamba/tests/ops/test_selective_scan.py:15-51, :43-45; fixture
+tests/golden/mamba_scan_grid.json) against the C oracle on the same rounded
+inputs; C5 at full size within rtol 1e-2 of the fp32 oracle (north star);
+the reference's known-answer test for the diagonal scan.
+"""
+
+import json
+import os
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from gpu_util import gpu, need_gpu, say
+from oracle import c_oracle, ops
+
+pytestmark = gpu
+DEV = "cuda"
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+GRID = json.load(open(os.path.join(GOLDEN, "mamba_scan_grid.json")))
+ITYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+
+
+def _inputs(batch, dim, dstate, seqlen, groups, itype, seed):
+    g = torch.Generator().manual_seed(seed)
+    A = -0.5 * torch.rand(dim, dstate, generator=g)
+    Bs = (batch, groups, dstate, seqlen)
+    B = torch.randn(*Bs, generator=g).to(itype)
+    C = torch.randn(*Bs, generator=g).to(itype)
+    D = torch.randn(dim, generator=g)
+    z = torch.randn(batch, dim, seqlen, generator=g).to(itype)
+    bias = 0.5 * torch.rand(dim, generator=g)
+    u = torch.randn(batch, dim, seqlen, generator=g).to(itype)
+    delta = (0.5 * torch.rand(batch, dim, seqlen, generator=g)).to(itype)
+    return u, delta, A, B, C, D, z, bias
+
+
+def _gpu(u, delta, A, B, C, D, z, bias, softplus, last=True):
+    from kernels.hip.selective_scan import selective_scan_fn
+    d = lambda t: None if t is None else t.to(DEV)
+    r = selective_scan_fn(d(u), d(delta), d(A), d(B), d(C), d(D), d(z), d(bias), softplus, last)
+    return (r[0].cpu(), r[1].cpu()) if last else r.cpu()
+
+
+@pytest.mark.parametrize("itype", ["float32", "float16", "bfloat16"])
+@pytest.mark.parametrize("groups", GRID["varBC_groups"])
+@pytest.mark.parametrize("seqlen", GRID["seqlen"])
+def test_reference_grid(itype, groups, seqlen):
+    need_gpu()
+    dt = ITYPES[itype]
+    rtol, atol = GRID["tolerances"][itype]
+    args = _inputs(GRID["batch"], GRID["dim"], GRID["dstate"], seqlen, groups, dt, seqlen + groups)
+    say("mamba grid", itype, groups, seqlen)
+    out, last = _gpu(*args, softplus=True)
+    ref, rlast = c_oracle.selective_scan(*args, delta_softplus=True)
+    assert out.dtype == dt
+    assert torch.allclose(out.float(), ref, rtol=rtol, atol=atol)
+    assert torch.allclose(last, rlast, rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("batch,dim,dstate,seqlen,groups", [
+    (1, 1, 1, 1, 1), (3, 3, 5, 63, 1), (2, 20, 16, 64, 1), (2, 40, 16, 100, 2), (1, 16, 7, 129, 1),
+    (2, 64, 16, 1000, 4), (1, 33, 16, 257, 1)])
+def test_shapes_and_options(batch, dim, dstate, seqlen, groups):
+    need_gpu()
+    u, delta, A, B, C, D, z, bias = _inputs(batch, dim, dstate, seqlen, groups, torch.bfloat16, dim * seqlen)
+    say("mamba shapes", batch, dim, dstate, seqlen, groups)
+    for softplus, zz, DD, bb in ((True, z, D, bias), (False, None, None, None)):
+        out, last = _gpu(u, delta, A, B, C, DD, zz, bb, softplus)
+        ref, rlast = c_oracle.selective_scan(u, delta, A, B, C, DD, zz, bb, softplus)
+        assert torch.allclose(out.float(), ref, rtol=3e-2, atol=5e-2)
+        assert torch.allclose(last, rlast, rtol=1e-4, atol=1e-4)
+    # 3-D B / C and fp32 delta with bf16 u
+    if groups == 1:
+        out = _gpu(u, delta.float(), A, B[:, 0], C[:, 0], D, z, bias, True, last=False)
+        ref, _ = c_oracle.selective_scan(u, delta.float(), A, B, C, D, z, bias, True)
+        assert torch.allclose(out.float(), ref, rtol=3e-2, atol=5e-2)
+
+
+def test_c5_full_size():
+    need_gpu()
+    import bench
+    c = bench.gen_c5()
+    say("C5 Mamba-1 scan B4 L4096 D2048 N16")
+    out = _gpu(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"], None, False, last=False)
+    ref, _ = c_oracle.selective_scan(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"])
+    assert out.dtype == torch.bfloat16
+    assert torch.allclose(out.float(), ref, rtol=1e-2, atol=1e-4)
+    # the torch oracle (silu in fp32) agrees on a channel slice
+    sl = slice(0, 8)
+    tref = ops.selective_scan_ref(c["u"][:1, sl], c["delta"][:1, sl], c["A"][sl], c["B"][:1], c["C"][:1],
+                                  c["D"][sl], c["z"][:1, sl])
+    assert torch.allclose(out[:1, sl].float(), tref.float(), rtol=1e-2, atol=1e-4)
+
+
+def test_split_equivalence_on_gpu():
+    """scan(L) == scan(L/2) continued from its last_state (closed-form invariant)."""
+    need_gpu()
+    u, delta, A, B, C, D, z, bias = _inputs(2, 32, 16, 512, 1, torch.float32, 77)
+    say("mamba split equivalence")
+    out, last = _gpu(u, delta, A, B, C, D, z, bias, True)
+    a, s1 = _gpu(u[..., :256], delta[..., :256], A, B[..., :256], C[..., :256], D, z[..., :256], bias, True)
+    ref2, s2 = c_oracle.selective_scan(u[..., 256:], delta[..., 256:], A, B[..., 256:], C[..., 256:], D,
+                                       z[..., 256:], bias, True, initial_state=s1)
+    assert torch.allclose(out[..., :256], a, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(out[..., 256:], ref2, rtol=1e-3, atol=1e-3)
+    assert torch.allclose(last, s2, rtol=1e-3, atol=1e-4)
+
+
+def test_deterministic():
+    need_gpu()
+    u, delta, A, B, C, D, z, bias = _inputs(2, 64, 16, 1024, 1, torch.bfloat16, 5)
+    say("mamba determinism")
+    outs = [_gpu(u, delta, A, B, C, D, z, bias, True)[0] for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_diag_scan_known_answer_and_random():
+    need_gpu()
+    from kernels.hip.selective_scan import kernel_fn
+    k = json.load(open(os.path.join(GOLDEN, "griffin_kat.json")))
+    dA = torch.tensor(k["decay"]).view(1, 4, 1).to(DEV)
+    dBx = torch.tensor(k["value"]).view(1, 4, 1).to(DEV)
+    say("diag scan KAT")
+    y = kernel_fn(dA, dBx, torch.ones_like(dA), torch.zeros(1, device=DEV), torch.zeros_like(dA))
+    assert torch.allclose(y.view(-1).cpu(), torch.tensor(k["expected"]), rtol=1e-6)
+    g = torch.Generator().manual_seed(9)
+    shp = (8, 512, 384)
+    dA = torch.sigmoid(torch.randn(*shp, generator=g))
+    dBx = 0.1 * torch.randn(*shp, generator=g)
+    C = torch.randn(*shp, generator=g)
+    D = torch.randn(384, generator=g)
+    x = torch.randn(*shp, generator=g)
+    say("diag scan random", shp)
+    y = kernel_fn(dA.to(DEV), dBx.to(DEV), C.to(DEV), D.to(DEV), x.to(DEV)).cpu()
+    assert torch.allclose(y, ops.diag_scan_ref(dA, dBx, C, D, x), rtol=1e-5, atol=1e-5)

@@ -1,0 +1,285 @@
+"""Pins the CPU oracle (CPU tier).
+
+Each oracle function is checked against something it does not itself
+compute: closed forms, invariants, torch's own independent implementations
+(F.cross_entropy and its autograd, torch.logsumexp), float64 brute force on
+tiny inputs, an independent bf16 round-to-nearest-even, and the reference's
+known-answer test (tests/golden/griffin_kat.json). The checks are chosen so
+that a dropped term, a wrong sign or index, or a transposed operand fails.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import c_oracle, ops
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _bf16_rne(x32: torch.Tensor) -> torch.Tensor:
+    """fp32 -> bf16 round-to-nearest-even by integer arithmetic (finite inputs)."""
+    b = x32.contiguous().numpy().view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint32) << 16
+    return torch.from_numpy(r.view(np.float32).copy()).bfloat16()
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_known_answer():
+    x = torch.tensor([[3.0, 4.0]])
+    r = math.sqrt(12.5)
+    y = ops.rmsnorm_ref(x, torch.tensor([1.0, 1.0]), eps=0.0)
+    assert torch.allclose(y, torch.tensor([[3 / r, 4 / r]]), rtol=1e-6)
+    y = ops.rmsnorm_ref(x, torch.tensor([2.0, 0.5]), eps=0.0)
+    assert torch.allclose(y, torch.tensor([[6 / r, 2 / r]]), rtol=1e-6)
+    # eps enters under the square root
+    y = ops.rmsnorm_ref(x, torch.tensor([1.0, 1.0]), eps=0.5)
+    assert torch.allclose(y, torch.tensor([[3 / math.sqrt(13.0), 4 / math.sqrt(13.0)]]), rtol=1e-6)
+
+
+def test_rmsnorm_invariants():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(16, 96, generator=g)
+    w = torch.ones(96)
+    y = ops.rmsnorm_ref(x, w, eps=0.0)
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(16), rtol=1e-5)   # unit RMS per row
+    assert torch.allclose(ops.rmsnorm_ref(7.3 * x, w, 0.0), y, rtol=1e-5, atol=1e-6)  # scale invariance
+    assert torch.equal(ops.rmsnorm_ref(torch.zeros(2, 8), torch.ones(8)), torch.zeros(2, 8))
+    assert torch.equal(ops.rmsnorm_f32_ref(x, w, 1e-6), ops.rmsnorm_ref(x, w, 1e-6))
+
+
+def test_rmsnorm_brute_force_f64():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(3, 5, generator=g)
+    w = torch.randn(5, generator=g)
+    y = ops.rmsnorm_f32_ref(x, w, 1e-6)
+    for i in range(3):
+        ms = sum(float(v) ** 2 for v in x[i]) / 5
+        for j in range(5):
+            assert abs(float(y[i, j]) - float(x[i, j]) / math.sqrt(ms + 1e-6) * float(w[j])) < 1e-5
+
+
+def test_fused_hidden_is_rne_of_exact_sum():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(64, 256, generator=g).bfloat16()
+    r = torch.randn(64, 256, generator=g).bfloat16()
+    w = (1 + 0.02 * torch.randn(256, generator=g)).bfloat16()
+    hidden, y = ops.fused_residual_add_rmsnorm_ref(x, r, w, 1e-5)
+    assert torch.equal(hidden, _bf16_rne(x.float() + r.float()))
+    # a tie rounds to even: 1 + 2^-8 lies halfway between bf16 1.0 and 1.0078125
+    h, _ = ops.fused_residual_add_rmsnorm_ref(torch.tensor([[1.0]]).bfloat16(),
+                                              torch.tensor([[2.0 ** -8]]).bfloat16(),
+                                              torch.ones(1).bfloat16())
+    assert float(h) == 1.0
+    # the norm is taken of the rounded sum, not of x alone
+    assert torch.equal(y, ops.rmsnorm_f32_ref(hidden, w, 1e-5))
+    assert not torch.equal(y, ops.rmsnorm_f32_ref(x, w, 1e-5))
+
+
+# ---------------------------------------------------------------------------
+# Softmax
+# ---------------------------------------------------------------------------
+
+def test_softmax_known_answer_and_mask():
+    y = ops.softmax_ref(torch.tensor([[0.0, math.log(2), math.log(3)]]))
+    assert torch.allclose(y, torch.tensor([[1 / 6, 1 / 3, 1 / 2]]), rtol=1e-6)
+    g = torch.Generator().manual_seed(4)
+    S = 16
+    x = (3 * torch.randn(2, 3, S, S, generator=g)).half()
+    x = x.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    y = ops.softmax_ref(x)
+    assert y.dtype == torch.float16
+    nz = (y != 0).sum(-1)
+    assert torch.equal(nz, torch.arange(1, S + 1).expand(2, 3, S))     # row i: i+1 non-zeros
+    assert bool((y[..., 0, 0] == 1.0).all())                             # row 0 is exactly 1
+    eq = torch.zeros(S, S).masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    ye = ops.softmax_ref(eq)
+    for i in range(S):
+        assert torch.allclose(ye[i, : i + 1], torch.full((i + 1,), 1.0 / (i + 1)))
+
+
+def test_softmax_invariants():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(32, 100, generator=g)
+    y = ops.softmax_ref(x)
+    assert torch.allclose(y.sum(-1), torch.ones(32), atol=1e-6)
+    assert torch.allclose(ops.softmax_ref(x + 11.0), y, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ls", [0.0, 0.1])
+def test_ce_rows_match_torch_cross_entropy(ls):
+    g = torch.Generator().manual_seed(6)
+    logits = 3 * torch.randn(24, 37, generator=g)
+    t = torch.randint(0, 37, (24,), generator=g)
+    t[[1, 5, 7]] = -100
+    losses, lse, _, _ = ops.ce_rows_ref(logits, t, 0.0, -100, ls)
+    ref = F.cross_entropy(logits.double(), t, ignore_index=-100, label_smoothing=ls, reduction="none")
+    assert torch.allclose(losses.double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(lse.double(), torch.logsumexp(logits.double(), -1), rtol=1e-6)
+    mean = ops.ce_mean_ref(losses, t)
+    assert torch.allclose(mean.double(), F.cross_entropy(logits.double(), t, label_smoothing=ls), rtol=1e-5)
+
+
+@pytest.mark.parametrize("softcap,ls", [(0.0, 0.0), (0.0, 0.2), (5.0, 0.0), (5.0, 0.1)])
+def test_ce_grad_matches_autograd(softcap, ls):
+    g = torch.Generator().manual_seed(7)
+    logits = (4 * torch.randn(10, 13, generator=g)).double().requires_grad_()
+    t = torch.randint(0, 13, (10,), generator=g)
+    t[3] = -100
+    x = softcap * torch.tanh(logits / softcap) if softcap > 0 else logits
+    loss = F.cross_entropy(x, t, ignore_index=-100, label_smoothing=ls)
+    loss.backward()
+    n_valid = int((t != -100).sum())
+    grad = ops.ce_grad_ref(logits.detach().float(), t, softcap, -100, ls, 1.0 / n_valid)
+    assert torch.allclose(grad.double(), logits.grad, atol=2e-6, rtol=1e-4)
+    losses, _, _, _ = ops.ce_rows_ref(logits.detach().float(), t, softcap, -100, ls)
+    assert torch.allclose(ops.ce_mean_ref(losses, t).double(), loss.detach(), rtol=1e-5)
+
+
+def test_ce_closed_forms():
+    V = 50
+    losses, lse, _, _ = ops.ce_rows_ref(torch.zeros(4, V), torch.tensor([0, 3, 49, 7]))
+    assert torch.allclose(lse, torch.full((4,), math.log(V)))
+    assert torch.allclose(losses, torch.full((4,), math.log(V)))
+    t = torch.full((4,), -100)
+    losses, _, _, _ = ops.ce_rows_ref(torch.randn(4, V), t)
+    assert float(ops.ce_mean_ref(losses, t)) == 0.0
+    x = torch.randn(4, V)
+    tt = torch.tensor([1, 2, 3, 4])
+    l0, s0, _, _ = ops.ce_rows_ref(x, tt)
+    l1, s1, _, _ = ops.ce_rows_ref(x + 9.0, tt)
+    assert torch.allclose(s1, s0 + 9.0, atol=1e-5) and torch.allclose(l1, l0, atol=1e-5)
+
+
+def test_lmhead_ce_ref_matches_materialised():
+    g = torch.Generator().manual_seed(8)
+    h = torch.randn(40, 64, generator=g)
+    W = 0.1 * torch.randn(1000, 64, generator=g)
+    t = torch.randint(0, 1000, (40,), generator=g)
+    t[[0, 9]] = -100
+    loss, lse, losses = ops.lmhead_ce_ref(h, W, t, vocab_chunk=4096)
+    logits = h.double() @ W.double().t()
+    assert torch.allclose(lse.double(), torch.logsumexp(logits, -1), rtol=1e-6)
+    assert torch.allclose(loss.double(), F.cross_entropy(logits, t), rtol=1e-5)
+    for chunk in (7, 256, 333):
+        l2, s2, _ = ops.lmhead_ce_ref(h, W, t, vocab_chunk=chunk)
+        assert torch.allclose(s2, lse, rtol=1e-6) and torch.allclose(l2, loss, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Scans
+# ---------------------------------------------------------------------------
+
+def _kat():
+    with open(os.path.join(GOLDEN, "griffin_kat.json")) as f:
+        return json.load(f)
+
+
+def test_diag_scan_known_answer():
+    k = _kat()
+    dA = torch.tensor(k["decay"]).view(1, 4, 1)
+    dBx = torch.tensor(k["value"]).view(1, 4, 1)
+    y = ops.diag_scan_ref(dA, dBx, torch.ones(1, 4, 1), torch.zeros(1), torch.zeros(1, 4, 1))
+    assert torch.allclose(y.view(-1), torch.tensor(k["expected"]), rtol=1e-6)
+    x = torch.randn(1, 4, 1)
+    y = ops.diag_scan_ref(dA, dBx, torch.zeros(1, 4, 1), torch.full((1,), 2.5), x)
+    assert torch.allclose(y, 2.5 * x)
+
+
+def test_selective_scan_known_answer():
+    """KAT mapped to N=1: A=-1, delta_t = -ln(a_t), B=C=1, D=None, u_t = b_t / delta_t."""
+    k = _kat()
+    a = torch.tensor(k["decay"], dtype=torch.float64)
+    delta = (-torch.log(a)).float().view(1, 1, 4)
+    u = (torch.tensor(k["value"], dtype=torch.float64) / -torch.log(a)).float().view(1, 1, 4)
+    A = torch.tensor([[-1.0]])
+    B = torch.ones(1, 1, 4)
+    y = ops.selective_scan_ref(u, delta, A, B, B.clone())
+    assert torch.allclose(y.view(-1), torch.tensor(k["expected"]), rtol=1e-5)
+    yc, _ = c_oracle.selective_scan(u, delta, A, B, B.clone())
+    assert torch.allclose(yc.view(-1), torch.tensor(k["expected"]), rtol=1e-5)
+
+
+def _scan_inputs(b=2, d=4, l=32, n=8, g=1, seed=9):
+    gen = torch.Generator().manual_seed(seed)
+    u = torch.randn(b, d, l, generator=gen)
+    delta = 0.5 * torch.rand(b, d, l, generator=gen)
+    A = -0.5 * torch.rand(d, n, generator=gen) - 0.1
+    B = torch.randn(b, g, n, l, generator=gen)
+    C = torch.randn(b, g, n, l, generator=gen)
+    D = torch.randn(d, generator=gen)
+    z = torch.randn(b, d, l, generator=gen)
+    bias = 0.5 * torch.rand(d, generator=gen)
+    return u, delta, A, B, C, D, z, bias
+
+
+def test_selective_scan_closed_forms():
+    u, delta, A, B, C, D, z, bias = _scan_inputs()
+    # delta = 0: no state, out = D * u * silu(z)
+    out = ops.selective_scan_ref(u, torch.zeros_like(delta), A, B, C, D, z)
+    assert torch.allclose(out, D[:, None] * u * F.silu(z), atol=1e-6)
+    # A = 0: the state is a running sum of delta*u*B
+    out = ops.selective_scan_ref(u, delta, torch.zeros_like(A), B, C)
+    h = torch.cumsum((delta * u)[:, :, None, :] * B, dim=-1)          # [b, d, n, l] (g=1 broadcasts)
+    assert torch.allclose(out, (h * C).sum(2), rtol=1e-4, atol=1e-5)
+    # L = 1
+    out = ops.selective_scan_ref(u[..., :1], delta[..., :1], A, B[..., :1], C[..., :1], D)
+    y1 = (delta[..., :1] * u[..., :1])[:, :, None, :] * B[..., :1] * C[..., :1]
+    assert torch.allclose(out, y1.sum(2) + D[:, None] * u[..., :1], atol=1e-6)
+
+
+def test_selective_scan_invariants():
+    u, delta, A, B, C, D, z, bias = _scan_inputs(l=40)
+    u2 = torch.randn_like(u)
+    lin = ops.selective_scan_ref(2 * u + 3 * u2, delta, A, B, C, D)
+    sep = 2 * ops.selective_scan_ref(u, delta, A, B, C, D) + 3 * ops.selective_scan_ref(u2, delta, A, B, C, D)
+    assert torch.allclose(lin, sep, rtol=1e-4, atol=1e-4)
+    # split equivalence: scan(L) == scan(L/2) then continue from last_state
+    full, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, bias, True, return_last_state=True)
+    h = 20
+    a1, s1 = ops.selective_scan_ref(u[..., :h], delta[..., :h], A, B[..., :h], C[..., :h], D,
+                                    z[..., :h], bias, True, return_last_state=True)
+    a2, s2 = ops.selective_scan_ref(u[..., h:], delta[..., h:], A, B[..., h:], C[..., h:], D,
+                                    z[..., h:], bias, True, return_last_state=True, initial_state=s1)
+    assert torch.allclose(torch.cat([a1, a2], -1), full, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(s2, last, rtol=1e-5, atol=1e-6)
+    # softplus / bias are applied to delta before everything else
+    pre = ops.selective_scan_ref(u, F.softplus(delta + bias[:, None]), A, B, C, D, z)
+    assert torch.allclose(pre, ops.selective_scan_ref(u, delta, A, B, C, D, z, bias, True), atol=1e-6)
+
+
+def test_selective_scan_groups():
+    u, delta, A, B, C, D, z, bias = _scan_inputs(d=8, g=2)
+    out = ops.selective_scan_ref(u, delta, A, B, C, D, z)
+    lo = ops.selective_scan_ref(u[:, :4], delta[:, :4], A[:4], B[:, 0], C[:, 0], D[:4], z[:, :4])
+    hi = ops.selective_scan_ref(u[:, 4:], delta[:, 4:], A[4:], B[:, 1], C[:, 1], D[4:], z[:, 4:])
+    assert torch.allclose(out, torch.cat([lo, hi], 1), atol=1e-6)
+
+
+def test_c_oracle_matches_torch_oracle():
+    for g in (1, 2):
+        u, delta, A, B, C, D, z, bias = _scan_inputs(d=8, l=70, g=g, seed=10 + g)
+        ref, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, bias, True, return_last_state=True)
+        out, lc = c_oracle.selective_scan(u, delta, A, B, C, D, z, bias, True)
+        assert torch.allclose(out, ref, rtol=1e-5, atol=1e-5)
+        assert torch.allclose(lc, last, rtol=1e-5, atol=1e-6)
+
+
+def test_silu_dtype_choice_is_rounding_only():
+    u, delta, A, B, C, D, z, bias = _scan_inputs()
+    zb = z.bfloat16()
+    a = ops.selective_scan_ref(u, delta, A, B, C, D, zb, silu_fp32=True)
+    b = ops.selective_scan_ref(u, delta, A, B, C, D, zb, silu_fp32=False)
+    assert torch.allclose(a, b, rtol=1e-2, atol=1e-2)
