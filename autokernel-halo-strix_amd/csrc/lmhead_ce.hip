@@ -19,10 +19,12 @@
 // Tile mechanics: the MFMA A operand is a 32-row slab of `weight` (vocab
 // rows), B is a 32-row slab of `hidden` (token rows); both are K-contiguous
 // in memory and are staged through LDS in 64-wide K steps, double buffered,
-// with the 16-byte chunk index XOR-swizzled by (row / 2) mod 8 so that the
-// ds_read_b128 fragment reads and the ds_write_b128 fills are bank-conflict
-// free. 8 waves per workgroup, each owning 128 vocab x 64 token accumulators
-// (4 x 2 MFMA 32x32 blocks). Workgroup ids are remapped so that the 32
+// by direct global-to-LDS loads (global_load_lds_dwordx4), with the 16-byte
+// chunk index XOR-swizzled by (row / 2) mod 8 so that the ds_read_b128
+// fragment reads are bank-conflict free. 4 waves per workgroup (one per SIMD), each owning 128 vocab x 128
+// token accumulators (4 x 4 MFMA 32x32 blocks, 256 accumulator registers):
+// every 16-byte fragment read from LDS feeds 4 MFMAs, and the fragments of
+// the next 16-wide K slice are read while the current slice's 16 MFMAs run. Workgroup ids are remapped so that the 32
 // workgroups an XCD runs at once cover a compact 4 x 8 block of tiles and
 // share its weight / hidden slabs in that XCD's L2.
 #include "ak_common.h"
@@ -33,7 +35,7 @@ namespace {
 constexpr int kTV = 256;      // vocab rows per workgroup tile
 constexpr int kTT = 256;      // tokens per workgroup tile
 constexpr int kKS = 64;       // K per LDS stage
-constexpr int kLThreads = 512;
+constexpr int kLThreads = 256;
 constexpr int kChunks = kKS / 8;                          // 16-byte chunks per staged row
 constexpr int kStageChunks = (kTV + kTT) * kChunks;       // u32x4 per stage
 constexpr int kGroupV = 4;                                // vocab tiles per XCD group
@@ -58,18 +60,18 @@ struct MSPair {
 };
 
 template <typename T>
-__global__ void __launch_bounds__(kLThreads)
+__global__ void __launch_bounds__(kLThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
                       const int64_t* __restrict__ targets, MSPair* __restrict__ part,
                       float* __restrict__ tgt_logit, int n_rows, int vocab, int d,
                       int64_t ldh, int64_t ldw, int n_vt, int n_tt) {
-  __shared__ u32x4 lds[2 * kStageChunks];  // 128 KiB
+  __shared__ u32x4 lds[2 * kStageChunks];  // 128 KiB: two K stages of weight + hidden slabs
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wv = wave >> 2;  // vocab half (128 rows)
-  const int wt = wave & 3;   // token quarter (64 columns)
+  const int wv = wave >> 1;  // vocab half (128 rows)
+  const int wt = wave & 1;   // token half (128 columns)
 
   // ---- tile coordinates (XCD-grouped order) ----
   const int n_tiles = n_vt * n_tt;
@@ -85,70 +87,113 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
   const int v0 = vt * kTV;
   const int t0 = tt * kTT;
 
-  // ---- global -> LDS loader: 4 weight chunks + 4 hidden chunks per thread ----
-  const T* gsrc[8];
-  int ldst[8];
+  // ---- global -> LDS loader (direct-to-LDS DMA, no staging registers) ----
+  // A stage is 512 rows x 8 chunks of 16 bytes: weight rows 0..255 then
+  // hidden rows 256..511. global_load_lds_dwordx4 writes lane i's 16 bytes to
+  // (uniform LDS block base + 16 i), so each instruction fills one 1 KiB block
+  // = 8 consecutive rows; lane i fetches the logical chunk that the XOR
+  // swizzle places at physical chunk i % 8 of row i / 8. Waves 0-1 load the
+  // weight slab, waves 2-3 the hidden slab, 128 rows (16 blocks) each.
+  const bool loads_w = wave < 2;
+  const int lrow0 = (wave & 1) * 128;
+  const int first = loads_w ? v0 : t0;
+  const int last = (loads_w ? vocab : n_rows) - 1 - first;
+  const int64_t gld = loads_w ? ldw : ldh;
+  const T* slab = (loads_w ? W : H) + (int64_t)first * gld;
+  const int lds_row0 = (loads_w ? 0 : kTV) + lrow0;
+  uint32_t goff[16];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int id = tid + kLThreads * q;
-    const int row = id >> 3, c = id & 7;
-    const int vr = min(v0 + row, vocab - 1);
-    const int tr = min(t0 + row, n_rows - 1);
-    gsrc[q] = W + (int64_t)vr * ldw + 8 * c;
-    gsrc[4 + q] = H + (int64_t)tr * ldh + 8 * c;
-    ldst[q] = row * kChunks + swz(row, c);
-    ldst[4 + q] = (kTV + row) * kChunks + swz(kTV + row, c);
+  for (int j = 0; j < 16; ++j) {
+    const int row = lrow0 + 8 * j + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    goff[j] = (uint32_t)min(row, last) * (uint32_t)gld + 8 * c;
   }
-  u32x4 stage_regs[8];
-  auto gload = [&](int k0) {
+  auto dma = [&](int k0, int st) {
+    u32x4* blk = lds + st * kStageChunks + lds_row0 * kChunks;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) stage_regs[q] = *reinterpret_cast<const u32x4*>(gsrc[q] + k0);
-  };
-  auto lstore = [&](int st) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) lds[st * kStageChunks + ldst[q]] = stage_regs[q];
+    for (int j = 0; j < 16; ++j) {
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(slab + goff[j] + k0),
+          (__attribute__((address_space(3))) void*)(blk + 8 * j * kChunks), 16, 0, 0);
+    }
   };
 
-  // fragment rows this lane reads
-  int arow[4], brow[2];
-#pragma unroll
-  for (int vb = 0; vb < 4; ++vb) arow[vb] = wv * 128 + vb * 32 + (lane & 31);
-#pragma unroll
-  for (int tb = 0; tb < 2; ++tb) brow[tb] = kTV + wt * 64 + tb * 32 + (lane & 31);
+  // Fragment reads: rows wv*128 + 32i + lane%32 (weight) and
+  // kTV + wt*128 + 32i + lane%32 (hidden); the swizzle is again common to i.
+  const int fr = lane & 31;
+  const int fsw = (fr >> 1) & 7;
+  const int abase = (wv * 128 + fr) * kChunks;
+  const int bbase = (kTV + wt * 128 + fr) * kChunks;
   const int khalf = lane >> 5;
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[4][4];
 #pragma unroll
   for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[vb][tb][r] = 0.0f;
 
+  auto load_frags = [&](const u32x4* sb, int kk, u32x4* af, u32x4* bf) {
+    const int c = (2 * kk + khalf) ^ fsw;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = sb[abase + 32 * i * kChunks + c];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bf[i] = sb[bbase + 32 * i * kChunks + c];
+  };
+
+  // Main loop. Branch-free so the scheduling directives below act on one
+  // basic block per K step: the global loads for step ks+1 go out during the
+  // first 16-wide slice, each slice's 16 MFMAs are interleaved with the 8
+  // ds_reads of the next slice's fragments, and the staged chunks are written
+  // to the other LDS stage at the end. On the last step the loader re-reads
+  // the last valid K slab into the unused stage instead of branching.
+  // Main loop. Branch-free so the scheduling directives below act on one
+  // basic block per K step: the DMA for step ks+1 goes out during the first
+  // 16-wide slice, and each slice's 16 MFMAs are interleaved with the 8
+  // ds_reads of the next slice's fragments. On the last step the loader
+  // re-reads the last valid K slab into the unused stage instead of
+  // branching. s_waitcnt(0) + barrier publish the new stage.
   const int nk = d / kKS;
-  gload(0);
-  lstore(0);
+  dma(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  u32x4 af[2][4], bf[2][4];
+  load_frags(lds, 0, af[0], bf[0]);
 
   for (int ks = 0; ks < nk; ++ks) {
     const int st = ks & 1;
-    if (ks + 1 < nk) gload((ks + 1) * kKS);
     const u32x4* sb = lds + st * kStageChunks;
+    dma(min(ks + 1, nk - 1) * kKS, st ^ 1);
 #pragma unroll
     for (int kk = 0; kk < kKS / 16; ++kk) {
-      const int chunk = 2 * kk + khalf;
-      u32x4 af[4], bfr[2];
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb) af[vb] = sb[arow[vb] * kChunks + swz(arow[vb], chunk)];
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb) bfr[tb] = sb[brow[tb] * kChunks + swz(brow[tb], chunk)];
+      const int cur = kk & 1;
+      if (kk + 1 < kKS / 16) load_frags(sb, kk + 1, af[cur ^ 1], bf[cur ^ 1]);
 #pragma unroll
       for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) acc[vb][tb] = mfma32(T(), af[vb], bfr[tb], acc[vb][tb]);
+        for (int tb = 0; tb < 4; ++tb)
+          acc[vb][tb] = mfma32(T(), af[cur][vb], bf[cur][tb], acc[vb][tb]);
+      if (kk == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // 2 global->LDS loads
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      } else if (kk + 1 < kKS / 16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
     }
-    if (ks + 1 < nk) lstore(st ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    load_frags(lds + (st ^ 1) * kStageChunks, 0, af[0], bf[0]);
   }
 
   // ---- epilogue: per-token online-softmax partial over this wave's 128 rows ----
@@ -156,8 +201,8 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
   const bool tail = v0 + kTV > vocab;
   float* msbuf = reinterpret_cast<float*>(lds);  // [2 halves][2 (m,s)][256 tokens]
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int col = wt * 64 + tb * 32 + (lane & 31);
+  for (int tb = 0; tb < 4; ++tb) {
+    const int col = wt * 128 + tb * 32 + (lane & 31);
     const int tok = t0 + col;
     if (tail) {
 #pragma unroll
@@ -207,7 +252,7 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
   }
   __syncthreads();
   // merge the two vocab halves and publish this tile's partial
-  if (tid < kTT) {
+  {
     const int tok = t0 + tid;
     if (tok < n_rows) {
       const float m0 = msbuf[0 * kTT + tid], s0 = msbuf[1 * kTT + tid];
@@ -221,24 +266,41 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
   }
 }
 
-// lse / per-token loss from the vocab-tile partials.
-__global__ void __launch_bounds__(256)
+// lse / per-token loss from the vocab-tile partials. A 1024-thread workgroup
+// owns 64 tokens; its 16 waves each fold every 16th vocab tile with an online
+// (max, sum) merge (coalesced 512-byte reads per wave), then the 16 partial
+// states are merged in a fixed order through LDS (deterministic).
+constexpr int kRowsPerBlock = 64;
+constexpr int kRowGroups = 16;
+
+__device__ __forceinline__ MSPair ms_merge(MSPair a, MSPair b) {
+  const float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return {m, 0.0f};
+  float s = 0.0f;
+  if (a.m != -INFINITY) s += a.s * __builtin_amdgcn_exp2f((a.m - m) * kLog2e);
+  if (b.m != -INFINITY) s += b.s * __builtin_amdgcn_exp2f((b.m - m) * kLog2e);
+  return {m, s};
+}
+
+__global__ void __launch_bounds__(kRowsPerBlock * kRowGroups)
 lmhead_ce_rows_kernel(const MSPair* __restrict__ part, const float* __restrict__ tgt_logit,
                       const int64_t* __restrict__ targets, float* __restrict__ lse,
                       float* __restrict__ losses, int n_rows, int vocab, int n_vt,
                       int64_t ignore_index) {
-  const int row = blockIdx.x * 256 + threadIdx.x;
-  if (row >= n_rows) return;
-  float m = -INFINITY;
-  for (int v = 0; v < n_vt; ++v) m = fmaxf(m, part[(int64_t)v * n_rows + row].m);
-  float s = 0.0f;
-  if (m != -INFINITY) {
-    for (int v = 0; v < n_vt; ++v) {
-      const MSPair pr = part[(int64_t)v * n_rows + row];
-      if (pr.m != -INFINITY) s += pr.s * __builtin_amdgcn_exp2f((pr.m - m) * kLog2e);
-    }
+  __shared__ MSPair red[kRowGroups][kRowsPerBlock];
+  const int r = threadIdx.x % kRowsPerBlock;
+  const int grp = threadIdx.x / kRowsPerBlock;
+  const int row = blockIdx.x * kRowsPerBlock + r;
+  MSPair st{-INFINITY, 0.0f};
+  if (row < n_rows) {
+#pragma unroll 4
+    for (int v = grp; v < n_vt; v += kRowGroups) st = ms_merge(st, part[(int64_t)v * n_rows + row]);
   }
-  const float l = m + fast_log(s);
+  red[grp][r] = st;
+  __syncthreads();
+  if (grp != 0 || row >= n_rows) return;
+  for (int g = 1; g < kRowGroups; ++g) st = ms_merge(st, red[g][r]);
+  const float l = st.m + fast_log(st.s);
   lse[row] = l;
   const int64_t t = targets[row];
   float loss;
@@ -308,7 +370,8 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
   lmhead_ce_tile_kernel<T><<<dim3(n_vt * n_tt), dim3(kLThreads), 0, s>>>(
       static_cast<const T*>(h), static_cast<const T*>(w), targets, part, tgt, n_rows, vocab, d, ldh,
       ldw, n_vt, n_tt);
-  lmhead_ce_rows_kernel<<<dim3((n_rows + 255) / 256), dim3(256), 0, s>>>(
+  lmhead_ce_rows_kernel<<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
+                          dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
       part, tgt, targets, lse, lrow, n_rows, vocab, n_vt, ignore_index);
   lmhead_ce_mean_kernel<<<dim3(1), dim3(1024), 0, s>>>(lrow, targets, loss, n_valid, n_rows,
                                                       ignore_index);

@@ -1,10 +1,11 @@
 // RMSNorm and fused residual-add + RMSNorm for gfx950.
 //
-// Row-parallel, HBM-bound. A row is owned by TPR threads (one wave for rows
-// up to 64*8 16-byte vectors, otherwise a 256- or 1024-thread workgroup).
-// Each thread keeps its slice of the row in registers as fp32 between the
-// sum-of-squares reduction and the normalise pass, so x and residual are read
-// from HBM exactly once and new_residual / y written exactly once.
+// Row-parallel, HBM-bound. A row is owned by 64..1024 threads holding one
+// 16-byte vector each (up to 8 for rows over 1024 vectors). Each thread keeps
+// its slice of the row in registers as fp32 between the sum-of-squares
+// reduction and the normalise pass, so x and residual are read from HBM
+// exactly once and new_residual / y written exactly once, with nontemporal
+// (streaming) accesses.
 //
 // Arithmetic follows reference.py:25-29 and :71-78 of the reference:
 //   h     = round_T(x + residual)              (fp32 add, one rounding)
@@ -15,81 +16,92 @@
 namespace ak {
 namespace {
 
-template <typename T, bool RES, int VPT, int TPR>
+// TPR threads own a row (TPR / 64 waves; 256 / TPR rows per 256-thread
+// workgroup when TPR < 256). The workgroup walks rows with a grid stride so
+// the grid can be sized to the machine; the loop bound is uniform per
+// workgroup, so the barrier of the multi-wave reduction is always reached by
+// every wave. NT selects nontemporal (streaming) global loads and stores.
+template <typename T, bool RES, int VPT, int TPR, bool NT>
 __global__ void __launch_bounds__(TPR >= 256 ? TPR : 256)
 rownorm_vec_kernel(const T* __restrict__ x, const T* __restrict__ r,
                    const T* __restrict__ w, T* __restrict__ nr, T* __restrict__ y,
                    int64_t rows, int cols, int64_t ld_x, int64_t ld_r,
                    int64_t ld_nr, int64_t ld_y, float eps) {
   constexpr int VE = Vec16<T>::VE;
-  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
-  static_assert(TPR == 64 || TPR >= 256, "row owners are one wave or a whole workgroup");
+  constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;  // rows per workgroup
+  constexpr int WPR = TPR / 64;                      // waves per row
+  static_assert(TPR % 64 == 0, "rows are owned by whole waves");
+  __shared__ float part[RPW][WPR];
 
   const int t = threadIdx.x % TPR;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_WG + threadIdx.x / TPR;
-  if (TPR == 64 && row >= rows) return;  // whole wave leaves together
+  const int rl = threadIdx.x / TPR;
   const int nvec = cols / VE;
+  auto ld = [](const T* p) { return NT ? load16_nt(p) : load16(p); };
+  auto st = [](T* p, const Vec16<T>& v) {
+    if (NT) store16_nt(p, v);
+    else store16(p, v);
+  };
 
-  const T* xr = x + row * ld_x;
-  float h[VPT][VE];
-  float ss = 0.0f;
-
+  for (int64_t base = (int64_t)blockIdx.x * RPW; base < rows; base += (int64_t)gridDim.x * RPW) {
+    const int64_t row = base + rl;
+    const bool live = row < rows;
+    float h[VPT][VE];
+    float ss = 0.0f;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int v = t + k * TPR;
-    if (v < nvec) {
-      Vec16<T> xv = load16(xr + (int64_t)v * VE);
-      if constexpr (RES) {
-        Vec16<T> rv = load16(r + row * ld_r + (int64_t)v * VE);
+    for (int k = 0; k < VPT; ++k) {
+      const int v = t + k * TPR;
+      if (live && v < nvec) {
+        Vec16<T> xv = ld(x + row * ld_x + (int64_t)v * VE);
+        if constexpr (RES) {
+          Vec16<T> rv = ld(r + row * ld_r + (int64_t)v * VE);
 #pragma unroll
-        for (int e = 0; e < VE; ++e) {
-          // Round the sum to T first: new_residual and the normalised value
-          // both see the same rounded hidden state.
-          h[k][e] = to_f32(from_f32<T>(to_f32(xv.e[e]) + to_f32(rv.e[e])));
+          for (int e = 0; e < VE; ++e) {
+            // Round the sum to T first: new_residual and the normalised value
+            // both see the same rounded hidden state.
+            h[k][e] = to_f32(from_f32<T>(to_f32(xv.e[e]) + to_f32(rv.e[e])));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VE; ++e) h[k][e] = to_f32(xv.e[e]);
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < VE; ++e) h[k][e] = to_f32(xv.e[e]);
+        for (int e = 0; e < VE; ++e) h[k][e] = 0.0f;
       }
-    } else {
 #pragma unroll
-      for (int e = 0; e < VE; ++e) h[k][e] = 0.0f;
+      for (int e = 0; e < VE; ++e) ss = fmaf(h[k][e], h[k][e], ss);
     }
-#pragma unroll
-    for (int e = 0; e < VE; ++e) ss = fmaf(h[k][e], h[k][e], ss);
-  }
 
-  ss = wave_sum(ss);
-  if constexpr (TPR > 64) {
-    __shared__ float part[TPR / 64];
-    const int wid = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) part[wid] = ss;
-    __syncthreads();
-    ss = 0.0f;
+    ss = wave_sum(ss);
+    if constexpr (WPR > 1) {
+      if ((threadIdx.x & 63) == 0) part[rl][t / 64] = ss;
+      __syncthreads();
+      ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TPR / 64; ++i) ss += part[i];
-  }
-
-  const float rms = sqrtf(ss / (float)cols + eps);
+      for (int i = 0; i < WPR; ++i) ss += part[rl][i];
+      __syncthreads();  // part is reused by the next row of this workgroup
+    }
+    const float rms = sqrtf(ss / (float)cols + eps);
 
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int v = t + k * TPR;
-    if (v < nvec) {
-      const int64_t off = (int64_t)v * VE;
-      Vec16<T> wv = load16(w + off);
-      Vec16<T> yv;
+    for (int k = 0; k < VPT; ++k) {
+      const int v = t + k * TPR;
+      if (live && v < nvec) {
+        const int64_t off = (int64_t)v * VE;
+        Vec16<T> wv = load16(w + off);
+        Vec16<T> yv;
 #pragma unroll
-      for (int e = 0; e < VE; ++e) yv.e[e] = from_f32<T>((h[k][e] / rms) * to_f32(wv.e[e]));
-      if constexpr (RES) {
-        if (nr != nullptr) {
-          Vec16<T> hv;
+        for (int e = 0; e < VE; ++e) yv.e[e] = from_f32<T>((h[k][e] / rms) * to_f32(wv.e[e]));
+        if constexpr (RES) {
+          if (nr != nullptr) {
+            Vec16<T> hv;
 #pragma unroll
-          for (int e = 0; e < VE; ++e) hv.e[e] = from_f32<T>(h[k][e]);
-          store16(nr + row * ld_nr + off, hv);
+            for (int e = 0; e < VE; ++e) hv.e[e] = from_f32<T>(h[k][e]);
+            st(nr + row * ld_nr + off, hv);
+          }
         }
+        st(y + row * ld_y + off, yv);
       }
-      store16(y + row * ld_y + off, yv);
     }
   }
 }
@@ -134,9 +146,9 @@ template <typename T, bool RES, int VPT, int TPR>
 void launch_vec(const T* x, const T* r, const T* w, T* nr, T* y, int64_t rows, int cols,
                 int64_t ld_x, int64_t ld_r, int64_t ld_nr, int64_t ld_y, float eps,
                 hipStream_t s) {
-  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
-  const int64_t grid = (rows + ROWS_PER_WG - 1) / ROWS_PER_WG;
-  rownorm_vec_kernel<T, RES, VPT, TPR><<<dim3((unsigned)grid), dim3(TPR * ROWS_PER_WG), 0, s>>>(
+  constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
+  const int64_t grid = (rows + RPW - 1) / RPW;
+  rownorm_vec_kernel<T, RES, VPT, TPR, true><<<dim3((unsigned)grid), dim3(TPR * RPW), 0, s>>>(
       x, r, w, nr, y, rows, cols, ld_x, ld_r, ld_nr, ld_y, eps);
 }
 
@@ -156,20 +168,27 @@ int dispatch(const void* xv, const void* rv, const void* wv, void* nrv, void* yv
   if (RES && nr) vec_ok = vec_ok && ld_nr % VE == 0 && aligned16(nr);
   const int64_t nvec = cols / VE;
   const int c = (int)cols;
-  if (vec_ok && nvec <= 64 * 8) {
-    if (nvec <= 64) launch_vec<T, RES, 1, 64>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-    else if (nvec <= 128) launch_vec<T, RES, 2, 64>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-    else if (nvec <= 256) launch_vec<T, RES, 4, 64>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-    else launch_vec<T, RES, 8, 64>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-  } else if (vec_ok && nvec <= 256 * 8) {
-    if (nvec <= 256 * 4) launch_vec<T, RES, 4, 256>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-    else launch_vec<T, RES, 8, 256>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-  } else if (vec_ok && nvec <= 1024 * 8) {
-    launch_vec<T, RES, 8, 1024>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s);
-  } else {
+#define AK_LAUNCH(VPT, TPR) launch_vec<T, RES, VPT, TPR>(x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps, s)
+  // One 16-byte vector per thread while the row fits in 1024 threads: the
+  // most waves in flight per byte, which is what saturates HBM here
+  // (fused C3 shape: 1 vector x 512 threads beat 8 vectors x 64 threads by
+  // 25% on MI355X).
+  if (!vec_ok) {
+    rownorm_generic_kernel<T, RES><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
+        x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps);
+  } else if (nvec <= 64) AK_LAUNCH(1, 64);
+  else if (nvec <= 128) AK_LAUNCH(1, 128);
+  else if (nvec <= 256) AK_LAUNCH(1, 256);
+  else if (nvec <= 512) AK_LAUNCH(1, 512);
+  else if (nvec <= 1024) AK_LAUNCH(1, 1024);
+  else if (nvec <= 2048) AK_LAUNCH(2, 1024);
+  else if (nvec <= 4096) AK_LAUNCH(4, 1024);
+  else if (nvec <= 8192) AK_LAUNCH(8, 1024);
+  else {
     rownorm_generic_kernel<T, RES><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
         x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps);
   }
+#undef AK_LAUNCH
   return ak_check_launch(name);
 }
 

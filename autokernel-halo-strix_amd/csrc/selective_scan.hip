@@ -74,7 +74,11 @@ __device__ __forceinline__ float softplus_f32(float x) {
   return x > 20.0f ? x : log1pf(expf(x));
 }
 
-__device__ __forceinline__ float silu_f32(float z) { return z / (1.0f + expf(-z)); }
+// silu(z) = z / (1 + exp(-z)) with the hardware exp2 and reciprocal (about
+// 1 ulp each), evaluated once per output element.
+__device__ __forceinline__ float silu_fast(float z) {
+  return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
 
 template <typename T>
 __device__ __forceinline__ float ld(const void* p, int64_t i) {
@@ -117,37 +121,57 @@ mamba_scan_fwd_kernel(ScanParams p) {
   float h = 0.0f;
   float* hb = hbuf[wave];
 
-  for (int l0 = 0; l0 < p.seqlen; l0 += kScanT) {
-    __syncthreads();  // previous tile's readers of Bs / Cs are done
-    {
-      // B and C tile: thread (sn, q) converts steps 4q..4q+3 of state sn.
-      const int sn = tid / 16, q = tid % 16;
-      float bv[4], cv[4];
+  // Global loads for one 64-step tile, issued one tile ahead of their use so
+  // that their latency hides behind the previous tile's recurrence.
+  struct TileRegs {
+    float bv[4], cv[4];  // B / C staging: state sn, steps 4q..4q+3
+    float dv[4], uv[4];  // this lane's broadcast steps 4n..4n+3
+    float uo[4], zo[4];  // output steps 16*blk + n, blk = 0..3
+  };
+  const int sn = tid / 16, q = tid % 16;
+  auto load_tile = [&](int l0, TileRegs& r) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int l = l0 + 4 * q + k;
-        const bool ok = sn < p.dstate && l < p.seqlen;
-        bv[k] = ok ? ld<TBC>(p.B, B_base + (int64_t)sn * p.B_ns + l) : 0.0f;
-        cv[k] = ok ? ld<TBC>(p.C, C_base + (int64_t)sn * p.C_ns + l) : 0.0f;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        Bs[sn * kBStride + 4 * q + k] = bv[k];
-        Cs[(4 * q + k) * kCStride + sn] = cv[k];
-      }
+    for (int k = 0; k < 4; ++k) {
+      const int l = l0 + 4 * q + k;
+      const bool ok = sn < p.dstate && l < p.seqlen;
+      r.bv[k] = ok ? ld<TBC>(p.B, B_base + (int64_t)sn * p.B_ns + l) : 0.0f;
+      r.cv[k] = ok ? ld<TBC>(p.C, C_base + (int64_t)sn * p.C_ns + l) : 0.0f;
     }
-    // This lane owns steps l0 + 4n .. 4n+3 of its channel for the broadcasts.
-    float dl[4], du[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int l = l0 + 4 * n + k;
       const bool ok = ch_ok && l < p.seqlen;
-      float dv = ok ? ld<TD>(p.delta, d_row + l) + dbias : 0.0f;
-      if (p.softplus) dv = softplus_f32(dv);
-      const float uv = ok ? ld<TU>(p.u, u_row + l) : 0.0f;
-      dl[k] = ok ? dv : 0.0f;
-      du[k] = dl[k] * uv;
+      r.dv[k] = ok ? ld<TD>(p.delta, d_row + l) : 0.0f;
+      r.uv[k] = ok ? ld<TU>(p.u, u_row + l) : 0.0f;
     }
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int l = l0 + 16 * blk + n;
+      const bool ok = ch_ok && l < p.seqlen;
+      r.uo[blk] = ok ? ld<TU>(p.u, u_row + l) : 0.0f;
+      r.zo[blk] = (ok && p.z) ? ld<TU>(p.z, z_row + l) : 0.0f;
+    }
+  };
+
+  TileRegs cur, nxt{};
+  load_tile(0, cur);
+  for (int l0 = 0; l0 < p.seqlen; l0 += kScanT) {
+    __syncthreads();  // previous tile's readers of Bs / Cs are done
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      Bs[sn * kBStride + 4 * q + k] = cur.bv[k];
+      Cs[(4 * q + k) * kCStride + sn] = cur.cv[k];
+    }
+    float dl[4], du[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool ok = ch_ok && l0 + 4 * n + k < p.seqlen;
+      float dv = cur.dv[k] + dbias;
+      if (p.softplus) dv = softplus_f32(dv);
+      dl[k] = ok ? dv : 0.0f;
+      du[k] = dl[k] * cur.uv[k];
+    }
+    if (l0 + kScanT < p.seqlen) load_tile(l0 + kScanT, nxt);
     __syncthreads();
 
 #pragma unroll
@@ -157,8 +181,7 @@ mamba_scan_fwd_kernel(ScanParams p) {
       for (int j4 = 0; j4 < 4; ++j4) {
         const int src = blk * 4 + j4;  // lane in the row that owns these 4 steps
         const float* brow = &Bs[n * kBStride + 16 * blk + 4 * j4];
-        const float b0 = brow[0], b1 = brow[1], b2 = brow[2], b3 = brow[3];
-        const float bvals[4] = {b0, b1, b2, b3};
+        const float bvals[4] = {brow[0], brow[1], brow[2], brow[3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           const float a = __builtin_amdgcn_exp2f(row_bcast(dl[k], src) * a_scaled);
@@ -172,21 +195,20 @@ mamba_scan_fwd_kernel(ScanParams p) {
       for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
       __builtin_amdgcn_wave_barrier();
       // Lane (c, j=n) now reduces step j of channel c over the 16 states.
-      const int j = n;
-      const float* hrow = &hb[c * kHC + j * kHJ];
-      const float* crow = &Cs[(16 * blk + j) * kCStride];
+      const float* hrow = &hb[c * kHC + n * kHJ];
+      const float* crow = &Cs[(16 * blk + n) * kCStride];
       float y = 0.0f;
 #pragma unroll
       for (int s = 0; s < 16; ++s) y = fmaf(hrow[s], crow[s], y);
       __builtin_amdgcn_wave_barrier();
-      const int l = l0 + 16 * blk + j;
+      const int l = l0 + 16 * blk + n;
       if (ch_ok && l < p.seqlen) {
-        const float uv = ld<TU>(p.u, u_row + l);
-        float o = fmaf(dskip, uv, y);
-        if (p.z) o *= silu_f32(ld<TU>(p.z, z_row + l));
+        float o = fmaf(dskip, cur.uo[blk], y);
+        if (p.z) o *= silu_fast(cur.zo[blk]);
         static_cast<TU*>(p.out)[o_row + l] = from_f32<TU>(o);
       }
     }
+    cur = nxt;
   }
   if (p.last_state && ch_ok && n_ok) {
     p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;

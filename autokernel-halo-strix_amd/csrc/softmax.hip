@@ -2,8 +2,9 @@
 //
 // HBM-bound: each row is read once into registers (as fp32), reduced for its
 // max and for sum(exp(x - max)) with wave64 DPP reductions, then normalised
-// and written once. Rows up to 64*8 16-byte vectors are owned by one wave
-// (no barriers), wider rows by a 256- or 1024-thread workgroup. Rows are
+// and written once, with nontemporal accesses. Rows of up to 128 16-byte
+// vectors are owned by one wave (no barriers), wider rows by up to 1024
+// threads holding one vector each (up to 8 past 1024 vectors). Rows are
 // indexed with 64-bit arithmetic and every row gets its own owner, so there
 // is no grid-size cap on the row count.
 //
@@ -15,75 +16,86 @@
 namespace ak {
 namespace {
 
-template <typename T, int VPT, int TPR>
+// TPR threads own a row (TPR / 64 waves; 256 / TPR rows per workgroup when
+// TPR < 256); rows are walked with a workgroup-uniform grid stride so the
+// cross-wave reductions' barriers are reached by every wave. NT selects
+// nontemporal global loads and stores.
+template <typename T, int VPT, int TPR, bool NT>
 __global__ void __launch_bounds__(TPR >= 256 ? TPR : 256)
 softmax_vec_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
                    int64_t ld_x, int64_t ld_y) {
   constexpr int VE = Vec16<T>::VE;
-  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
+  constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
+  constexpr int WPR = TPR / 64;
+  static_assert(TPR % 64 == 0, "rows are owned by whole waves");
+  __shared__ float part[RPW][WPR];
   const int t = threadIdx.x % TPR;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_WG + threadIdx.x / TPR;
-  if (TPR == 64 && row >= rows) return;
+  const int rl = threadIdx.x / TPR;
   const int nvec = cols / VE;
-  const T* xr = x + row * ld_x;
 
-  float v[VPT][VE];
-  float m = -INFINITY;
+  for (int64_t base = (int64_t)blockIdx.x * RPW; base < rows; base += (int64_t)gridDim.x * RPW) {
+    const int64_t row = base + rl;
+    const bool live = row < rows;
+    const T* xr = x + row * ld_x;
+    float v[VPT][VE];
+    float m = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int c = t + k * TPR;
-    if (c < nvec) {
-      Vec16<T> xv = load16(xr + (int64_t)c * VE);
+    for (int k = 0; k < VPT; ++k) {
+      const int c = t + k * TPR;
+      if (live && c < nvec) {
+        Vec16<T> xv = NT ? load16_nt(xr + (int64_t)c * VE) : load16(xr + (int64_t)c * VE);
 #pragma unroll
-      for (int e = 0; e < VE; ++e) {
-        v[k][e] = to_f32(xv.e[e]);
-        m = fmaxf(m, v[k][e]);
+        for (int e = 0; e < VE; ++e) {
+          v[k][e] = to_f32(xv.e[e]);
+          m = fmaxf(m, v[k][e]);
+        }
       }
     }
-  }
-  m = wave_max(m);
-  __shared__ float part[TPR > 64 ? TPR / 64 : 1];
-  if constexpr (TPR > 64) {
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = m;
-    __syncthreads();
-    m = part[0];
+    m = wave_max(m);
+    if constexpr (WPR > 1) {
+      if ((threadIdx.x & 63) == 0) part[rl][t / 64] = m;
+      __syncthreads();
+      m = part[rl][0];
 #pragma unroll
-    for (int i = 1; i < TPR / 64; ++i) m = fmaxf(m, part[i]);
-    __syncthreads();
-  }
+      for (int i = 1; i < WPR; ++i) m = fmaxf(m, part[rl][i]);
+      __syncthreads();
+    }
 
-  // exp(x - m): the max element gives exp2(0) = 1 exactly.
-  float s = 0.0f;
+    // exp(x - m): the max element gives exp2(0) = 1 exactly.
+    float s = 0.0f;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int c = t + k * TPR;
-    if (c < nvec) {
+    for (int k = 0; k < VPT; ++k) {
+      const int c = t + k * TPR;
+      if (live && c < nvec) {
 #pragma unroll
-      for (int e = 0; e < VE; ++e) {
-        v[k][e] = fast_exp(v[k][e] - m);
-        s += v[k][e];
+        for (int e = 0; e < VE; ++e) {
+          v[k][e] = fast_exp(v[k][e] - m);
+          s += v[k][e];
+        }
       }
     }
-  }
-  s = wave_sum(s);
-  if constexpr (TPR > 64) {
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = s;
-    __syncthreads();
-    s = 0.0f;
+    s = wave_sum(s);
+    if constexpr (WPR > 1) {
+      if ((threadIdx.x & 63) == 0) part[rl][t / 64] = s;
+      __syncthreads();
+      s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < TPR / 64; ++i) s += part[i];
-  }
-  const float inv = 1.0f / s;
+      for (int i = 0; i < WPR; ++i) s += part[rl][i];
+      __syncthreads();
+    }
+    const float inv = 1.0f / s;
 
-  T* yr = y + row * ld_y;
+    T* yr = y + row * ld_y;
 #pragma unroll
-  for (int k = 0; k < VPT; ++k) {
-    const int c = t + k * TPR;
-    if (c < nvec) {
-      Vec16<T> o;
+    for (int k = 0; k < VPT; ++k) {
+      const int c = t + k * TPR;
+      if (live && c < nvec) {
+        Vec16<T> o;
 #pragma unroll
-      for (int e = 0; e < VE; ++e) o.e[e] = from_f32<T>(v[k][e] * inv);
-      store16(yr + (int64_t)c * VE, o);
+        for (int e = 0; e < VE; ++e) o.e[e] = from_f32<T>(v[k][e] * inv);
+        if (NT) store16_nt(yr + (int64_t)c * VE, o);
+        else store16(yr + (int64_t)c * VE, o);
+      }
     }
   }
 }
@@ -141,12 +153,12 @@ softmax_generic_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
   }
 }
 
-template <typename T, int VPT, int TPR>
+template <typename T, int VPT, int TPR, bool NT>
 void launch_vec(const T* x, T* y, int64_t rows, int cols, int64_t ld_x, int64_t ld_y,
                 hipStream_t s) {
-  constexpr int ROWS_PER_WG = TPR >= 256 ? 1 : 256 / TPR;
-  const int64_t grid = (rows + ROWS_PER_WG - 1) / ROWS_PER_WG;
-  softmax_vec_kernel<T, VPT, TPR><<<dim3((unsigned)grid), dim3(TPR * ROWS_PER_WG), 0, s>>>(
+  constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
+  const int64_t grid = (rows + RPW - 1) / RPW;
+  softmax_vec_kernel<T, VPT, TPR, NT><<<dim3((unsigned)grid), dim3(TPR * RPW), 0, s>>>(
       x, y, rows, cols, ld_x, ld_y);
 }
 
@@ -160,19 +172,18 @@ int dispatch(const void* xv, void* yv, int64_t rows, int64_t cols, int64_t ld_x,
                       aligned16(y);
   const int64_t nvec = cols / VE;
   const int c = (int)cols;
-  if (vec_ok && nvec <= 64 * 8) {
-    if (nvec <= 64) launch_vec<T, 1, 64>(x, y, rows, c, ld_x, ld_y, s);
-    else if (nvec <= 128) launch_vec<T, 2, 64>(x, y, rows, c, ld_x, ld_y, s);
-    else if (nvec <= 256) launch_vec<T, 4, 64>(x, y, rows, c, ld_x, ld_y, s);
-    else launch_vec<T, 8, 64>(x, y, rows, c, ld_x, ld_y, s);
-  } else if (vec_ok && nvec <= 256 * 8) {
-    if (nvec <= 256 * 4) launch_vec<T, 4, 256>(x, y, rows, c, ld_x, ld_y, s);
-    else launch_vec<T, 8, 256>(x, y, rows, c, ld_x, ld_y, s);
-  } else if (vec_ok && nvec <= 1024 * 8) {
-    launch_vec<T, 8, 1024>(x, y, rows, c, ld_x, ld_y, s);
-  } else {
+#define AK_LAUNCH(VPT, TPR) launch_vec<T, VPT, TPR, true>(x, y, rows, c, ld_x, ld_y, s)
+  if (!vec_ok || nvec > 8192) {
     softmax_generic_kernel<T><<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, y, rows, c, ld_x, ld_y);
-  }
+  } else if (nvec <= 64) AK_LAUNCH(1, 64);
+  else if (nvec <= 128) AK_LAUNCH(2, 64);
+  else if (nvec <= 256) AK_LAUNCH(1, 256);
+  else if (nvec <= 512) AK_LAUNCH(1, 512);
+  else if (nvec <= 1024) AK_LAUNCH(1, 1024);
+  else if (nvec <= 2048) AK_LAUNCH(2, 1024);
+  else if (nvec <= 4096) AK_LAUNCH(4, 1024);
+  else AK_LAUNCH(8, 1024);
+#undef AK_LAUNCH
   return ak_check_launch("ak_softmax_fwd");
 }
 

@@ -188,7 +188,8 @@ class _CrossEntropyHIP(torch.autograd.Function):
             logits, targets, row_max, row_sum = ctx.saved_tensors
             # The loss is a mean over non-ignored rows, so its gradient is
             # scaled by 1 / n_valid (torch.nn.functional.cross_entropy's
-            # gradient); the reference's tiny mode used 1 / batch here.
+            # gradient); the reference's tiny mode used 1 / batch here
+            # (kernels/ce_fused.py:607, :661).
             n_valid = float(ctx.n_valid_t.item())
             g = float(grad_loss.item()) if grad_loss.dim() == 0 else 1.0
             grad_logits = _get_bwd_module().cross_entropy_bwd_tiny_hip(

@@ -95,7 +95,7 @@ def _rmsnorm_backward(ctx, grad_output):
     grad_normed = g_f * w_f
     # d/dx of x * r * w with r = (mean(x^2) + eps)^-1/2; the projection term
     # carries one more factor of r (the reference's HIP backward kernel,
-    # rmsnorm_backward.py:166-168; its PyTorch fallback at :73-97 drops it).
+    # rmsnorm_backward.py:166-168; its PyTorch fallback, _torch_ops.py:95, drops it).
     grad_x = rms_inv * (grad_normed - normed * (grad_normed * normed).sum(-1, keepdim=True) / D)
     return grad_x.to(x.dtype), grad_weight.to(weight.dtype), None
 

@@ -42,6 +42,21 @@ BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, vendor spec
 ROTATE_BYTES = 640 * 2 ** 20   # > 2x the 256 MB MALL
 
 METRIC = "HBM GB/s (% of roofline) per kernel; selective-scan Mtok/s vs CPU ref"
+TRAFFIC_TABLE = os.path.join(ROOT, "profiles", "hbm_traffic_pmc.md")
+
+
+def measured_traffic(kernel):
+    """Calibrated HBM bytes per launch of ``kernel`` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None if absent)."""
+    try:
+        with open(TRAFFIC_TABLE) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 7 and cells[0] == kernel:
+                    return int(cells[4].replace(",", ""))
+    except OSError:
+        pass
+    return None
 
 
 # ---------------------------------------------------------------------------
@@ -259,6 +274,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -268,6 +286,13 @@ def main(argv=None):
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.ones(256 * 2 ** 20 // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     names = [n.strip() for n in args.only.split(",") if n.strip()]
     if "c2" not in names:
         names.insert(0, "c2")
@@ -329,7 +354,7 @@ def main(argv=None):
         "config": {"workload": case.workload, "rows": 98304, "cols": 1024, "mask": "causal -inf",
                    "accumulate": "fp32", "input_sets_rotated": len(case.sets)},
         "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": h["frac"], "traffic": None},
+                     "frac": h["frac"], "traffic": measured_traffic("softmax_vec_kernel")},
         "cpu_baseline": None,
         "kernels": kernels,
         "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
