@@ -2,13 +2,14 @@
 //
 // logits[t, v] = hidden[t, :] . weight[v, :] are produced on the matrix
 // cores (v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation) and consumed in
-// registers: each 256(vocab) x 256(token) workgroup tile reduces its logits
-// to one online-softmax partial (max, sum exp(x - max)) per token, and the
-// workgroup whose vocab range holds a token's target records that token's
-// target logit. Logits never reach memory. A row kernel then merges the
-// partials of all vocab tiles into logsumexp and per-token loss, and a
-// single-workgroup kernel forms the mean over non-ignored tokens in a fixed
-// order (deterministic).
+// registers: each wave of a 256(vocab) x 256(token) tile reduces its
+// 128 x 128 block of logits to one online-softmax partial (max, sum
+// exp(x - max)) per token. Logits never reach memory. A row kernel then
+// merges the partials of all vocab tiles into logsumexp, computes each
+// token's target logit as its own dot product hidden[t] . weight[target[t]]
+// (fp32 accumulation) and forms the per-token loss; a single-workgroup
+// kernel forms the mean over non-ignored tokens in a fixed order
+// (deterministic).
 //
 // Semantics: kernels/hip/chunked_linear_cross_entropy.py:55-148 and
 // kernels/ce_fused.py:236-260 of the reference (loss = lse - logit[target],
@@ -16,29 +17,42 @@
 // denominator, which is clamped to >= 1). The logsumexp runs over all
 // `vocab` columns (padded vocab entries are not masked, as in the reference).
 //
-// Tile mechanics: the MFMA A operand is a 32-row slab of `weight` (vocab
-// rows), B is a 32-row slab of `hidden` (token rows); both are K-contiguous
-// in memory and are staged through LDS in 64-wide K steps, double buffered,
-// by direct global-to-LDS loads (global_load_lds_dwordx4), with the 16-byte
-// chunk index XOR-swizzled by (row / 2) mod 8 so that the ds_read_b128
-// fragment reads are bank-conflict free. 4 waves per workgroup (one per SIMD), each owning 128 vocab x 128
-// token accumulators (4 x 4 MFMA 32x32 blocks, 256 accumulator registers):
-// every 16-byte fragment read from LDS feeds 4 MFMAs, and the fragments of
-// the next 16-wide K slice are read while the current slice's 16 MFMAs run. Workgroup ids are remapped so that the 32
-// workgroups an XCD runs at once cover a compact 4 x 8 block of tiles and
-// share its weight / hidden slabs in that XCD's L2.
+// Tile kernel mechanics:
+// * Persistent: one 256-thread workgroup per CU walks its tiles in an
+//   XCD-grouped order (the 32 workgroups of an XCD cover a compact block of
+//   vocab x token tiles, so their weight / hidden slabs are shared in that
+//   XCD's L2).
+// * Operands: the MFMA A operand is a 32-row slab of `weight` (vocab rows),
+//   B a 32-row slab of `hidden` (token rows). Both are K-contiguous and are
+//   staged through LDS in K blocks of 64 (one 128-byte cache line per row)
+//   by direct global-to-LDS loads (global_load_lds_dwordx4, 8 rows x 128 B
+//   per instruction). The 160 KiB of LDS hold a ring of 5 slots of 256 rows
+//   x 128 B; weight and hidden blocks take turns, each operand is loaded
+//   two K blocks ahead of its use, and the loads are spread over the block's
+//   MFMAs so that the CU's address unit keeps up without stalling them. The
+//   ring runs on across tile boundaries. The 16-byte chunk index of a staged row is XOR-swizzled by
+//   (row / 2) mod 8, which makes the ds_read_b128 fragment reads
+//   bank-conflict free.
+// * 4 waves (one per SIMD), each owning 128 vocab x 128 token accumulators
+//   (4 x 4 MFMA 32x32 blocks, 256 accumulator registers): every 16-byte
+//   fragment read from LDS feeds 4 MFMAs. The instruction order is pinned:
+//   the 16 MFMAs of a 16-wide K slice run over 16 different accumulators
+//   while the fragments of the slice after next are read; one barrier per K
+//   block (after its second slice) publishes the next block's slots.
 #include "ak_common.h"
 
 namespace ak {
 namespace {
 
-constexpr int kTV = 256;      // vocab rows per workgroup tile
-constexpr int kTT = 256;      // tokens per workgroup tile
-constexpr int kKS = 64;       // K per LDS stage
+constexpr int kTV = 256;      // vocab rows per tile
+constexpr int kTT = 256;      // tokens per tile
+constexpr int kKB = 64;       // K per block (one 128-byte line per bf16 row)
+constexpr int kSlots = 5;     // LDS ring slots
 constexpr int kLThreads = 256;
-constexpr int kChunks = kKS / 8;                          // 16-byte chunks per staged row
-constexpr int kStageChunks = (kTV + kTT) * kChunks;       // u32x4 per stage
-constexpr int kGroupV = 4;                                // vocab tiles per XCD group
+constexpr int kChunks = kKB / 8;                         // 16-byte chunks per staged row
+constexpr int kSlotChunks = 256 * kChunks;               // u32x4 per slot (32 KiB)
+constexpr int kDma = 256 / 8 / 4;                        // DMA instructions per wave per slot
+constexpr int kGroupV = 4;                               // vocab tiles per XCD group
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -53,223 +67,359 @@ __device__ __forceinline__ f32x16_t mfma32(f16, u32x4 a, u32x4 b, f32x16_t c) {
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), expcnt and lgkmcnt(0).
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
 struct MSPair {
   float m, s;
 };
 
-template <typename T>
+// One accumulator element copied from its AGPR to a VGPR at this point of
+// the program (an explicit read keeps the compiler from copying all 256
+// accumulators into VGPRs at once ahead of the epilogue).
+__device__ __forceinline__ float acc_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
+// Tile coordinates of this workgroup's i-th tile. Work item w = block + i *
+// grid runs on XCD w % 8 (workgroups are dealt to the 8 XCDs round-robin);
+// items of one XCD are numbered consecutively, then cut into groups of
+// kGroupV vocab tiles x all token tiles, token-minor within a group.
+__device__ __forceinline__ void tile_coords(int i, int n_vt, int n_tt, int& vt, int& tt) {
+  const int n_tiles = n_vt * n_tt;
+  const int w = (int)blockIdx.x + i * (int)gridDim.x;
+  int lin = w;
+  if ((gridDim.x & 7) == 0) {
+    const int x = w & 7, base = n_tiles >> 3, rem = n_tiles & 7;
+    lin = x * base + min(x, rem) + (w >> 3);
+  }
+  const int per_group = kGroupV * n_tt;
+  const int grp = lin / per_group;
+  const int in_grp = lin - grp * per_group;
+  const int gv0 = grp * kGroupV;
+  const int gvn = min(kGroupV, n_vt - gv0);
+  vt = gv0 + in_grp % gvn;
+  tt = in_grp / gvn;
+}
+
+// Instruction order of one 16-MFMA K slice: kDs x (MFMA, DS read), then
+// kDmaN x (MFMA, global-to-LDS load), then the remaining MFMAs. (Finer
+// interleavings are not honoured by the compiler's scheduler, which then
+// clusters the reads.)
+template <int kDs, int kDmaN>
+__device__ __forceinline__ void slice_order() {
+#pragma unroll
+  for (int i = 0; i < kDs; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+  }
+#pragma unroll
+  for (int i = 0; i < kDmaN; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 global->LDS load
+  }
+  if (16 - kDs - kDmaN > 0) __builtin_amdgcn_sched_group_barrier(0x008, 16 - kDs - kDmaN, 0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Workgroup barrier that publishes LDS filled by this workgroup's
+// global_load_lds DMA: the caller has already waited (s_waitcnt) for its own
+// DMA loads. A release fence here would wait for every outstanding DMA load
+// (vmcnt(0)) and so drain the ring; the empty asm statements keep the
+// compiler from moving LDS accesses across the barrier instead.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Row range of a tile along one dimension of `n` rows: the tile owns rows
+// [own, min(own + 256, n)) and stages the 256 rows starting at `first`. With
+// kShift (n >= 256) a tail tile is shifted back so that its 256 staged rows
+// end at row n - 1 (the overlap with the previous tile is masked);
+// otherwise staged rows past n - 1 re-read row n - 1.
+template <bool kShift>
+__device__ __forceinline__ int tile_first(int own, int n) {
+  return kShift ? min(own, n - 256) : own;
+}
+
+// Partial of vocab tile vt, vocab half h (0/1), token t: part[(2 vt + h) * n_rows + t].
+//
+// kFineMask: the vocab rows a tile owns may end inside a wave's 128-row
+// half (vocab % 128 != 0, or unshifted tail tiles), so the epilogue masks
+// element by element; otherwise a wave's half is either wholly owned or
+// wholly skipped.
+template <typename T, bool kShift, bool kFineMask>
 __global__ void __launch_bounds__(kLThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
-lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W,
-                      const int64_t* __restrict__ targets, MSPair* __restrict__ part,
-                      float* __restrict__ tgt_logit, int n_rows, int vocab, int d,
-                      int64_t ldh, int64_t ldw, int n_vt, int n_tt) {
-  __shared__ u32x4 lds[2 * kStageChunks];  // 128 KiB: two K stages of weight + hidden slabs
+lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* __restrict__ part,
+                      int n_rows, int vocab, int d, int64_t ldh, int64_t ldw, int n_vt, int n_tt) {
+  __shared__ u32x4 lds[kSlots * kSlotChunks];  // 160 KiB ring
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wv = wave >> 1;  // vocab half (128 rows)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = wave >> 1;  // vocab half (128 rows) of the accumulators
   const int wt = wave & 1;   // token half (128 columns)
 
-  // ---- tile coordinates (XCD-grouped order) ----
   const int n_tiles = n_vt * n_tt;
-  int lin = blockIdx.x;
-  if ((n_tiles & 7) == 0) lin = (lin & 7) * (n_tiles >> 3) + (lin >> 3);
-  const int per_group = kGroupV * n_tt;
-  const int grp = lin / per_group;
-  const int in_grp = lin % per_group;
-  const int gv0 = grp * kGroupV;
-  const int gvn = min(kGroupV, n_vt - gv0);
-  const int vt = gv0 + in_grp % gvn;
-  const int tt = in_grp / gvn;
-  const int v0 = vt * kTV;
-  const int t0 = tt * kTT;
+  const int n_my = (int)blockIdx.x < n_tiles ? (n_tiles - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+  if (n_my == 0) return;
+  const int nb = d / kKB;  // K blocks per tile
 
-  // ---- global -> LDS loader (direct-to-LDS DMA, no staging registers) ----
-  // A stage is 512 rows x 8 chunks of 16 bytes: weight rows 0..255 then
-  // hidden rows 256..511. global_load_lds_dwordx4 writes lane i's 16 bytes to
-  // (uniform LDS block base + 16 i), so each instruction fills one 1 KiB block
-  // = 8 consecutive rows; lane i fetches the logical chunk that the XOR
-  // swizzle places at physical chunk i % 8 of row i / 8. Waves 0-1 load the
-  // weight slab, waves 2-3 the hidden slab, 128 rows (16 blocks) each.
-  const bool loads_w = wave < 2;
-  const int lrow0 = (wave & 1) * 128;
-  const int first = loads_w ? v0 : t0;
-  const int last = (loads_w ? vocab : n_rows) - 1 - first;
-  const int64_t gld = loads_w ? ldw : ldh;
-  const T* slab = (loads_w ? W : H) + (int64_t)first * gld;
-  const int lds_row0 = (loads_w ? 0 : kTV) + lrow0;
-  uint32_t goff[16];
+  // ---- loader ----
+  // A slot is 256 rows x 8 chunks of 16 bytes. global_load_lds_dwordx4
+  // writes lane i's 16 bytes to (uniform LDS base + 16 i), so one
+  // instruction fills 8 consecutive rows, each a full 128-byte line; lane i
+  // fetches the logical chunk that the swizzle puts at physical chunk i % 8
+  // of row i / 8. Each wave stages 64 rows of every slot. Byte offsets
+  // within a 256-row slab fit 32 bits (row pitch < 2^23 elements).
+  // The row of instruction j is lrow + 8 j; its swizzle key ((row / 2) mod
+  // 8) = (4 j + lane / 16) mod 8 depends on j only through j's parity.
+  const int lrow = wave * 64 + (lane >> 3);
+  const uint32_t c16[2] = {16u * (uint32_t)((lane & 7) ^ (lane >> 4)),
+                           16u * (uint32_t)((lane & 7) ^ ((lane >> 4) + 4))};
+  const uint32_t ldw_b = (uint32_t)ldw * (uint32_t)sizeof(T);
+  const uint32_t ldh_b = (uint32_t)ldh * (uint32_t)sizeof(T);
+  const uint32_t voff_w[2] = {(uint32_t)lrow * ldw_b + c16[0], (uint32_t)lrow * ldw_b + c16[1]};
+  const uint32_t voff_h[2] = {(uint32_t)lrow * ldh_b + c16[0], (uint32_t)lrow * ldh_b + c16[1]};
+  // Where the rows of one operand of one K block come from.
+  struct Src {
+    const char* p;  // row 0 of the 256-row slab, at the block's K offset
+    int last;       // last valid slab row (clamped variant only)
+  };
+  auto dma = [&](Src src, uint32_t ld_b, const uint32_t* voff, int slot, int j0 = 0,
+                 int j1 = kDma) {
+    u32x4* blk = lds + slot * kSlotChunks + wave * 64 * kChunks;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const int row = lrow0 + 8 * j + (lane >> 3);
-    const int c = (lane & 7) ^ ((row >> 1) & 7);
-    goff[j] = (uint32_t)min(row, last) * (uint32_t)gld + 8 * c;
-  }
-  auto dma = [&](int k0, int st) {
-    u32x4* blk = lds + st * kStageChunks + lds_row0 * kChunks;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(slab + goff[j] + k0),
-          (__attribute__((address_space(3))) void*)(blk + 8 * j * kChunks), 16, 0, 0);
+    for (int j = j0; j < j1; ++j) {
+      const char* q;
+      if (kShift) q = src.p + 8 * j * ld_b + voff[j & 1];
+      else q = src.p + (uint32_t)min(lrow + 8 * j, src.last) * ld_b + c16[j & 1];
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)q,
+                                       (__attribute__((address_space(3))) void*)(blk + 8 * j * kChunks),
+                                       16, 0, 0);
+    }
+  };
+  // Cursor over (tile, K block) for one operand: the slab of this
+  // workgroup's tile `it` (tiles past the last one repeat the last tile).
+  struct Cursor {
+    int it, blk;
+    const char* slab;
+    int last;
+  };
+  auto cursor_tile = [&](Cursor& c, bool is_w) {
+    int vt, tt;
+    tile_coords(min(c.it, n_my - 1), n_vt, n_tt, vt, tt);
+    const int n = is_w ? vocab : n_rows;
+    const int first = tile_first<kShift>(is_w ? vt * kTV : tt * kTT, n);
+    c.slab = reinterpret_cast<const char*>((is_w ? W : H) + (int64_t)first * (is_w ? ldw : ldh));
+    c.last = n - 1 - first;
+  };
+  auto cursor_src = [&](const Cursor& c) {
+    return Src{c.slab + c.blk * kKB * (int)sizeof(T), c.last};
+  };
+  auto cursor_next = [&](Cursor& c, bool is_w) {
+    if (++c.blk == nb) {
+      c.blk = 0;
+      ++c.it;
+      cursor_tile(c, is_w);
     }
   };
 
-  // Fragment reads: rows wv*128 + 32i + lane%32 (weight) and
-  // kTV + wt*128 + 32i + lane%32 (hidden); the swizzle is again common to i.
+  // ---- fragment reads ----
+  // Rows wv*128 + 32i + lane%32 of the weight slot and wt*128 + 32i +
+  // lane%32 of the hidden slot; lanes 32-63 take the upper 8 K of a slice.
   const int fr = lane & 31;
   const int fsw = (fr >> 1) & 7;
-  const int abase = (wv * 128 + fr) * kChunks;
-  const int bbase = (kTV + wt * 128 + fr) * kChunks;
   const int khalf = lane >> 5;
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[vb][tb][r] = 0.0f;
-
-  auto load_frags = [&](const u32x4* sb, int kk, u32x4* af, u32x4* bf) {
-    const int c = (2 * kk + khalf) ^ fsw;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = sb[abase + 32 * i * kChunks + c];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) bf[i] = sb[bbase + 32 * i * kChunks + c];
+  const int arow = (wv * 128 + fr) * kChunks;
+  const int brow = (wt * 128 + fr) * kChunks;
+  auto frag = [&](int slot, int row, int i, int kk) {
+    return lds[slot * kSlotChunks + row + 32 * i * kChunks + ((2 * kk + khalf) ^ fsw)];
   };
 
-  // Main loop. Branch-free so the scheduling directives below act on one
-  // basic block per K step: the global loads for step ks+1 go out during the
-  // first 16-wide slice, each slice's 16 MFMAs are interleaved with the 8
-  // ds_reads of the next slice's fragments, and the staged chunks are written
-  // to the other LDS stage at the end. On the last step the loader re-reads
-  // the last valid K slab into the unused stage instead of branching.
-  // Main loop. Branch-free so the scheduling directives below act on one
-  // basic block per K step: the DMA for step ks+1 goes out during the first
-  // 16-wide slice, and each slice's 16 MFMAs are interleaved with the 8
-  // ds_reads of the next slice's fragments. On the last step the loader
-  // re-reads the last valid K slab into the unused stage instead of
-  // branching. s_waitcnt(0) + barrier publish the new stage.
-  const int nk = d / kKS;
-  dma(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  u32x4 af[2][4], bf[2][4];
-  load_frags(lds, 0, af[0], bf[0]);
+  // ---- prologue: K blocks 0 and 1 ----
+  // Ring order: W0 H0 W1 H1 W2 H2 W3 ...; operand block q lives in slot q % 5.
+  Cursor cw{0, 0, nullptr, 0}, ch{0, 0, nullptr, 0};
+  cursor_tile(cw, true);
+  cursor_tile(ch, false);
+  dma(cursor_src(cw), ldw_b, voff_w, 0);  // q = 0
+  cursor_next(cw, true);
+  dma(cursor_src(ch), ldh_b, voff_h, 1);  // q = 1
+  cursor_next(ch, false);
+  dma(cursor_src(cw), ldw_b, voff_w, 2);  // q = 2
+  dma(cursor_src(ch), ldh_b, voff_h, 3);  // q = 3
+  // cw and ch at K block 1: each K block first advances them to the blocks
+  // it loads (weight and hidden of block j + 2)
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * kDma));  // q = 0, 1 landed
+  ring_barrier();
 
-  for (int ks = 0; ks < nk; ++ks) {
-    const int st = ks & 1;
-    const u32x4* sb = lds + st * kStageChunks;
-    dma(min(ks + 1, nk - 1) * kKS, st ^ 1);
-#pragma unroll
-    for (int kk = 0; kk < kKS / 16; ++kk) {
-      const int cur = kk & 1;
-      if (kk + 1 < kKS / 16) load_frags(sb, kk + 1, af[cur ^ 1], bf[cur ^ 1]);
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-          acc[vb][tb] = mfma32(T(), af[cur][vb], bf[cur][tb], acc[vb][tb]);
-      if (kk == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // 2 global->LDS loads
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      } else if (kk + 1 < kKS / 16) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    load_frags(lds + (st ^ 1) * kStageChunks, 0, af[0], bf[0]);
-  }
+  f32x16_t acc[4][4];
+  u32x4 af[4][4], bf[4][4];  // fragments of the 4 slices of a K block
 
-  // ---- epilogue: per-token online-softmax partial over this wave's 128 rows ----
-  const int vbase = v0 + wv * 128;
-  const bool tail = v0 + kTV > vocab;
-  float* msbuf = reinterpret_cast<float*>(lds);  // [2 halves][2 (m,s)][256 tokens]
+  // Slots of K block j (counted over all of this workgroup's blocks):
+  // weight in (2j) % 5, hidden in (2j + 1) % 5.
+  int sw = 0, sh = 1;
+  auto load_frags = [&](int slw, int slh, int kk, u32x4* a, u32x4* b) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int col = wt * 128 + tb * 32 + (lane & 31);
-    const int tok = t0 + col;
-    if (tail) {
-#pragma unroll
-      for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int v = vbase + vb * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-          if (v >= vocab) acc[vb][tb][r] = -INFINITY;
-        }
+    for (int i = 0; i < 4; ++i) {
+      a[i] = frag(slw, arow, i, kk);
+      b[i] = frag(slh, brow, i, kk);
     }
-    float m = -INFINITY;
+  };
+  auto mfmas = [&](auto first_tag, const u32x4* a, const u32x4* b) {
+    constexpr bool kFirst = decltype(first_tag)::value;
 #pragma unroll
     for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) m = fmaxf(m, acc[vb][tb][r]);
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
-    const float ms = m * kLog2e;
-    float s = 0.0f;
-#pragma unroll
-    for (int vb = 0; vb < 4; ++vb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s += __builtin_amdgcn_exp2f(fmaf(acc[vb][tb][r], kLog2e, -ms));
-    s += __shfl_xor(s, 32, 64);
+      for (int tb = 0; tb < 4; ++tb)
+        acc[vb][tb] = mfma32(T(), a[vb], b[tb], kFirst ? f32x16_t{} : acc[vb][tb]);
+  };
 
-    // target logit: recorded by the one lane that holds it
-    if (tok < n_rows) {
-      const int64_t tgt = targets[tok];
-      const int64_t lr = tgt - vbase;
-      if (lr >= 0 && lr < 128 && tgt < vocab) {
-        const int i = (int)lr & 31, tvb = (int)lr >> 5;
-        if (((i >> 2) & 1) == khalf) {
-          const int tr = (i & 3) + 4 * (i >> 3);
-          float tv = 0.0f;
+  // One K block j: 4 slices of 16 MFMAs. Fragments are read two slices
+  // ahead of their MFMAs (slices 0 and 1 of block j are in af/bf[0..1] on
+  // entry), which gives the LDS reads a full slice of slack against the
+  // ring's DMA writes into LDS. Loads are spread over the block so that the
+  // CU's address unit (about 20 cycles per 1 KiB load) is never asked for
+  // more than a slice can cover: the weight operand of block j + 2 goes into
+  // slot (2j + 4) % 5 (free since block j - 1) during slices 0 and 1. The
+  // barrier after slice 1 (a) shows every wave done reading block j's slots
+  // (its last fragments are read during slice 1), and the hidden operand of
+  // block j + 2 then goes into block j's weight slot during slices 2 and 3;
+  // (b) publishes block j + 1's slots, whose first two slices' fragments
+  // slices 2 and 3 read (this wave's loads of them are done once only the 8
+  // loads issued after them, weight j + 2, are outstanding; memory
+  // operations complete in issue order, and anything else issued later only
+  // makes the wait stricter). A tile's last block reads no fragments of the
+  // next block (the epilogue runs first).
+  auto block = [&](auto first_tag, auto last_tag) {
+    constexpr bool kLastBlk = decltype(last_tag)::value;
+    cursor_next(cw, true);
+    cursor_next(ch, false);
+    const Src ws = cursor_src(cw), hs = cursor_src(ch);
+    const int pw = sw + 4 >= kSlots ? sw + 4 - kSlots : sw + 4;  // slot of q = 2j + 4
+    const int nsw = sw + 2 >= kSlots ? sw + 2 - kSlots : sw + 2;
+    const int nsh = sh + 2 >= kSlots ? sh + 2 - kSlots : sh + 2;
+    load_frags(sw, sh, 2, af[2], bf[2]);
+    mfmas(first_tag, af[0], bf[0]);
+    dma(ws, ldw_b, voff_w, pw, 0, kDma / 2);
+    slice_order<8, kDma / 2>();
+    load_frags(sw, sh, 3, af[3], bf[3]);
+    mfmas(std::false_type{}, af[1], bf[1]);
+    dma(ws, ldw_b, voff_w, pw, kDma / 2, kDma);
+    slice_order<8, kDma / 2>();
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(kDma));
+    ring_barrier();
+    if (!kLastBlk) load_frags(nsw, nsh, 0, af[0], bf[0]);
+    mfmas(std::false_type{}, af[2], bf[2]);
+    dma(hs, ldh_b, voff_h, sw, 0, kDma / 2);
+    if constexpr (kLastBlk) slice_order<0, kDma / 2>();
+    else slice_order<8, kDma / 2>();
+    if (!kLastBlk) load_frags(nsw, nsh, 1, af[1], bf[1]);
+    mfmas(std::false_type{}, af[3], bf[3]);
+    dma(hs, ldh_b, voff_h, sw, kDma / 2, kDma);
+    if constexpr (kLastBlk) slice_order<0, kDma / 2>();
+    else slice_order<8, kDma / 2>();
+    sw = nsw;
+    sh = nsh;
+  };
+
+  using yes = std::true_type;
+  using no = std::false_type;
+  for (int it = 0; it < n_my; ++it) {
+    int vt, tt;
+    tile_coords(it, n_vt, n_tt, vt, tt);
+    const int v_own = vt * kTV, t_own = tt * kTT;
+    const int v_first = tile_first<kShift>(v_own, vocab);
+    const int t_first = tile_first<kShift>(t_own, n_rows);
+
+    load_frags(sw, sh, 0, af[0], bf[0]);
+    load_frags(sw, sh, 1, af[1], bf[1]);
+    if (nb == 1) {
+      block(yes{}, yes{});
+    } else {
+      block(yes{}, no{});
+      for (int kb = 1; kb < nb - 1; ++kb) block(no{}, no{});
+      block(no{}, yes{});
+    }
+    // The epilogue reads the accumulators with explicit v_accvgpr_read
+    // instructions, which the compiler does not space from the last MFMAs
+    // that wrote them: give those MFMAs (16 passes at most) their wait states.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+
+    // ---- epilogue: per-token online-softmax partial of this wave's 128 rows ----
+    // Row x of this wave's 128-row half (counted from its first staged row,
+    // lanes 32-63 offset by 4) is a real, owned vocab entry iff lo <= x < hi.
+    const int lo_w = v_own - v_first - wv * 128;                    // wave-uniform
+    const int hi_w = min(vocab, v_own + kTV) - v_first - wv * 128;
+    const int lo = lo_w - 4 * khalf;
+    const int hi = hi_w - 4 * khalf;
+    MSPair* prow = part + (int64_t)(2 * vt + wv) * n_rows;
+    MSPair res[4];
+    auto epilogue = [&](auto tail_tag) {
+      constexpr bool kTail = decltype(tail_tag)::value;
 #pragma unroll
-          for (int vb = 0; vb < 4; ++vb)
+      for (int tb = 0; tb < 4; ++tb) {
+        // this token block's 64 logits of the lane, read once from the AGPRs
+        float x[4][16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (vb == tvb && r == tr) tv = acc[vb][tb][r];
-          tgt_logit[tok] = tv;
-        }
+        for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            x[vb][r] = acc_read(acc[vb][tb][r]);
+            if (kTail) {
+              const int o = vb * 32 + 8 * (r >> 2) + (r & 3);
+              x[vb][r] = (o >= lo && o < hi) ? x[vb][r] : -INFINITY;
+            }
+          }
+        float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], x[vb][r]);
+        float m = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        const float ms = m * kLog2e;
+        float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            s4[r & 3] += __builtin_amdgcn_exp2f(fmaf(x[vb][r], kLog2e, -ms));
+        float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        s += __shfl_xor(s, 32, 64);
+        res[tb] = MSPair{m, s};
+        __builtin_amdgcn_sched_barrier(0);  // one token block's values live at a time
       }
+    };
+    if (kFineMask) {
+      epilogue(yes{});
+    } else if (lo_w < 128 && hi_w > 0) {
+      // vocab % 128 == 0: a half that holds any owned row holds 128
+      epilogue(no{});
+    } else {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) res[tb] = MSPair{-INFINITY, 0.0f};
     }
-    if (lane < 32) {
-      msbuf[(wv * 2 + 0) * kTT + col] = m;
-      msbuf[(wv * 2 + 1) * kTT + col] = s;
-    }
-  }
-  __syncthreads();
-  // merge the two vocab halves and publish this tile's partial
-  {
-    const int tok = t0 + tid;
-    if (tok < n_rows) {
-      const float m0 = msbuf[0 * kTT + tid], s0 = msbuf[1 * kTT + tid];
-      const float m1 = msbuf[2 * kTT + tid], s1 = msbuf[3 * kTT + tid];
-      const float m = fmaxf(m0, m1);
-      float s = 0.0f;
-      if (m0 != -INFINITY) s += s0 * __builtin_amdgcn_exp2f((m0 - m) * kLog2e);
-      if (m1 != -INFINITY) s += s1 * __builtin_amdgcn_exp2f((m1 - m) * kLog2e);
-      part[(int64_t)vt * n_rows + tok] = MSPair{m, s};
+    // lanes 0-31 hold the (m, s) of token columns t_first + wt*128 + tb*32 + lane
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int tok = t_first + wt * 128 + tb * 32 + fr;
+      if (lane < 32 && tok >= t_own && tok < n_rows) prow[tok] = res[tb];
     }
   }
+  // drain the ring's trailing (unused) loads before the workgroup exits
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 }
 
 // lse / per-token loss from the vocab-tile partials. A 1024-thread workgroup
-// owns 64 tokens; its 16 waves each fold every 16th vocab tile with an online
-// (max, sum) merge (coalesced 512-byte reads per wave), then the 16 partial
-// states are merged in a fixed order through LDS (deterministic).
+// owns 64 tokens. Its 16 waves first compute the target logits of 4 tokens
+// each (a wave-wide fp32 dot product over d), then each fold every 16th
+// partial (two per vocab tile) with an online (max, sum) merge (coalesced
+// 512-byte reads per wave); the 16 partial states are merged in a fixed
+// order through LDS (deterministic).
 constexpr int kRowsPerBlock = 64;
 constexpr int kRowGroups = 16;
 
@@ -282,19 +432,59 @@ __device__ __forceinline__ MSPair ms_merge(MSPair a, MSPair b) {
   return {m, s};
 }
 
+template <typename T>
 __global__ void __launch_bounds__(kRowsPerBlock * kRowGroups)
-lmhead_ce_rows_kernel(const MSPair* __restrict__ part, const float* __restrict__ tgt_logit,
-                      const int64_t* __restrict__ targets, float* __restrict__ lse,
-                      float* __restrict__ losses, int n_rows, int vocab, int n_vt,
-                      int64_t ignore_index) {
+lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
+                      const MSPair* __restrict__ part, const int64_t* __restrict__ targets,
+                      float* __restrict__ lse, float* __restrict__ losses, int n_rows, int vocab,
+                      int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index) {
+  constexpr int kPerWave = kRowsPerBlock / kRowGroups;
   __shared__ MSPair red[kRowGroups][kRowsPerBlock];
+  __shared__ float tl[kRowsPerBlock];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * kRowsPerBlock;
+
+  // target logits of rows row0 + wave * kPerWave + q
+  {
+    float acc[kPerWave];
+    bool ok[kPerWave];
+    const T* hp[kPerWave];
+    const T* wp[kPerWave];
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      const int row = row0 + wave * kPerWave + q;
+      const int64_t t = row < n_rows ? targets[row] : (int64_t)-1;
+      ok[q] = row < n_rows && t >= 0 && t < vocab;
+      hp[q] = H + (int64_t)(ok[q] ? row : 0) * ldh;
+      wp[q] = W + (ok[q] ? t : 0) * ldw;
+      acc[q] = 0.0f;
+    }
+    const int d8 = d / 8;
+    for (int c = lane; c < d8; c += 64) {
+#pragma unroll
+      for (int q = 0; q < kPerWave; ++q) {
+        if (!ok[q]) continue;
+        const Vec16<T> a = load16<T>(hp[q] + 8 * c);
+        const Vec16<T> b = load16<T>(wp[q] + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q] = fmaf(to_f32(a.e[e]), to_f32(b.e[e]), acc[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      const float v = wave_sum(acc[q]);
+      if (lane == 0) tl[wave * kPerWave + q] = v;
+    }
+  }
+
   const int r = threadIdx.x % kRowsPerBlock;
   const int grp = threadIdx.x / kRowsPerBlock;
-  const int row = blockIdx.x * kRowsPerBlock + r;
+  const int row = row0 + r;
   MSPair st{-INFINITY, 0.0f};
   if (row < n_rows) {
 #pragma unroll 4
-    for (int v = grp; v < n_vt; v += kRowGroups) st = ms_merge(st, part[(int64_t)v * n_rows + row]);
+    for (int v = grp; v < 2 * n_vt; v += kRowGroups) st = ms_merge(st, part[(int64_t)v * n_rows + row]);
   }
   red[grp][r] = st;
   __syncthreads();
@@ -306,7 +496,7 @@ lmhead_ce_rows_kernel(const MSPair* __restrict__ part, const float* __restrict__
   float loss;
   if (t == ignore_index) loss = 0.0f;
   else if (t < 0 || t >= vocab) loss = NAN;
-  else loss = l - tgt_logit[row];
+  else loss = l - tl[r];
   losses[row] = loss;
 }
 
@@ -343,17 +533,29 @@ lmhead_ce_mean_kernel(const float* __restrict__ losses, const int64_t* __restric
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t part, tgt, losses, total;
+  size_t part, losses, total;
 };
 
 WsLayout ws_layout(int64_t n_rows, int64_t vocab) {
   const int64_t n_vt = (vocab + kTV - 1) / kTV;
   WsLayout w;
   w.part = 0;
-  w.tgt = align256((size_t)n_vt * n_rows * sizeof(MSPair));
-  w.losses = w.tgt + align256((size_t)n_rows * 4);
+  w.losses = align256((size_t)2 * n_vt * n_rows * sizeof(MSPair));
   w.total = w.losses + align256((size_t)n_rows * 4);
   return w;
+}
+
+int cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 template <typename T>
@@ -362,17 +564,23 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
                    int64_t ldh, int64_t ldw, int64_t ignore_index, hipStream_t s) {
   const int n_vt = (vocab + kTV - 1) / kTV;
   const int n_tt = (n_rows + kTT - 1) / kTT;
+  const int grid = min(n_vt * n_tt, cu_count());
   WsLayout L = ws_layout(n_rows, vocab);
   char* base = static_cast<char*>(ws);
   MSPair* part = reinterpret_cast<MSPair*>(base + L.part);
-  float* tgt = reinterpret_cast<float*>(base + L.tgt);
   float* lrow = losses ? losses : reinterpret_cast<float*>(base + L.losses);
-  lmhead_ce_tile_kernel<T><<<dim3(n_vt * n_tt), dim3(kLThreads), 0, s>>>(
-      static_cast<const T*>(h), static_cast<const T*>(w), targets, part, tgt, n_rows, vocab, d, ldh,
-      ldw, n_vt, n_tt);
-  lmhead_ce_rows_kernel<<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
-                          dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
-      part, tgt, targets, lse, lrow, n_rows, vocab, n_vt, ignore_index);
+  const T* hp = static_cast<const T*>(h);
+  const T* wp = static_cast<const T*>(w);
+  const dim3 gd(grid), bd(kLThreads);
+  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0)
+    lmhead_ce_tile_kernel<T, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+  else if (vocab >= kTV && n_rows >= kTT)
+    lmhead_ce_tile_kernel<T, true, true><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+  else
+    lmhead_ce_tile_kernel<T, false, true><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+  lmhead_ce_rows_kernel<T><<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
+                             dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
+      hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index);
   lmhead_ce_mean_kernel<<<dim3(1), dim3(1024), 0, s>>>(lrow, targets, loss, n_valid, n_rows,
                                                       ignore_index);
 }
@@ -396,11 +604,14 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape n_rows=%lld vocab=%lld d=%lld", name,
                         (long long)n_rows, (long long)vocab, (long long)d);
-  if (d % ak::kKS) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: d=%lld must be a multiple of %d", name, (long long)d, ak::kKS);
+  if (d % ak::kKB)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: d=%lld must be a multiple of %d", name,
+                        (long long)d, ak::kKB);
   if (n_rows > (1 << 30) || vocab > (1 << 30) || d > (1 << 20))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
-  if (ld_h < d || ld_w < d || ld_h % 8 || ld_w % 8)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitches must be >= d and multiples of 8 elements", name);
+  if (ld_h < d || ld_w < d || ld_h % 8 || ld_w % 8 || ld_h >= (1 << 23) || ld_w >= (1 << 23))
+    return ak_set_error(AK_ERR_INVALID_ARG,
+                        "%s: row pitches must be >= d, multiples of 8 and < 2^23 elements", name);
   if (!hidden || !weight || !targets || !loss || !lse || !workspace)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   if (!ak::aligned16(hidden) || !ak::aligned16(weight) || !ak::aligned16(workspace))

@@ -119,8 +119,10 @@ int ak_ce_bwd_tiny(const void* logits, const int64_t* targets,
  * Replaces the per-chunk F.linear + cross_entropy_fwd_hip loop of
  * kernels/hip/chunked_linear_cross_entropy.py:55-148 (forward value and the
  * logsumexp side output). Only dtype AK_DTYPE_BF16 and AK_DTYPE_F16 are
- * accepted; d must be a multiple of 64 and the rows of hidden and weight
- * 16-byte aligned. workspace must hold ak_lmhead_ce_workspace_bytes() bytes.
+ * accepted; d must be a multiple of 64, the rows of hidden and weight
+ * 16-byte aligned and their pitches below 2^23 elements. workspace must
+ * hold ak_lmhead_ce_workspace_bytes() bytes. logit[i, target[i]] is
+ * computed as its own fp32-accumulated dot product.
  */
 size_t ak_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab);
 int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targets,

@@ -45,7 +45,7 @@ def test_version_and_arch(lib):
 def test_workspace_query(lib):
     ws = _lib.lmhead_ce_workspace_bytes(8192, 50304)
     n_vt = (50304 + 255) // 256
-    assert ws >= n_vt * 8192 * 8 + 2 * 8192 * 4
+    assert ws >= n_vt * 8192 * 8 + 8192 * 4   # (max, sum) partials + per-row losses
     assert ws % 256 == 0
     assert _lib.lmhead_ce_workspace_bytes(0, 10) == 0
 
