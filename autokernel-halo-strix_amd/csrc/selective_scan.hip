@@ -16,8 +16,10 @@
 // from the lane that loaded them through DPP row_newbcast fused into those
 // multiplies. The output reduction over states goes through a padded LDS
 // transpose every 16 steps: lane (c, j) then owns step j of channel c and
-// folds h[n] * C[n] with 16 FMAs. B and C are staged per 64-step tile in LDS
-// as fp32, converted once per workgroup. exp uses exp2 with A pre-scaled by
+// folds h[n] * C[n] with 16 FMAs, one block later than the recurrence so
+// that the transpose's LDS latency is hidden. B and C are staged per 64-step
+// tile in LDS as fp32, converted once per workgroup; each lane reads its
+// state's 64 B values once per tile. exp uses exp2 with A pre-scaled by
 // log2(e), like the reference kernel (selective_scan_fwd_kernel.cuh:173-177).
 #include "ak_common.h"
 
@@ -47,26 +49,17 @@ struct ScanParams {
   int softplus;
 };
 
-// Broadcast lane k of each 16-lane row (DPP row_newbcast:k).
-__device__ __forceinline__ float row_bcast(float v, int k) {
-  switch (k) {
-    case 0: return dpp<0x150>(v);
-    case 1: return dpp<0x151>(v);
-    case 2: return dpp<0x152>(v);
-    case 3: return dpp<0x153>(v);
-    case 4: return dpp<0x154>(v);
-    case 5: return dpp<0x155>(v);
-    case 6: return dpp<0x156>(v);
-    case 7: return dpp<0x157>(v);
-    case 8: return dpp<0x158>(v);
-    case 9: return dpp<0x159>(v);
-    case 10: return dpp<0x15A>(v);
-    case 11: return dpp<0x15B>(v);
-    case 12: return dpp<0x15C>(v);
-    case 13: return dpp<0x15D>(v);
-    case 14: return dpp<0x15E>(v);
-    default: return dpp<0x15F>(v);
-  }
+// v * m, with v taken from lane K of each 16-lane row (DPP row_newbcast:K
+// fused into the multiply). The DPP source must not have been written by a
+// VALU instruction in the two preceding cycles; callers write it once per
+// tile and separate that write from the first use with an s_nop 1.
+template <int K>
+__device__ __forceinline__ float mul_bcast(float v, float m) {
+  float r;
+  asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+               : "=v"(r)
+               : "v"(v), "v"(m), "i"(K));
+  return r;
 }
 
 __device__ __forceinline__ float softplus_f32(float x) {
@@ -78,11 +71,6 @@ __device__ __forceinline__ float softplus_f32(float x) {
 // 1 ulp each), evaluated once per output element.
 __device__ __forceinline__ float silu_fast(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
-}
-
-template <typename T>
-__device__ __forceinline__ float ld(const void* p, int64_t i) {
-  return to_f32(static_cast<const T*>(p)[i]);
 }
 
 template <typename TU, typename TD, typename TBC>
@@ -122,34 +110,58 @@ mamba_scan_fwd_kernel(ScanParams p) {
   float* hb = hbuf[wave];
 
   // Global loads for one 64-step tile, issued one tile ahead of their use so
-  // that their latency hides behind the previous tile's recurrence.
+  // that their latency hides behind the previous tile's recurrence. They
+  // load from clamped, always-valid addresses without conditions and keep
+  // the storage type: masking and conversion to fp32 happen at the use, a
+  // tile later (a conditional or converting load would have to wait for its
+  // data right away).
   struct TileRegs {
-    float bv[4], cv[4];  // B / C staging: state sn, steps 4q..4q+3
-    float dv[4], uv[4];  // this lane's broadcast steps 4n..4n+3
-    float uo[4], zo[4];  // output steps 16*blk + n, blk = 0..3
+    TBC bv[4], cv[4];  // B / C staging: state sn, steps 4q..4q+3
+    TD dv[4];          // this lane's broadcast steps 4n..4n+3
+    TU uv[4];
+    TU uo[4], zo[4];   // output steps 16*blk + n, blk = 0..3
   };
   const int sn = tid / 16, q = tid % 16;
+  const int sn_c = min(sn, p.dstate - 1);
+  const int last_l = p.seqlen - 1;
+  // without z the gate loads read u instead (unused)
+  const TU* const zsrc = static_cast<const TU*>(p.z ? p.z : p.u);
+  const int64_t zrow = p.z ? z_row : u_row;
   auto load_tile = [&](int l0, TileRegs& r) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int l = l0 + 4 * q + k;
-      const bool ok = sn < p.dstate && l < p.seqlen;
-      r.bv[k] = ok ? ld<TBC>(p.B, B_base + (int64_t)sn * p.B_ns + l) : 0.0f;
-      r.cv[k] = ok ? ld<TBC>(p.C, C_base + (int64_t)sn * p.C_ns + l) : 0.0f;
+      const int l = min(l0 + 4 * q + k, last_l);
+      r.bv[k] = static_cast<const TBC*>(p.B)[B_base + (int64_t)sn_c * p.B_ns + l];
+      r.cv[k] = static_cast<const TBC*>(p.C)[C_base + (int64_t)sn_c * p.C_ns + l];
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int l = l0 + 4 * n + k;
-      const bool ok = ch_ok && l < p.seqlen;
-      r.dv[k] = ok ? ld<TD>(p.delta, d_row + l) : 0.0f;
-      r.uv[k] = ok ? ld<TU>(p.u, u_row + l) : 0.0f;
+      const int l = min(l0 + 4 * n + k, last_l);
+      r.dv[k] = static_cast<const TD*>(p.delta)[d_row + l];
+      r.uv[k] = static_cast<const TU*>(p.u)[u_row + l];
     }
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
-      const int l = l0 + 16 * blk + n;
-      const bool ok = ch_ok && l < p.seqlen;
-      r.uo[blk] = ok ? ld<TU>(p.u, u_row + l) : 0.0f;
-      r.zo[blk] = (ok && p.z) ? ld<TU>(p.z, z_row + l) : 0.0f;
+      const int l = min(l0 + 16 * blk + n, last_l);
+      r.uo[blk] = static_cast<const TU*>(p.u)[u_row + l];
+      r.zo[blk] = zsrc[zrow + l];
+    }
+  };
+
+  // The output reduction of a 16-step block runs one block late: its
+  // transpose reads are issued right after the states are written and are
+  // consumed after the next block's recurrence, which hides their latency.
+  float ph[16] = {}, pc[16] = {};  // pending block: h[c][j][0..15] and C[j][0..15]
+  float p_uo = 0.0f, p_zo = 0.0f;
+  int p_l = -1;              // pending output step (-1: none)
+  auto finish_pending = [&]() {
+    float y = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) y = fmaf(ph[s], pc[s], y);
+    if (ch_ok && p_l >= 0 && p_l < p.seqlen) {
+      float o = fmaf(dskip, p_uo, y);
+      if (p.z) o *= silu_fast(p_zo);
+      static_cast<TU*>(p.out)[o_row + p_l] = from_f32<TU>(o);
     }
   };
 
@@ -159,57 +171,98 @@ mamba_scan_fwd_kernel(ScanParams p) {
     __syncthreads();  // previous tile's readers of Bs / Cs are done
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      Bs[sn * kBStride + 4 * q + k] = cur.bv[k];
-      Cs[(4 * q + k) * kCStride + sn] = cur.cv[k];
+      const bool ok = sn < p.dstate && l0 + 4 * q + k < p.seqlen;
+      Bs[sn * kBStride + 4 * q + k] = ok ? to_f32(cur.bv[k]) : 0.0f;
+      Cs[(4 * q + k) * kCStride + sn] = ok ? to_f32(cur.cv[k]) : 0.0f;
     }
     float dl[4], du[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const bool ok = ch_ok && l0 + 4 * n + k < p.seqlen;
-      float dv = cur.dv[k] + dbias;
+      float dv = to_f32(cur.dv[k]) + dbias;
       if (p.softplus) dv = softplus_f32(dv);
       dl[k] = ok ? dv : 0.0f;
-      du[k] = dl[k] * cur.uv[k];
+      du[k] = dl[k] * to_f32(cur.uv[k]);
     }
+    // wait states between the last VALU write of dl / du and their DPP reads
+    asm volatile("s_nop 1"
+                 : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
+                   "+v"(du[2]), "+v"(du[3]));
     if (l0 + kScanT < p.seqlen) load_tile(l0 + kScanT, nxt);
+    // keep the compiler from sinking the prefetch towards its use
+    asm volatile("" ::: "memory");
     __syncthreads();
+    // B[n][l0 .. l0 + 63] of this lane's state, read once per tile
+    float bt[kScanT];
+#pragma unroll
+    for (int l = 0; l < kScanT; ++l) bt[l] = Bs[n * kBStride + l];
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
       float hv[16];
+      // Steps 16 blk + 4 j4 + k come from lane src = 4 blk + j4 of the row.
+      // All decay factors and inputs of the block are formed first (they do
+      // not depend on h), then the 16-step FMA chain runs; this keeps the
+      // exp results away from their uses (no hazard wait states).
+      float av[16], xv[16];
+      auto steps4 = [&](auto src_c, int j4) {
+        constexpr int kSrc = decltype(src_c)::value;
 #pragma unroll
-      for (int j4 = 0; j4 < 4; ++j4) {
-        const int src = blk * 4 + j4;  // lane in the row that owns these 4 steps
-        const float* brow = &Bs[n * kBStride + 16 * blk + 4 * j4];
-        const float bvals[4] = {brow[0], brow[1], brow[2], brow[3]};
+        for (int k = 0; k < 4; ++k) av[4 * j4 + k] = mul_bcast<kSrc>(dl[k], a_scaled);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float a = __builtin_amdgcn_exp2f(row_bcast(dl[k], src) * a_scaled);
-          const float x = row_bcast(du[k], src) * bvals[k];
-          h = fmaf(a, h, x);
-          hv[4 * j4 + k] = h;
-        }
+        for (int k = 0; k < 4; ++k)
+          xv[4 * j4 + k] = mul_bcast<kSrc>(du[k], bt[16 * blk + 4 * j4 + k]);
+      };
+      switch (blk) {
+        case 0:
+          steps4(std::integral_constant<int, 0>{}, 0); steps4(std::integral_constant<int, 1>{}, 1);
+          steps4(std::integral_constant<int, 2>{}, 2); steps4(std::integral_constant<int, 3>{}, 3);
+          break;
+        case 1:
+          steps4(std::integral_constant<int, 4>{}, 0); steps4(std::integral_constant<int, 5>{}, 1);
+          steps4(std::integral_constant<int, 6>{}, 2); steps4(std::integral_constant<int, 7>{}, 3);
+          break;
+        case 2:
+          steps4(std::integral_constant<int, 8>{}, 0); steps4(std::integral_constant<int, 9>{}, 1);
+          steps4(std::integral_constant<int, 10>{}, 2); steps4(std::integral_constant<int, 11>{}, 3);
+          break;
+        default:
+          steps4(std::integral_constant<int, 12>{}, 0); steps4(std::integral_constant<int, 13>{}, 1);
+          steps4(std::integral_constant<int, 14>{}, 2); steps4(std::integral_constant<int, 15>{}, 3);
+          break;
       }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) av[j] = __builtin_amdgcn_exp2f(av[j]);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        h = fmaf(av[j], h, xv[j]);
+        hv[j] = h;
+      }
+      // Order: this block's recurrence, then the previous block's output
+      // (whose transpose reads are by now complete), then this block's
+      // transpose. The empty asm statement (h must be final before it) and
+      // the scheduling barrier pin that order.
+      asm volatile("" : "+v"(h));
+      __builtin_amdgcn_sched_barrier(0);
+      finish_pending();  // previous block's output
       // Transpose through LDS: hbuf[c][j][n] = h at step j of this block.
 #pragma unroll
       for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
       __builtin_amdgcn_wave_barrier();
-      // Lane (c, j=n) now reduces step j of channel c over the 16 states.
-      const float* hrow = &hb[c * kHC + n * kHJ];
-      const float* crow = &Cs[(16 * blk + n) * kCStride];
-      float y = 0.0f;
+      // Lane (c, j=n) owns step j of channel c: its 16 states and C values.
 #pragma unroll
-      for (int s = 0; s < 16; ++s) y = fmaf(hrow[s], crow[s], y);
-      __builtin_amdgcn_wave_barrier();
-      const int l = l0 + 16 * blk + n;
-      if (ch_ok && l < p.seqlen) {
-        float o = fmaf(dskip, cur.uo[blk], y);
-        if (p.z) o *= silu_fast(cur.zo[blk]);
-        static_cast<TU*>(p.out)[o_row + l] = from_f32<TU>(o);
+      for (int s2 = 0; s2 < 16; ++s2) {
+        ph[s2] = hb[c * kHC + n * kHJ + s2];
+        pc[s2] = Cs[(16 * blk + n) * kCStride + s2];
       }
+      __builtin_amdgcn_wave_barrier();
+      p_uo = to_f32(cur.uo[blk]);
+      p_zo = p.z ? to_f32(cur.zo[blk]) : 0.0f;
+      p_l = l0 + 16 * blk + n;
     }
     cur = nxt;
   }
+  finish_pending();
   if (p.last_state && ch_ok && n_ok) {
     p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
   }
