@@ -414,13 +414,14 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
   __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 }
 
-// lse / per-token loss from the vocab-tile partials. A 1024-thread workgroup
-// owns 64 tokens. Its 16 waves first compute the target logits of 4 tokens
-// each (a wave-wide fp32 dot product over d), then each fold every 16th
-// partial (two per vocab tile) with an online (max, sum) merge (coalesced
-// 512-byte reads per wave); the 16 partial states are merged in a fixed
-// order through LDS (deterministic).
-constexpr int kRowsPerBlock = 64;
+// lse / per-token loss from the vocab-tile partials. A 512-thread workgroup
+// owns 32 tokens (8192 tokens give 256 workgroups, one per CU). Its 8 waves
+// first compute the target logits of 4 tokens each (a wave-wide fp32 dot
+// product over d), then 16 groups of 32 threads each fold every 16th partial
+// (two per vocab tile) with an online (max, sum) merge (coalesced 256-byte
+// reads); the 16 partial states are merged in a fixed order through LDS
+// (deterministic).
+constexpr int kRowsPerBlock = 32;
 constexpr int kRowGroups = 16;
 
 __device__ __forceinline__ MSPair ms_merge(MSPair a, MSPair b) {
@@ -438,7 +439,7 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
                       const MSPair* __restrict__ part, const int64_t* __restrict__ targets,
                       float* __restrict__ lse, float* __restrict__ losses, int n_rows, int vocab,
                       int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index) {
-  constexpr int kPerWave = kRowsPerBlock / kRowGroups;
+  constexpr int kPerWave = kRowsPerBlock / (kRowsPerBlock * kRowGroups / 64);  // tokens per wave
   __shared__ MSPair red[kRowGroups][kRowsPerBlock];
   __shared__ float tl[kRowsPerBlock];
   const int lane = threadIdx.x & 63;
@@ -460,8 +461,30 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
       wp[q] = W + (ok[q] ? t : 0) * ldw;
       acc[q] = 0.0f;
     }
+    // all loads of the first two 16-byte chunks per lane (d <= 1024) are
+    // issued before any FMA; longer rows continue in a loop
     const int d8 = d / 8;
-    for (int c = lane; c < d8; c += 64) {
+    Vec16<T> a0[kPerWave], b0[kPerWave], a1[kPerWave], b1[kPerWave];
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      const int c0 = min(lane, d8 - 1), c1 = min(lane + 64, d8 - 1);
+      a0[q] = load16<T>(hp[q] + 8 * c0);
+      b0[q] = load16<T>(wp[q] + 8 * c0);
+      a1[q] = load16<T>(hp[q] + 8 * c1);
+      b1[q] = load16<T>(wp[q] + 8 * c1);
+    }
+#pragma unroll
+    for (int q = 0; q < kPerWave; ++q) {
+      if (ok[q] && lane < d8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q] = fmaf(to_f32(a0[q].e[e]), to_f32(b0[q].e[e]), acc[q]);
+      }
+      if (ok[q] && lane + 64 < d8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q] = fmaf(to_f32(a1[q].e[e]), to_f32(b1[q].e[e]), acc[q]);
+      }
+    }
+    for (int c = lane + 128; c < d8; c += 64) {
 #pragma unroll
       for (int q = 0; q < kPerWave; ++q) {
         if (!ok[q]) continue;
@@ -483,8 +506,19 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
   const int row = row0 + r;
   MSPair st{-INFINITY, 0.0f};
   if (row < n_rows) {
-#pragma unroll 4
-    for (int v = grp; v < 2 * n_vt; v += kRowGroups) st = ms_merge(st, part[(int64_t)v * n_rows + row]);
+    // 8 partials in flight per thread, then merged in order
+    const int n_part = 2 * n_vt;
+    for (int v0 = grp; v0 < n_part; v0 += 8 * kRowGroups) {
+      MSPair buf[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int v = min(v0 + i * kRowGroups, n_part - 1);
+        buf[i] = part[(int64_t)v * n_rows + row];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (v0 + i * kRowGroups < n_part) st = ms_merge(st, buf[i]);
+    }
   }
   red[grp][r] = st;
   __syncthreads();
