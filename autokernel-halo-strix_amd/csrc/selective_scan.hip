@@ -268,6 +268,285 @@ mamba_scan_fwd_kernel(ScanParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: seqlen a multiple of 64, channels per group a multiple of 16,
+// 4-element (8- or 16-byte) aligned rows, every per-workgroup extent below
+// 2 GiB (checked on the host). Same lane decomposition and arithmetic as
+// mamba_scan_fwd_kernel, with
+// * buffer loads and stores through wave-uniform resources whose base is the
+//   workgroup's first channel: per-lane 32-bit offsets are fixed for the
+//   whole scan and the tile offset rides in the scalar offset, so no address
+//   arithmetic runs per tile; delta and u come in one 8/16-byte load per
+//   lane and tile, B and C in one each per thread;
+// * B / C staging double-buffered in LDS with one workgroup barrier per
+//   tile: tile t + 1 is written while tile t is read, from registers loaded
+//   a tile earlier;
+// * the output dot product split into four independent FMA chains;
+// * softplus chosen at compile time (as a run-time branch the compiler
+//   if-converts it and evaluates log1p(exp(x)) on every tile).
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+// Raw bits of 4 consecutive elements of T.
+template <typename T>
+using Raw4 = std::conditional_t<sizeof(T) == 4, u32x4, u32x2>;
+// Raw bits of one element of T.
+template <typename T>
+using Raw1 = std::conditional_t<sizeof(T) == 4, uint32_t, uint16_t>;
+
+// Buffer resource over `bytes` bytes at `base` (raw, unswizzled; gfx9 data
+// format field as used for untyped buffer access).
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <typename T>
+__device__ __forceinline__ Raw4<T> bload4(Rsrc r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 4)
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ Raw1<T> bload1(Rsrc r, uint32_t voff, uint32_t soff) {
+  if constexpr (sizeof(T) == 4)
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+  else
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float raw_f32(Raw1<T> v) {
+  return to_f32(__builtin_bit_cast(T, v));
+}
+
+// Element k (compile-time after unrolling) of a Raw4 as fp32.
+template <typename T>
+__device__ __forceinline__ float raw4_f32(const Raw4<T>& v, int k) {
+  if constexpr (sizeof(T) == 4) {
+    // the element goes through a scalar first: hipcc (ROCm 7.2) folds a
+    // __builtin_bit_cast of an ext_vector element to element 0 for every k
+    const uint32_t w = v[k];
+    return __builtin_bit_cast(float, w);
+  } else {
+    const uint32_t w = v[k >> 1];
+    return raw_f32<T>((uint16_t)((k & 1) ? (w >> 16) : (w & 0xFFFFu)));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void bstore1(Rsrc r, uint32_t voff, float v) {
+  if constexpr (sizeof(T) == 4)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, 0, 0);
+  else
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, (int)voff, 0, 0);
+}
+
+template <typename TU, typename TD, typename TBC, bool kSoftplus>
+__global__ void __launch_bounds__(256)
+mamba_scan_fast_kernel(ScanParams p) {
+  __shared__ float Bs[2][16 * kBStride];
+  __shared__ float Cs[2][kScanT * kCStride];
+  __shared__ float hbuf[4][4 * kHC];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int c = lane / 16;  // channel within the wave
+  const int n = lane % 16;  // state owned by this lane
+
+  const int per_batch = p.ngroups * p.tiles_per_group;
+  const int b = blockIdx.x / per_batch;
+  const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
+  const int tile = blockIdx.x % p.tiles_per_group;
+  const int d0 = g * p.ch_per_group + tile * kScanCh;  // first channel of the workgroup
+  const int wc = wave * 4 + c;                          // channel within the workgroup
+  const int d = d0 + wc;
+  const bool n_ok = n < p.dstate;
+
+  const float a_scaled = n_ok ? p.A[(int64_t)d * p.A_ds + n] * kLog2e : 0.0f;
+  const float dbias = p.delta_bias ? p.delta_bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+
+  // Wave-uniform resources over the workgroup's 16 channels (rows) and over
+  // its group's B / C rows.
+  const uint32_t L = (uint32_t)p.seqlen;
+  auto row_rsrc = [&](const void* base, int64_t bs, int64_t ds, int esz) {
+    const char* q = static_cast<const char*>(base) + ((int64_t)b * bs + (int64_t)d0 * ds) * esz;
+    return make_rsrc(q, (uint32_t)(((kScanCh - 1) * ds + L) * esz));
+  };
+  const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
+  const Rsrc rs_d = row_rsrc(p.delta, p.d_bs, p.d_ds, sizeof(TD));
+  const Rsrc rs_z = p.z ? row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU)) : rs_u;
+  const int64_t zds = p.z ? p.z_ds : p.u_ds;
+  const Rsrc rs_o = row_rsrc(p.out, p.o_bs, p.o_ds, sizeof(TU));
+  const uint32_t bc_bytes_B = (uint32_t)(((p.dstate - 1) * p.B_ns + L) * sizeof(TBC));
+  const uint32_t bc_bytes_C = (uint32_t)(((p.dstate - 1) * p.C_ns + L) * sizeof(TBC));
+  const Rsrc rs_B = make_rsrc(static_cast<const TBC*>(p.B) + (int64_t)b * p.B_bs + (int64_t)g * p.B_gs, bc_bytes_B);
+  const Rsrc rs_C = make_rsrc(static_cast<const TBC*>(p.C) + (int64_t)b * p.C_bs + (int64_t)g * p.C_gs, bc_bytes_C);
+
+  // Per-lane byte offsets, fixed for the whole scan.
+  const uint32_t vo_d4 = (uint32_t)(wc * p.d_ds + 4 * n) * sizeof(TD);   // delta, steps 4n..4n+3
+  const uint32_t vo_u4 = (uint32_t)(wc * p.u_ds + 4 * n) * sizeof(TU);   // u, steps 4n..4n+3
+  const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);       // u, step 16 blk + n
+  const uint32_t vo_z1 = (uint32_t)(wc * zds + n) * sizeof(TU);
+  const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);
+  const int sn = tid / 16, q = tid % 16;  // staging: state sn, steps 4q..4q+3
+  const int sn_c = min(sn, p.dstate - 1);
+  const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
+  const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
+
+  struct Regs {
+    Raw4<TD> dv;
+    Raw4<TU> uv;
+    Raw1<TU> uo[4], zo[4];
+  };
+  struct Stage {
+    Raw4<TBC> bv, cv;
+  };
+  const int nt = p.seqlen / kScanT;
+  auto load_regs = [&](int t, Regs& r) {
+    const uint32_t l0 = (uint32_t)t * kScanT;
+    r.dv = bload4<TD>(rs_d, vo_d4, l0 * sizeof(TD));
+    r.uv = bload4<TU>(rs_u, vo_u4, l0 * sizeof(TU));
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      r.uo[blk] = bload1<TU>(rs_u, vo_u1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+      r.zo[blk] = bload1<TU>(rs_z, vo_z1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+    }
+  };
+  auto load_stage = [&](int t, Stage& s) {
+    const uint32_t l0 = (uint32_t)t * kScanT;
+    s.bv = bload4<TBC>(rs_B, vo_B, l0 * sizeof(TBC));
+    s.cv = bload4<TBC>(rs_C, vo_C, l0 * sizeof(TBC));
+  };
+  auto write_stage = [&](const Stage& s, int buf) {
+    const bool ok = sn < p.dstate;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      Bs[buf][sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(s.bv, k) : 0.0f;
+      Cs[buf][(4 * q + k) * kCStride + sn] = ok ? raw4_f32<TBC>(s.cv, k) : 0.0f;
+    }
+  };
+
+  float h = 0.0f;
+  float* hb = hbuf[wave];
+  float ph[16] = {}, pc[16] = {};  // pending block: h[c][j][0..15] and C[j][0..15]
+  float p_uo = 0.0f, p_zo = 0.0f;
+  uint32_t p_off = 0;     // byte offset of the pending output element
+  bool pending = false;   // wave-uniform
+  auto finish_pending = [&]() {
+    float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
+    float o = fmaf(dskip, p_uo, (y4[0] + y4[1]) + (y4[2] + y4[3]));
+    if (p.z) o *= silu_fast(p_zo);
+    bstore1<TU>(rs_o, p_off, o);
+  };
+
+  auto compute = [&](int t, const Regs& cur) {
+    const int buf = t & 1;
+    float dl[4], du[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float dv = raw4_f32<TD>(cur.dv, k) + dbias;
+      if constexpr (kSoftplus) dv = softplus_f32(dv);
+      dl[k] = dv;
+      du[k] = dv * raw4_f32<TU>(cur.uv, k);
+    }
+    // wait states between the last VALU write of dl / du and their DPP reads
+    asm volatile("s_nop 1"
+                 : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
+                   "+v"(du[2]), "+v"(du[3]));
+    float bt[kScanT];
+#pragma unroll
+    for (int l = 0; l < kScanT; ++l) bt[l] = Bs[buf][n * kBStride + l];
+
+#pragma unroll
+    for (int blk = 0; blk < kScanT / 16; ++blk) {
+      float hv[16], av[16], xv[16];
+      auto steps4 = [&](auto src_c, int j4) {
+        constexpr int kSrc = decltype(src_c)::value;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) av[4 * j4 + k] = mul_bcast<kSrc>(dl[k], a_scaled);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          xv[4 * j4 + k] = mul_bcast<kSrc>(du[k], bt[16 * blk + 4 * j4 + k]);
+      };
+      switch (blk) {
+        case 0:
+          steps4(std::integral_constant<int, 0>{}, 0); steps4(std::integral_constant<int, 1>{}, 1);
+          steps4(std::integral_constant<int, 2>{}, 2); steps4(std::integral_constant<int, 3>{}, 3);
+          break;
+        case 1:
+          steps4(std::integral_constant<int, 4>{}, 0); steps4(std::integral_constant<int, 5>{}, 1);
+          steps4(std::integral_constant<int, 6>{}, 2); steps4(std::integral_constant<int, 7>{}, 3);
+          break;
+        case 2:
+          steps4(std::integral_constant<int, 8>{}, 0); steps4(std::integral_constant<int, 9>{}, 1);
+          steps4(std::integral_constant<int, 10>{}, 2); steps4(std::integral_constant<int, 11>{}, 3);
+          break;
+        default:
+          steps4(std::integral_constant<int, 12>{}, 0); steps4(std::integral_constant<int, 13>{}, 1);
+          steps4(std::integral_constant<int, 14>{}, 2); steps4(std::integral_constant<int, 15>{}, 3);
+          break;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) av[j] = __builtin_amdgcn_exp2f(av[j]);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        h = fmaf(av[j], h, xv[j]);
+        hv[j] = h;
+      }
+      asm volatile("" : "+v"(h));
+      __builtin_amdgcn_sched_barrier(0);
+      if (pending) finish_pending();  // previous block's output
+#pragma unroll
+      for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2) {
+        ph[s2] = hb[c * kHC + n * kHJ + s2];
+        pc[s2] = Cs[buf][(16 * blk + n) * kCStride + s2];
+      }
+      __builtin_amdgcn_wave_barrier();
+      p_uo = raw_f32<TU>(cur.uo[blk]);
+      p_zo = p.z ? raw_f32<TU>(cur.zo[blk]) : 0.0f;
+      p_off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
+      pending = true;
+    }
+  };
+
+  // One tile: publish tile t's staging (barrier), stage tile t + 1, issue
+  // the loads of tile t + 2's B / C and tile t + 1's delta / u / z (clamped
+  // to the last tile: unconditional loads of valid addresses), then compute.
+  Stage st;
+  auto tile_body = [&](int t, const Regs& cur, Regs& nxt) {
+    __syncthreads();
+    write_stage(st, (t + 1) & 1);
+    load_stage(min(t + 2, nt - 1), st);
+    load_regs(min(t + 1, nt - 1), nxt);
+    asm volatile("" ::: "memory");
+    compute(t, cur);
+  };
+
+  Regs ra, rb;
+  load_stage(0, st);
+  load_regs(0, ra);
+  write_stage(st, 0);
+  load_stage(min(1, nt - 1), st);
+  for (int t = 0; t < nt; t += 2) {
+    tile_body(t, ra, rb);
+    if (t + 1 < nt) tile_body(t + 1, rb, ra);
+  }
+  finish_pending();
+  if (p.last_state && n_ok) {
+    p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
+  }
+}
+
 // Diagonal recurrence over [batch, seqlen, d_inner] fp32, one lane per
 // (batch, channel); consecutive lanes read consecutive channels, so every
 // step is a coalesced 256-byte row segment per wave.
@@ -289,10 +568,41 @@ diag_scan_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
   }
 }
 
+// Whether the fast kernel's layout assumptions hold: whole 64-step tiles,
+// whole 16-channel workgroups, 4-element aligned rows for the vector loads,
+// and every buffer resource's extent (16 channel rows, or dstate B / C rows)
+// below 2 GiB.
+template <typename TU, typename TD, typename TBC>
+bool scan_fast_ok(const ScanParams& p) {
+  auto al4 = [](const void* ptr, int64_t s0, int64_t s1, int64_t s2, size_t esz) {
+    return (reinterpret_cast<uintptr_t>(ptr) % (4 * esz)) == 0 && s0 % 4 == 0 && s1 % 4 == 0 &&
+           s2 % 4 == 0;
+  };
+  auto fits = [&](int64_t rows, int64_t pitch, size_t esz) {
+    return pitch >= 0 && ((rows - 1) * pitch + p.seqlen) * (int64_t)esz < ((int64_t)1 << 31);
+  };
+  if (p.seqlen % kScanT != 0 || p.ch_per_group % kScanCh != 0) return false;
+  if (!al4(p.u, p.u_bs, p.u_ds, 0, sizeof(TU)) || !al4(p.delta, p.d_bs, p.d_ds, 0, sizeof(TD)))
+    return false;
+  if (!al4(p.B, p.B_bs, p.B_gs, p.B_ns, sizeof(TBC)) || !al4(p.C, p.C_bs, p.C_gs, p.C_ns, sizeof(TBC)))
+    return false;
+  if (p.u_bs < 0 || p.d_bs < 0 || p.o_bs < 0 || p.z_bs < 0 || p.B_bs < 0 || p.C_bs < 0 ||
+      p.B_gs < 0 || p.C_gs < 0)
+    return false;
+  return fits(kScanCh, p.u_ds, sizeof(TU)) && fits(kScanCh, p.d_ds, sizeof(TD)) &&
+         fits(kScanCh, p.o_ds, sizeof(TU)) && (!p.z || fits(kScanCh, p.z_ds, sizeof(TU))) &&
+         fits(p.dstate, p.B_ns, sizeof(TBC)) && fits(p.dstate, p.C_ns, sizeof(TBC));
+}
+
 template <typename TU, typename TD, typename TBC>
 void launch_scan(const ScanParams& p, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
-  mamba_scan_fwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
+  if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
+    mamba_scan_fast_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p))
+    mamba_scan_fast_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else
+    mamba_scan_fwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
 }
 
 template <typename TU>

@@ -80,6 +80,51 @@ def test_shapes_and_options(batch, dim, dstate, seqlen, groups):
         assert torch.allclose(out.float(), ref, rtol=3e-2, atol=5e-2)
 
 
+@pytest.mark.parametrize("batch,dim,dstate,seqlen,groups,itype", [
+    (2, 32, 16, 256, 1, "bfloat16"), (1, 64, 8, 512, 2, "float16"), (2, 16, 16, 128, 1, "float32"),
+    (3, 48, 5, 64, 3, "bfloat16"), (1, 32, 16, 2048, 2, "bfloat16")])
+def test_fast_path_shapes(batch, dim, dstate, seqlen, groups, itype):
+    """Shapes on the vectorised whole-tile kernel (seqlen % 64 == 0, 16 | dim / groups)."""
+    need_gpu()
+    dt = ITYPES[itype]
+    rtol, atol = GRID["tolerances"][itype]
+    u, delta, A, B, C, D, z, bias = _inputs(batch, dim, dstate, seqlen, groups, dt, 3 * dim + seqlen)
+    say("mamba fast path", batch, dim, dstate, seqlen, groups, itype)
+    for softplus, zz, DD, bb in ((True, z, D, bias), (False, None, None, None), (False, z, D, None)):
+        out, last = _gpu(u, delta, A, B, C, DD, zz, bb, softplus)
+        ref, rlast = c_oracle.selective_scan(u, delta, A, B, C, DD, zz, bb, softplus)
+        assert out.dtype == dt
+        assert torch.allclose(out.float(), ref, rtol=rtol, atol=atol)
+        assert torch.allclose(last, rlast, rtol=1e-4, atol=1e-4)
+    if groups == 1:
+        out = _gpu(u, delta.float(), A, B[:, 0], C[:, 0], D, z, bias, True, last=False)
+        ref, _ = c_oracle.selective_scan(u, delta.float(), A, B, C, D, z, bias, True)
+        assert torch.allclose(out.float(), ref, rtol=rtol, atol=atol)
+
+
+def test_fast_and_generic_paths_agree():
+    """The same scan through the whole-tile kernel (contiguous) and the generic
+    kernel (a view with a row pitch that is not a multiple of 4 elements)."""
+    need_gpu()
+    u, delta, A, B, C, D, z, bias = _inputs(2, 32, 16, 320, 1, torch.bfloat16, 31)
+    say("mamba fast vs generic")
+    from kernels.hip.selective_scan import selective_scan_fn
+    fast, lf = _gpu(u, delta, A, B, C, D, z, bias, True)
+    pad = torch.zeros(2, 32, 321, dtype=torch.bfloat16, device=DEV)
+    pad[..., :320] = u.to(DEV)
+    uv = pad[..., :320]
+    assert uv.stride(1) == 321
+    d = lambda t: t.to(DEV)
+    gen, lg = selective_scan_fn(uv, d(delta), d(A), d(B), d(C), d(D), d(z), d(bias), True, True)
+    gen, lg = gen.cpu(), lg.cpu()
+    ref, rl = c_oracle.selective_scan(u, delta, A, B, C, D, z, bias, True)
+    assert torch.allclose(fast.float(), ref, rtol=3e-2, atol=5e-2)
+    assert torch.allclose(gen.float(), ref, rtol=3e-2, atol=5e-2)
+    assert torch.allclose(lf, lg, rtol=1e-5, atol=1e-5)
+    # bf16 outputs of the two paths differ by at most one rounding step
+    assert ((fast.float() - gen.float()).abs() <= 2 ** -7 * fast.float().abs() + 1e-6).all()
+
+
 def test_c5_full_size():
     need_gpu()
     import bench
