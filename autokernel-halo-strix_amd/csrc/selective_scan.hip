@@ -393,7 +393,10 @@ mamba_scan_fast_kernel(ScanParams p) {
   const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);       // u, step 16 blk + n
   const uint32_t vo_z1 = (uint32_t)(wc * zds + n) * sizeof(TU);
   const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);
-  const int sn = tid / 16, q = tid % 16;  // staging: state sn, steps 4q..4q+3
+  // staging: state sn, steps 4q..4q+3; the 16 lanes of a row take 16
+  // different states, so the transposed Cs writes of a wave hit 64 distinct
+  // banks (with 16 lanes per state they conflicted 8-way)
+  const int sn = tid % 16, q = tid / 16;
   const int sn_c = min(sn, p.dstate - 1);
   const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
   const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
