@@ -45,6 +45,12 @@ _SIGNATURES = {
     "ak_rmsnorm_fwd": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
     "ak_fused_add_rmsnorm_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
                                  _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
+    "ak_rmsnorm_bwd_workspace_bytes": [_i64, _i64],
+    "ak_rmsnorm_bwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                       ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
+    "ak_fused_add_rmsnorm_bwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _f32, _int, _c_void_p],
     "ak_softmax_fwd": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
     "ak_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                   _i64, _i64, _i64, _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
@@ -61,6 +67,7 @@ _RESTYPES = {
     "ak_last_error": ctypes.c_char_p,
     "ak_target_arch": ctypes.c_char_p,
     "ak_lmhead_ce_workspace_bytes": ctypes.c_size_t,
+    "ak_rmsnorm_bwd_workspace_bytes": ctypes.c_size_t,
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -173,6 +180,44 @@ def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Ten
             _rows_view(x, "x"), _rows_view(residual, "residual"), ld_nr, _rows_view(y, "y"),
             float(eps), dtype_code(x.dtype), _stream(x))
     _check(rc, "ak_fused_add_rmsnorm_fwd")
+
+
+def rmsnorm_bwd_workspace_bytes(rows: int, cols: int) -> int:
+    return int(load().ak_rmsnorm_bwd_workspace_bytes(rows, cols))
+
+
+def rmsnorm_bwd(x: torch.Tensor, weight: torch.Tensor, grad_out: torch.Tensor,
+                grad_x: torch.Tensor, grad_weight: Optional[torch.Tensor],
+                workspace: Optional[torch.Tensor], eps: float) -> None:
+    """RMSNorm backward over 2-D ``[rows, cols]`` views; grad_weight fp32 ``[cols]``."""
+    require_device(x, weight, grad_out, grad_x, grad_weight, workspace)
+    rows, cols = x.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with torch.cuda.device(x.device):
+        rc = load().ak_rmsnorm_bwd(
+            _ptr(x), _ptr(weight), _ptr(grad_out), _ptr(grad_x), _ptr(grad_weight),
+            _ptr(workspace), ws_bytes, rows, cols, _rows_view(x, "x"),
+            _rows_view(grad_out, "grad_out"), _rows_view(grad_x, "grad_x"), float(eps),
+            dtype_code(x.dtype), _stream(x))
+    _check(rc, "ak_rmsnorm_bwd")
+
+
+def fused_add_rmsnorm_bwd(hidden: torch.Tensor, weight: torch.Tensor,
+                          grad_hidden: Optional[torch.Tensor], grad_normed: torch.Tensor,
+                          grad_x: torch.Tensor, grad_weight: Optional[torch.Tensor],
+                          workspace: Optional[torch.Tensor], eps: float) -> None:
+    """Fused residual + RMSNorm backward over 2-D views; grad_hidden may be None."""
+    require_device(hidden, weight, grad_hidden, grad_normed, grad_x, grad_weight, workspace)
+    rows, cols = hidden.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    ld_gh = _rows_view(grad_hidden, "grad_hidden") if grad_hidden is not None else cols
+    with torch.cuda.device(hidden.device):
+        rc = load().ak_fused_add_rmsnorm_bwd(
+            _ptr(hidden), _ptr(weight), _ptr(grad_hidden), _ptr(grad_normed), _ptr(grad_x),
+            _ptr(grad_weight), _ptr(workspace), ws_bytes, rows, cols,
+            _rows_view(hidden, "hidden"), ld_gh, _rows_view(grad_normed, "grad_normed"),
+            _rows_view(grad_x, "grad_x"), float(eps), dtype_code(hidden.dtype), _stream(hidden))
+    _check(rc, "ak_fused_add_rmsnorm_bwd")
 
 
 def softmax(x: torch.Tensor, y: torch.Tensor) -> None:

@@ -11,12 +11,15 @@ Same op names and schemas as the reference (``kernels/hip/_torch_ops.py``):
 
 The trailing ``eps`` (default 1e-6, the reference's fixed value) is an
 addition, so reference call sites are unchanged. Each op has ``register_fake`` (shape propagation for torch.compile) and
-``register_autograd``. The forwards run the gfx950 kernels; the backwards are
-PyTorch formulas in fp32 on the GPU: for the norms the gradient the
-reference's HIP backward kernels compute (``rmsnorm_backward.py:166-168``,
-``fused_residual_rmsnorm_backward.py:168-170``), for the diagonal scan the
-reference's sequential formula (``_torch_ops.py:346-386``). Importing this
-module registers the ops.
+``register_autograd``. The forwards run the gfx950 kernels. The norm
+backwards run the gfx950 backward kernels (``kernels.hip.rmsnorm_backward``,
+``kernels.hip.fused_residual_rmsnorm_backward``), as the reference did for
+fp16 (``_torch_ops.py:77-80``, ``:266-271``); ``AUTOKERNEL_NO_BWD_HIP=1``
+selects the same gradient as fp32 PyTorch formulas on the GPU instead (the
+gradient of ``rmsnorm_backward.py:166-168`` /
+``fused_residual_rmsnorm_backward.py:168-170``). The diagonal scan's backward
+is the reference's sequential formula (``_torch_ops.py:346-386``). Importing
+this module registers the ops.
 
 Autocast: under ``torch.autocast("cuda", dtype=...)`` floating inputs are
 cast to the active autocast dtype (fp16 or bf16) before the kernel runs.
@@ -30,15 +33,26 @@ from typing import Tuple
 
 import torch
 
-# Set AUTOKERNEL_NO_BWD_HIP=1 to force the PyTorch backward formulas (kept for
-# API compatibility: the backward passes here are PyTorch formulas already).
+# AUTOKERNEL_NO_BWD_HIP=1 selects the fp32 PyTorch formulas for the norm
+# backwards instead of the gfx950 backward kernels (reference
+# _torch_ops.py:20-50).
 _USE_BWD_HIP = os.environ.get("AUTOKERNEL_NO_BWD_HIP", "0") != "1"
 
 RMSNORM_EPS = 1e-6
 
 
 def _use_hip_backward():
-    return False
+    """Whether the norm backwards run the gfx950 kernels: not when disabled,
+    and not while torch.compile traces (the formulas are traceable, the
+    library calls are not), as in the reference (_torch_ops.py:24-38)."""
+    if not _USE_BWD_HIP:
+        return False
+    try:
+        if torch.compiler.is_compiling():
+            return False
+    except AttributeError:
+        pass
+    return True
 
 
 def disable_hip_backward():
@@ -85,6 +99,10 @@ def _rmsnorm_setup(ctx, inputs, output):
 def _rmsnorm_backward(ctx, grad_output):
     x, weight = ctx.saved_tensors
     eps = ctx.eps
+    if _use_hip_backward() and x.is_cuda:
+        from kernels.hip.rmsnorm_backward import kernel_fn as rmsnorm_bwd_fn
+        grad_x, grad_weight = rmsnorm_bwd_fn(x, weight, grad_output, eps)
+        return grad_x, grad_weight.to(weight.dtype), None
     x_f = x.float()
     w_f = weight.float()
     g_f = grad_output.float()
@@ -130,6 +148,13 @@ def _fused_res_rmsnorm_setup(ctx, inputs, output):
 def _fused_res_rmsnorm_backward(ctx, grad_hidden, grad_normed):
     hidden, weight = ctx.saved_tensors
     eps = ctx.eps
+    if _use_hip_backward() and hidden.is_cuda and grad_normed is not None:
+        from kernels.hip.fused_residual_rmsnorm_backward import kernel_fn as fused_bwd_fn
+        grad_x, _, grad_weight = fused_bwd_fn(hidden, weight, grad_hidden, grad_normed, eps)
+        return grad_x, grad_x, grad_weight.to(weight.dtype), None
+    if grad_normed is None:
+        gx = grad_hidden.to(hidden.dtype)
+        return gx, gx, torch.zeros_like(weight), None
     h_f = hidden.float()
     w_f = weight.float()
     gn_f = grad_normed.float()

@@ -113,6 +113,9 @@ def gen_c5(b=4, d=2048, l=4096, n=16):
 C1_BYTES = 2048 * 768 * 4 * 2 + 768 * 4
 C2_BYTES = 2 * 8 * 12 * 1024 * 1024 * 2
 C3_BYTES = 4 * 16384 * 4096 * 2 + 4096 * 2
+# fused residual + RMSNorm backward at the C3 shape: read hidden, grad_hidden,
+# grad_normed, weight; write grad_x and the fp32 weight gradient
+C3B_BYTES = 4 * 16384 * 4096 * 2 + 4096 * 2 + 4096 * 4
 C4_FLOP = 2 * 8192 * 50304 * 768
 C4_MIN_BYTES = 8192 * 768 * 2 + 50304 * 768 * 2 + 8192 * 8 + 8192 * 4 + 4
 C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2 + 2048 * 16 * 4 + 2048 * 4
@@ -173,6 +176,23 @@ def make_case(name):
         launch = lambda s: _lib.fused_add_rmsnorm(s["x"], s["r"], s["w"], s["nr"], s["y"], s["eps"])
         return Case(name, "C3 fused residual + RMSNorm bf16 [16384, 4096]", "hbm", C3_BYTES, 16384,
                     launch, sets, "rownorm_vec_kernel")
+    if name == "c3b":
+        c = gen_c3()
+        g = torch.Generator().manual_seed(1)
+        cpu = {"h": (c["x"] + c["r"]), "w": c["w"],
+               "gh": torch.randn(16384, 4096, generator=g).bfloat16(),
+               "gn": torch.randn(16384, 4096, generator=g).bfloat16(), "eps": c["eps"]}
+        k = _sets(C3B_BYTES)
+        sets = _replicate(cpu, k)
+        wsb = _lib.rmsnorm_bwd_workspace_bytes(16384, 4096)
+        for s in sets:
+            s["gx"] = torch.empty_like(s["h"])
+            s["gw"] = torch.empty(4096, dtype=torch.float32, device="cuda")
+            s["ws"] = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        launch = lambda s: _lib.fused_add_rmsnorm_bwd(s["h"], s["w"], s["gh"], s["gn"], s["gx"],
+                                                      s["gw"], s["ws"], s["eps"])
+        return Case(name, "C3-shape fused residual + RMSNorm backward bf16 [16384, 4096]", "hbm",
+                    C3B_BYTES, 16384, launch, sets, "rownorm_bwd_vec_kernel")
     if name == "c4":
         cpu = gen_c4()
         sets = _replicate(cpu, 2)
@@ -250,6 +270,14 @@ def cpu_baseline(name, budget_s=4.0):
         c = gen_c3(rows=1024)
         t = timed(lambda: ops.fused_residual_add_rmsnorm_ref(c["x"], c["r"], c["w"], c["eps"]), 5)
         return C3_BYTES * (1024 / 16384) / t / 1e9, "GB/s", "1024 of 16384 rows of C3"
+    if name == "c3b":
+        c = gen_c3(rows=1024)
+        g = torch.Generator().manual_seed(1)
+        h = c["x"] + c["r"]
+        gh = torch.randn(1024, 4096, generator=g).bfloat16()
+        gn = torch.randn(1024, 4096, generator=g).bfloat16()
+        t = timed(lambda: ops.fused_residual_rmsnorm_bwd_ref(h, c["w"], gh, gn, c["eps"]), 5)
+        return C3B_BYTES * (1024 / 16384) / t / 1e9, "GB/s", "1024 of 16384 rows of the C3-shape backward (float64 oracle)"
     if name == "c4":
         c = gen_c4()
         rows = 64
@@ -272,7 +300,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "

@@ -74,6 +74,42 @@ int ak_fused_add_rmsnorm_fwd(const void* x, const void* residual, const void* we
                              float eps, int dtype, void* stream);
 
 /*
+ * RMSNorm backward, per row in fp32 (x the forward input):
+ *   r = 1 / sqrt(mean(x^2) + eps),  n = x * r,  g = grad_out * weight
+ *   grad_x      = round_dtype(r * (g - n * sum(g * n) / cols))
+ *   grad_weight = sum over rows of grad_out * n           (fp32, [cols])
+ * Replaces kernels/hip/rmsnorm_backward.py:239-281 (kernel_fn) and its
+ * kernel :60-189 (which accumulated grad_weight with fp32 atomics); the
+ * row sums of grad_weight here run in a fixed order (deterministic).
+ * grad_weight may be NULL (then no workspace is needed); otherwise workspace
+ * must hold ak_rmsnorm_bwd_workspace_bytes(rows, cols) bytes, 16-byte
+ * aligned. x, weight, grad_out and grad_x share the element type dtype.
+ */
+size_t ak_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t cols);
+int ak_rmsnorm_bwd(const void* x, const void* weight, const void* grad_out,
+                   void* grad_x, float* grad_weight,
+                   void* workspace, size_t workspace_bytes,
+                   int64_t rows, int64_t cols,
+                   int64_t ld_x, int64_t ld_g, int64_t ld_gx,
+                   float eps, int dtype, void* stream);
+
+/*
+ * Fused residual add + RMSNorm backward: the RMSNorm backward above applied
+ * to the saved hidden state (x + residual) and grad_normed, plus grad_hidden:
+ *   grad_x = grad_residual = round_dtype(grad_hidden + r * (g - n * sum(g * n) / cols))
+ * with g = grad_normed * weight; grad_hidden may be NULL (treated as zero).
+ * Replaces kernels/hip/fused_residual_rmsnorm_backward.py:248-298
+ * (kernel_fn) and its kernel :61-197. Workspace as for ak_rmsnorm_bwd.
+ */
+int ak_fused_add_rmsnorm_bwd(const void* hidden, const void* weight,
+                             const void* grad_hidden, const void* grad_normed,
+                             void* grad_x, float* grad_weight,
+                             void* workspace, size_t workspace_bytes,
+                             int64_t rows, int64_t cols,
+                             int64_t ld_h, int64_t ld_gh, int64_t ld_gn, int64_t ld_gx,
+                             float eps, int dtype, void* stream);
+
+/*
  * Row softmax over the last dimension with fp32 accumulation.
  * Replaces kernels/hip/softmax.py:273-326 (softmax_hip); semantics of
  * reference.py:14-17 (softmax_ref). -inf entries give exact zeros.

@@ -56,6 +56,39 @@ def fused_residual_add_rmsnorm_ref(x: torch.Tensor, residual: torch.Tensor, weig
     return hidden, ((hf / rms) * weight.float()).to(x.dtype)
 
 
+def rmsnorm_bwd_ref(x: torch.Tensor, weight: torch.Tensor, grad_out: torch.Tensor,
+                    eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm backward in float64 (unrounded), the gradient of
+    ``kernels/hip/rmsnorm_backward.py:60-189`` (formula at :166-168):
+
+        r = 1 / sqrt(mean(x^2) + eps), n = x * r, g = grad_out * weight
+        grad_x = r * (g - n * sum(g * n) / D),  grad_weight = sum_rows(grad_out * n)
+
+    Returns ``(grad_x, grad_weight)`` as float64 with ``x``'s shape and ``(D,)``.
+    """
+    xd, wd, gd = x.double(), weight.double(), grad_out.double()
+    r = 1.0 / torch.sqrt(torch.mean(xd * xd, dim=-1, keepdim=True) + eps)
+    n = xd * r
+    g = gd * wd
+    D = x.shape[-1]
+    grad_x = r * (g - n * (g * n).sum(-1, keepdim=True) / D)
+    grad_w = (gd * n).reshape(-1, D).sum(0)
+    return grad_x, grad_w
+
+
+def fused_residual_rmsnorm_bwd_ref(hidden: torch.Tensor, weight: torch.Tensor,
+                                   grad_hidden: Optional[torch.Tensor], grad_normed: torch.Tensor,
+                                   eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fused residual + RMSNorm backward in float64 (unrounded), following
+    ``kernels/hip/fused_residual_rmsnorm_backward.py:61-197`` (:168-178):
+    grad_x = grad_residual = grad_hidden + RMSNorm-backward(hidden, grad_normed).
+    Returns ``(grad_x, grad_weight)``."""
+    gx, gw = rmsnorm_bwd_ref(hidden, weight, grad_normed, eps)
+    if grad_hidden is not None:
+        gx = gx + grad_hidden.double()
+    return gx, gw
+
+
 # ---------------------------------------------------------------------------
 # Softmax
 # ---------------------------------------------------------------------------

@@ -27,6 +27,20 @@ def _fused(x, r, w, nr, y, eps):
     y.copy_(out)
 
 
+def _rmsnorm_bwd(x, w, g, gx, gw, ws, eps):
+    a, b = ops.rmsnorm_bwd_ref(x, w, g, eps)
+    gx.copy_(a.to(gx.dtype))
+    if gw is not None:
+        gw.copy_(b.float())
+
+
+def _fused_bwd(h, w, gh, gn, gx, gw, ws, eps):
+    a, b = ops.fused_residual_rmsnorm_bwd_ref(h, w, gh, gn, eps)
+    gx.copy_(a.to(gx.dtype))
+    if gw is not None:
+        gw.copy_(b.float())
+
+
 def _softmax(x, y):
     y.copy_(ops.softmax_ref(x))
 
@@ -102,6 +116,9 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "require_device", lambda *tensors: None)
     monkeypatch.setattr(_lib, "rmsnorm", _rmsnorm)
     monkeypatch.setattr(_lib, "fused_add_rmsnorm", _fused)
+    monkeypatch.setattr(_lib, "rmsnorm_bwd", _rmsnorm_bwd)
+    monkeypatch.setattr(_lib, "fused_add_rmsnorm_bwd", _fused_bwd)
+    monkeypatch.setattr(_lib, "rmsnorm_bwd_workspace_bytes", lambda rows, cols: 256)
     monkeypatch.setattr(_lib, "softmax", _softmax)
     monkeypatch.setattr(_lib, "ce_fwd", _ce_fwd)
     monkeypatch.setattr(_lib, "ce_bwd_tiny", _ce_bwd_tiny)

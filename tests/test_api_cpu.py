@@ -50,6 +50,34 @@ def test_kernel_fns_shapes_and_dtypes(fake_backend):
         frn.kernel_fn(x, r[:, :2], w)
 
 
+def test_norm_backward_modules(fake_backend):
+    """kernels.hip.rmsnorm_backward / fused_residual_rmsnorm_backward: the
+    reference's kernel_fn signatures and return contracts (grad_weight fp32;
+    the fused form returns grad_x twice)."""
+    from kernels.hip import fused_residual_rmsnorm_backward as frb
+    from kernels.hip import rmsnorm_backward as rb
+    assert rb.KERNEL_TYPE == "rmsnorm_backward" and frb.KERNEL_TYPE == "fused_residual_rmsnorm_backward"
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 3, 64, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(64, generator=g))
+    dy = torch.randn(2, 3, 64, generator=g).bfloat16()
+    gx, gw = rb.kernel_fn(x, w, dy)
+    assert gx.shape == x.shape and gx.dtype == x.dtype and gw.dtype == torch.float32 and gw.shape == (64,)
+    ref_x, ref_w = ops.rmsnorm_bwd_ref(x, w.bfloat16(), dy, 1e-6)
+    assert torch.equal(gx, ref_x.bfloat16()) and torch.allclose(gw.double(), ref_w, rtol=1e-6)
+    gh = torch.randn(2, 3, 64, generator=g).bfloat16()
+    a, b, c = frb.kernel_fn(x, w, gh, dy, eps=1e-5)
+    assert a is b and c.dtype == torch.float32
+    rx, _ = ops.fused_residual_rmsnorm_bwd_ref(x, w.bfloat16(), gh, dy, 1e-5)
+    assert torch.equal(a, rx.bfloat16())
+    a0, _, _ = frb.kernel_fn(x, w, None, dy)
+    assert torch.equal(a0, ops.rmsnorm_bwd_ref(x, w.bfloat16(), dy)[0].bfloat16())
+    with pytest.raises(ValueError):
+        rb.kernel_fn(x, w, dy[:, :2])
+    with pytest.raises(ValueError):
+        frb.kernel_fn(x, torch.ones(63), gh, dy)
+
+
 def test_ce_fused_module_api(fake_backend):
     import kernel
     from kernels import ce_fused

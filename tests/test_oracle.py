@@ -67,6 +67,73 @@ def test_rmsnorm_brute_force_f64():
             assert abs(float(y[i, j]) - float(x[i, j]) / math.sqrt(ms + 1e-6) * float(w[j])) < 1e-5
 
 
+@pytest.mark.parametrize("eps", [1e-6, 1e-5, 0.3])
+def test_rmsnorm_bwd_matches_autograd(eps):
+    """The oracle's backward equals torch autograd of the float64 forward
+    (reference.py:25-29); the reference's own PyTorch fallback formula
+    (_torch_ops.py:95, which drops one factor of 1/rms in the projection
+    term) does not."""
+    g = torch.Generator().manual_seed(11)
+    x = (3 * torch.randn(6, 40, generator=g)).double().requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(40, generator=g)).double().requires_grad_(True)
+    dy = torch.randn(6, 40, generator=g).double()
+    ops.rmsnorm_ref(x, w, eps).backward(dy)
+    gx, gw = ops.rmsnorm_bwd_ref(x.detach(), w.detach(), dy, eps)
+    assert torch.allclose(gx, x.grad, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(gw, w.grad, rtol=1e-12, atol=1e-12)
+    # the fallback formula of the reference's _torch_ops.py:95
+    xd = x.detach()
+    r = (xd.pow(2).mean(-1, keepdim=True) + eps).rsqrt()
+    n = xd * r
+    gn = dy * w.detach()
+    wrong = gn * r - n * (gn * n).sum(-1, keepdim=True) / 40
+    assert not torch.allclose(wrong, x.grad, rtol=1e-3, atol=1e-3)
+
+
+def test_rmsnorm_bwd_closed_forms():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(5, 64, generator=g).double()
+    w = torch.randn(64, generator=g).double()
+    dy = torch.randn(5, 64, generator=g).double()
+    gx, gw = ops.rmsnorm_bwd_ref(x, w, dy, 0.0)
+    # zero upstream gradient -> zero gradients
+    z = ops.rmsnorm_bwd_ref(x, w, torch.zeros_like(dy), 0.0)
+    assert torch.equal(z[0], torch.zeros_like(x)) and torch.equal(z[1], torch.zeros(64, dtype=torch.float64))
+    # with eps = 0 the output is scale invariant, so the gradient is orthogonal
+    # to x row by row and scales as 1/c under x -> c x
+    assert torch.allclose((gx * x).sum(-1), torch.zeros(5, dtype=torch.float64), atol=1e-10)
+    gx2, gw2 = ops.rmsnorm_bwd_ref(4.0 * x, w, dy, 0.0)
+    assert torch.allclose(gx2, gx / 4.0, rtol=1e-12, atol=1e-14)
+    assert torch.allclose(gw2, gw, rtol=1e-12, atol=1e-14)
+    # grad_weight is the column sum of dy * (x / rms), by brute force
+    for j in (0, 17, 63):
+        s = 0.0
+        for i in range(5):
+            rms = math.sqrt(sum(float(v) ** 2 for v in x[i]) / 64)
+            s += float(dy[i, j]) * float(x[i, j]) / rms
+        assert abs(float(gw[j]) - s) < 1e-10
+
+
+def test_fused_rmsnorm_bwd_matches_autograd():
+    """grad_x = grad_residual = grad_hidden + norm backward, against autograd of
+    the dual-output forward (hidden, rmsnorm(hidden)) in float64."""
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(4, 48, generator=g).double().requires_grad_(True)
+    r = torch.randn(4, 48, generator=g).double().requires_grad_(True)
+    w = (1 + 0.1 * torch.randn(48, generator=g)).double().requires_grad_(True)
+    gh = torch.randn(4, 48, generator=g).double()
+    gn = torch.randn(4, 48, generator=g).double()
+    hidden = x + r
+    y = ops.rmsnorm_ref(hidden, w, 1e-5)
+    torch.autograd.backward([hidden, y], [gh, gn])
+    gx, gw = ops.fused_residual_rmsnorm_bwd_ref(hidden.detach(), w.detach(), gh, gn, 1e-5)
+    assert torch.allclose(gx, x.grad, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(gx, r.grad, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(gw, w.grad, rtol=1e-12, atol=1e-12)
+    gx0, _ = ops.fused_residual_rmsnorm_bwd_ref(hidden.detach(), w.detach(), None, gn, 1e-5)
+    assert torch.allclose(gx0 + gh, gx, rtol=1e-12, atol=1e-12)
+
+
 def test_fused_hidden_is_rne_of_exact_sum():
     g = torch.Generator().manual_seed(3)
     x = torch.randn(64, 256, generator=g).bfloat16()
