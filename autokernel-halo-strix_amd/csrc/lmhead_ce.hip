@@ -57,6 +57,7 @@ constexpr int kGroupV = 4;                               // vocab tiles per XCD 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16_t mfma32(bf16, u32x4 a, u32x4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -145,16 +146,31 @@ __device__ __forceinline__ int tile_first(int own, int n) {
   return kShift ? min(own, n - 256) : own;
 }
 
+// Backward (kGrad) outputs: dz[t, v] = softmax(logits)[t, v] * s_t with
+// s_t = grad_loss / denom for a counted token, 0 for an ignored one and NaN
+// for a target outside [0, vocab); the target entry itself is written
+// afterwards by lmhead_ce_grad_target_kernel.
+struct GradArgs {
+  const float* lse;        // [n_rows] logsumexp of the forward
+  const int64_t* targets;  // [n_rows]
+  const float* grad_loss;  // [1] upstream gradient of the mean loss
+  const float* denom;      // [1] number of counted tokens (clamped >= 1)
+  void* dz;                // [n_rows, ld_dz] element type T
+  int64_t ld_dz;
+  int64_t ignore_index;
+};
+
 // Partial of vocab tile vt, vocab half h (0/1), token t: part[(2 vt + h) * n_rows + t].
 //
 // kFineMask: the vocab rows a tile owns may end inside a wave's 128-row
 // half (vocab % 128 != 0, or unshifted tail tiles), so the epilogue masks
 // element by element; otherwise a wave's half is either wholly owned or
 // wholly skipped.
-template <typename T, bool kShift, bool kFineMask>
+template <typename T, bool kShift, bool kFineMask, bool kGrad>
 __global__ void __launch_bounds__(kLThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* __restrict__ part,
-                      int n_rows, int vocab, int d, int64_t ldh, int64_t ldw, int n_vt, int n_tt) {
+                      int n_rows, int vocab, int d, int64_t ldh, int64_t ldw, int n_vt, int n_tt,
+                      GradArgs ga) {
   __shared__ u32x4 lds[kSlots * kSlotChunks];  // 160 KiB ring
 
   const int tid = threadIdx.x;
@@ -356,6 +372,64 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
     const int hi_w = min(vocab, v_own + kTV) - v_first - wv * 128;
     const int lo = lo_w - 4 * khalf;
     const int hi = hi_w - 4 * khalf;
+    if constexpr (kGrad) {
+      // dz = exp(z - lse_t) * s_t for this wave's 128 vocab rows x 128
+      // tokens. A lane holds token t_first + wt*128 + tb*32 + lane%32 and, per
+      // 32-row vocab block, rows 8g + 4*khalf + 0..3 (g = 0..3) of that token.
+      // v_permlane32_swap pairs groups (0, 2) and (1, 3) across the two half
+      // waves, so that every lane then holds 8 consecutive vocab entries of one
+      // token row: one 16-byte store (kFineMask: element-wise stores).
+      const float gs = ga.grad_loss[0] / ga.denom[0];
+      T* dzp = static_cast<T*>(ga.dz);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int tok = t_first + wt * 128 + tb * 32 + fr;
+        const int tok_c = min(tok, n_rows - 1);
+        const bool tok_ok = tok >= t_own && tok < n_rows;
+        const float lse2 = ga.lse[tok_c] * kLog2e;
+        const int64_t tg = ga.targets[tok_c];
+        const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= vocab) ? NAN : gs);
+        T* drow = dzp + (int64_t)tok_c * ga.ld_dz + v_first + wv * 128;
+#pragma unroll
+        for (int vb = 0; vb < 4; ++vb) {
+          uint32_t pk[4][2];
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            float e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              e[j] = __builtin_amdgcn_exp2f(fmaf(acc_read(acc[vb][tb][4 * g4 + j]), kLog2e, -lse2)) * st;
+            const int x0 = vb * 32 + 8 * g4;  // row of e[0] in the half, as counted by lo / hi
+            if constexpr (kFineMask) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (tok_ok && x0 + j >= lo && x0 + j < hi) drow[4 * khalf + x0 + j] = from_f32<T>(e[j]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 2; ++j)
+                pk[g4][j] = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(e[2 * j])) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(e[2 * j + 1])) << 16);
+            }
+          }
+          if constexpr (!kFineMask) {
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+              // lanes 0-31 end with rows 0..7 of group pr, lanes 32-63 with
+              // rows 0..7 of group pr + 2, both as (x0, x1, y0, y1)
+              const auto s0 = __builtin_amdgcn_permlane32_swap(pk[pr][0], pk[pr + 2][0], false, false);
+              const auto s1 = __builtin_amdgcn_permlane32_swap(pk[pr][1], pk[pr + 2][1], false, false);
+              const int x0 = vb * 32 + 8 * (pr + 2 * khalf);
+              if (tok_ok && x0 >= lo_w && x0 < hi_w) {
+                const u32x4 v = {s0[0], s1[0], s0[1], s1[1]};
+                *reinterpret_cast<u32x4*>(drow + x0) = v;
+              }
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      continue;
+    }
     MSPair* prow = part + (int64_t)(2 * vt + wv) * n_rows;
     MSPair res[4];
     auto epilogue = [&](auto tail_tag) {
@@ -564,6 +638,36 @@ lmhead_ce_mean_kernel(const float* __restrict__ losses, const int64_t* __restric
   }
 }
 
+// Target entries of the backward: dz[t, target[t]] = (exp(z_t - lse_t) - 1) * s_t
+// with z_t = hidden[t] . weight[target[t]] as an fp32 dot product (one wave per
+// token, as the row kernel computes target logits). Ignored tokens and targets
+// outside [0, vocab) keep what the tile kernel wrote (0 and NaN rows).
+template <typename T>
+__global__ void __launch_bounds__(256)
+lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, GradArgs ga,
+                             int n_rows, int vocab, int d, int64_t ldh, int64_t ldw) {
+  const int lane = threadIdx.x & 63;
+  const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= n_rows) return;  // the whole wave
+  const int64_t tg = ga.targets[tok];
+  if (tg == ga.ignore_index || tg < 0 || tg >= vocab) return;
+  const T* hp = H + (int64_t)tok * ldh;
+  const T* wp = W + tg * ldw;
+  float acc = 0.0f;
+  for (int c = lane; c < d / 8; c += 64) {
+    const Vec16<T> a = load16<T>(hp + 8 * c);
+    const Vec16<T> b = load16<T>(wp + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(to_f32(a.e[e]), to_f32(b.e[e]), acc);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    const float gs = ga.grad_loss[0] / ga.denom[0];
+    const float p = __builtin_amdgcn_exp2f((acc - ga.lse[tok]) * kLog2e);
+    static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tg] = from_f32<T>((p - 1.0f) * gs);
+  }
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
@@ -607,16 +711,35 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
   const T* wp = static_cast<const T*>(w);
   const dim3 gd(grid), bd(kLThreads);
   if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0)
-    lmhead_ce_tile_kernel<T, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+    lmhead_ce_tile_kernel<T, true, false, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
   else if (vocab >= kTV && n_rows >= kTT)
-    lmhead_ce_tile_kernel<T, true, true><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+    lmhead_ce_tile_kernel<T, true, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
   else
-    lmhead_ce_tile_kernel<T, false, true><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt);
+    lmhead_ce_tile_kernel<T, false, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
   lmhead_ce_rows_kernel<T><<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
                              dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
       hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index);
   lmhead_ce_mean_kernel<<<dim3(1), dim3(1024), 0, s>>>(lrow, targets, loss, n_valid, n_rows,
                                                       ignore_index);
+}
+
+template <typename T>
+void launch_lmhead_bwd(const void* h, const void* w, const GradArgs& ga, int n_rows, int vocab,
+                       int d, int64_t ldh, int64_t ldw, hipStream_t s) {
+  const int n_vt = (vocab + kTV - 1) / kTV;
+  const int n_tt = (n_rows + kTT - 1) / kTT;
+  const int grid = min(n_vt * n_tt, cu_count());
+  const T* hp = static_cast<const T*>(h);
+  const T* wp = static_cast<const T*>(w);
+  const dim3 gd(grid), bd(kLThreads);
+  const bool vec_ok = ga.ld_dz % 8 == 0 && aligned16(ga.dz);
+  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0 && vec_ok)
+    lmhead_ce_tile_kernel<T, true, false, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else if (vocab >= kTV && n_rows >= kTT)
+    lmhead_ce_tile_kernel<T, true, true, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else
+    lmhead_ce_tile_kernel<T, false, true, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  lmhead_ce_grad_target_kernel<T><<<dim3((n_rows + 3) / 4), dim3(256), 0, s>>>(hp, wp, ga, n_rows, vocab, d, ldh, ldw);
 }
 
 }  // namespace
@@ -662,5 +785,43 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
   else
     ak::launch_lmhead<ak::f16>(hidden, weight, targets, loss, lse, losses, n_valid, workspace,
                                (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, s);
+  return ak_check_launch(name);
+}
+
+extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
+                                const float* lse, const float* grad_loss, const float* denom,
+                                void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
+                                int64_t d, int64_t ld_h, int64_t ld_w, int64_t ignore_index,
+                                int dtype, void* stream) {
+  const char* name = "ak_lmhead_ce_bwd";
+  if (dtype != AK_DTYPE_BF16 && dtype != AK_DTYPE_F16)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dtype must be bf16 or fp16", name);
+  if (n_rows <= 0 || vocab <= 0 || d <= 0)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape n_rows=%lld vocab=%lld d=%lld", name,
+                        (long long)n_rows, (long long)vocab, (long long)d);
+  if (d % ak::kKB)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: d=%lld must be a multiple of %d", name,
+                        (long long)d, ak::kKB);
+  if (n_rows > (1 << 30) || vocab > (1 << 30) || d > (1 << 20))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  if (ld_h < d || ld_w < d || ld_h % 8 || ld_w % 8 || ld_h >= (1 << 23) || ld_w >= (1 << 23))
+    return ak_set_error(AK_ERR_INVALID_ARG,
+                        "%s: row pitches must be >= d, multiples of 8 and < 2^23 elements", name);
+  if (ld_gl < vocab || ld_gl % 4)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grad_logits pitch must be >= vocab and a multiple of 4", name);
+  if (!hidden || !weight || !targets || !lse || !grad_loss || !denom || !grad_logits)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  if (!ak::aligned16(hidden) || !ak::aligned16(weight) ||
+      (reinterpret_cast<uintptr_t>(grad_logits) & 7u))
+    return ak_set_error(AK_ERR_INVALID_ARG,
+                        "%s: hidden and weight must be 16-byte, grad_logits 8-byte aligned", name);
+  const int64_t n_tiles = ((vocab + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
+  if (n_tiles > 0x7FFFFFFF) return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many tiles", name);
+  ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index};
+  hipStream_t s = ak_stream(stream);
+  if (dtype == AK_DTYPE_BF16)
+    ak::launch_lmhead_bwd<ak::bf16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);
+  else
+    ak::launch_lmhead_bwd<ak::f16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);
   return ak_check_launch(name);
 }

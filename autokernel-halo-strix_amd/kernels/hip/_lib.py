@@ -60,6 +60,7 @@ _SIGNATURES = {
     "ak_lmhead_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                          _c_void_p],
+    "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_int, _c_void_p],
     "ak_selective_scan_fwd": [_c_void_p] * 10 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
 }
@@ -275,6 +276,23 @@ def lmhead_ce(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
             n_rows, vocab, d, _rows_view(hidden, "hidden"), _rows_view(weight, "weight"),
             int(ignore_index), dtype_code(hidden.dtype), _stream(hidden))
     _check(rc, "ak_lmhead_ce_fwd")
+
+
+def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                  lse: torch.Tensor, grad_loss: torch.Tensor, denom: torch.Tensor,
+                  grad_logits: torch.Tensor, ignore_index: int) -> None:
+    """dL/dlogits of the mean CE into ``grad_logits`` ``[n_rows, vocab]`` (row pitch a
+    multiple of 4); ``grad_loss`` and ``denom`` are 1-element fp32 device tensors."""
+    require_device(hidden, weight, targets, lse, grad_loss, denom, grad_logits)
+    n_rows, d = hidden.shape
+    vocab = weight.shape[0]
+    with torch.cuda.device(hidden.device):
+        rc = load().ak_lmhead_ce_bwd(
+            _ptr(hidden), _ptr(weight), _ptr(targets), _ptr(lse), _ptr(grad_loss), _ptr(denom),
+            _ptr(grad_logits), _rows_view(grad_logits, "grad_logits"), n_rows, vocab, d,
+            _rows_view(hidden, "hidden"), _rows_view(weight, "weight"), int(ignore_index),
+            dtype_code(hidden.dtype), _stream(hidden))
+    _check(rc, "ak_lmhead_ce_bwd")
 
 
 def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool) -> None:

@@ -16,11 +16,23 @@ With ``softcap`` or ``label_smoothing`` set, or for fp32 / unaligned inputs,
 the forward runs the reference's row-chunked algorithm: per ``chunk_size``
 rows a GEMM (``torch.nn.functional.linear``) feeds the gfx950 CE row kernel.
 
-Backward: per row chunk the logits are recomputed with a GEMM and turned
-into ``dL/dlogits`` by the CE row kernel from the saved logsumexp, then
-``grad_hidden = dlogits @ W`` and ``grad_W += dlogits^T @ h`` (fp32
-accumulation), as in the reference (``:97-132``). As in the reference, the
-z-loss term contributes to the returned loss only, not to the gradient.
+Backward (plain CE, the fused forward's conditions): ``ak_lmhead_ce_bwd``
+recomputes the logits tile by tile on the matrix cores from the saved
+logsumexp and writes ``dL/dlogits`` (softmax minus one-hot, times the
+upstream gradient over the counted rows) directly from registers in the
+input dtype; the device scalars stay on the device (no host sync). Then
+``grad_hidden = dlogits @ W`` and ``grad_W = dlogits^T @ h`` are two plain
+GEMMs with fp32 accumulation (hipBLASLt via torch). Rows are processed in
+chunks whose ``dlogits`` block stays under ``GRAD_LOGITS_BUDGET`` bytes (one
+chunk at the C4 shape: 8192 x 50304 bf16 = 824 MB of the 288 GB of HBM), so
+``grad_W`` is normally one GEMM rounded once to the weight dtype; beyond the
+budget each chunk's product is rounded and the chunks are summed in fp32.
+Otherwise (softcap, label smoothing, fp32 or unaligned inputs) per row chunk
+the logits are recomputed with a GEMM and turned into ``dL/dlogits`` by the
+CE row kernel from the saved logsumexp, then ``grad_hidden = dlogits @ W``
+and ``grad_W += dlogits^T @ h`` (fp32 accumulation), as in the reference
+(``:97-132``, ``:150-175``). As in the reference, the z-loss term
+contributes to the returned loss only, not to the gradient.
 
 ``chunk_size`` is the row-chunk of the GEMM paths; the fused forward tiles
 the vocabulary itself. Inputs keep their dtype (the reference coerced
@@ -68,6 +80,51 @@ def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch
     return loss, lse, n_valid
 
 
+# Largest dlogits block (bytes) the fused backward materialises at once.
+GRAD_LOGITS_BUDGET = 4 << 30
+
+
+def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                       lse: torch.Tensor, denom: torch.Tensor, grad_loss: torch.Tensor,
+                       ignore_index: int = -100, need_hidden: bool = True,
+                       need_weight: bool = True):
+    """Fused backward of :func:`lmhead_ce_forward`'s mean loss.
+
+    ``lse`` is the forward's logsumexp, ``denom`` the number of counted rows
+    (a 0-d or 1-element fp32 tensor, clamped to >= 1) and ``grad_loss`` the
+    upstream gradient of the loss. Returns ``(grad_hidden, grad_weight)`` in
+    the input dtype (``None`` where not requested).
+    """
+    _lib.require_device(hidden, weight, targets, lse, denom, grad_loss)
+    hidden = hidden.contiguous()
+    weight = weight.contiguous()
+    targets = targets.contiguous().to(torch.int64)
+    n, d = hidden.shape
+    vocab = weight.shape[0]
+    ldv = (vocab + 7) // 8 * 8  # 16-byte rows for the kernel's vector stores
+    g1 = grad_loss.reshape(1).to(torch.float32).contiguous()
+    den1 = denom.reshape(1).to(torch.float32).contiguous()
+    lse = lse.contiguous()
+    rows = max(1, min(n, GRAD_LOGITS_BUDGET // (ldv * hidden.element_size())))
+    grad_hidden = torch.empty_like(hidden) if need_hidden else None
+    grad_w32 = None
+    for start in range(0, n, rows):
+        end = min(start + rows, n)
+        dz = torch.empty((end - start, ldv), dtype=hidden.dtype, device=hidden.device)
+        _lib.lmhead_ce_bwd(hidden[start:end], weight, targets[start:end], lse[start:end], g1, den1,
+                           dz, ignore_index)
+        g = dz[:, :vocab]
+        if need_hidden:
+            torch.mm(g, weight, out=grad_hidden[start:end])
+        if need_weight:
+            part = torch.mm(g.t(), hidden[start:end])
+            if start == 0 and end == n:
+                return grad_hidden, part
+            grad_w32 = part.float() if grad_w32 is None else grad_w32.add_(part.float())
+    grad_weight = grad_w32.to(weight.dtype) if need_weight else None
+    return grad_hidden, grad_weight
+
+
 def _chunked_forward(hidden, weight, targets, chunk_size, softcap, ignore_index, label_smoothing):
     """Row-chunked GEMM + CE row kernel; returns (loss_sum, lse, n_valid float tensor)."""
     from kernels.ce_fused import _get_fwd_module
@@ -103,6 +160,7 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
             valid = (targets != ignore_index).to(torch.float32)
             loss = loss + z_loss_weight * ((lse * valid).pow(2).sum() / n_valid)
         ctx.save_for_backward(hidden, weight, targets, lse, n_valid)
+        ctx.fused = _fused_ok(hidden, weight, softcap, label_smoothing)
         ctx.chunk_size = int(chunk_size)
         ctx.softcap = float(softcap)
         ctx.ignore_index = int(ignore_index)
@@ -114,6 +172,10 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
         from kernels.ce_fused import _get_bwd_module
         hidden, weight, targets, lse, n_valid = ctx.saved_tensors
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if ctx.fused and (need_h or need_w):
+            gh, gw = lmhead_ce_backward(hidden, weight, targets, lse, n_valid, grad_output,
+                                        ctx.ignore_index, need_h, need_w)
+            return gh, gw, None, None, None, None, None, None
         grad_hidden = torch.empty_like(hidden) if need_h else None
         grad_weight = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device) if need_w else None
         if need_h or need_w:

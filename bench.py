@@ -118,6 +118,9 @@ C3_BYTES = 4 * 16384 * 4096 * 2 + 4096 * 2
 C3B_BYTES = 4 * 16384 * 4096 * 2 + 4096 * 2 + 4096 * 4
 C4_FLOP = 2 * 8192 * 50304 * 768
 C4_MIN_BYTES = 8192 * 768 * 2 + 50304 * 768 * 2 + 8192 * 8 + 8192 * 4 + 4
+# backward: logits recomputed on the matrix cores, then grad_hidden and
+# grad_weight GEMMs: three products of 2 N V D flop each
+C4B_FLOP = 3 * C4_FLOP
 C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2 + 2048 * 16 * 4 + 2048 * 4
 
 
@@ -206,6 +209,17 @@ def make_case(name):
                                           s["ws"], -100)
         return Case(name, "C4 lm-head + CE bf16 [8192, 768] x [50304, 768]", "mfma", C4_FLOP, 8192,
                     launch, sets, "lmhead_ce_tile_kernel")
+    if name == "c4b":
+        from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_backward, lmhead_ce_forward
+        cpu = gen_c4()
+        sets = _replicate(cpu, 2)
+        for s in sets:
+            _, s["lse"], nv = lmhead_ce_forward(s["h"], s["W"], s["t"])
+            s["den"] = nv.to(torch.float32).clamp(min=1.0)
+            s["g"] = torch.ones((), dtype=torch.float32, device="cuda")
+        launch = lambda s: lmhead_ce_backward(s["h"], s["W"], s["t"], s["lse"], s["den"], s["g"])
+        return Case(name, "C4 lm-head + CE backward bf16 (dlogits on the matrix cores + 2 GEMMs)",
+                    "mfma", C4B_FLOP, 8192, launch, sets, "lmhead_ce_tile_kernel (grad) + GEMMs")
     if name == "c5":
         cpu = gen_c5()
         k = _sets(C5_BYTES)
@@ -284,6 +298,20 @@ def cpu_baseline(name, budget_s=4.0):
         h, t_ = c["h"][:rows], c["t"][:rows]
         t = timed(lambda: ops.lmhead_ce_ref(h, c["W"], t_), 3)
         return 2 * rows * 50304 * 768 / t / 1e12, "TFLOP/s", f"{rows} of 8192 rows of C4 (fp32 GEMM per 4096-column vocab chunk)"
+    if name == "c4b":
+        c = gen_c4()
+        rows = 32
+        h, t_ = c["h"][:rows].float(), c["t"][:rows]
+        Wf = c["W"].float()
+
+        def bwd():
+            z = h @ Wf.t()
+            p = torch.softmax(z, -1)
+            p[torch.arange(rows), t_.clamp(min=0)] -= 1.0
+            p[t_ == -100] = 0.0
+            return p @ Wf, p.t() @ h
+        t = timed(bwd, 3)
+        return 3 * 2 * rows * 50304 * 768 / t / 1e12, "TFLOP/s", f"{rows} of 8192 rows of the C4 backward (fp32 torch)"
     if name == "c5":
         c = gen_c5(b=1, d=64)
         t = timed(lambda: ops.selective_scan_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"],
@@ -300,7 +328,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c5")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4b,c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "

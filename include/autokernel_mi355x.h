@@ -169,6 +169,30 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
                      int dtype, void* stream);
 
 /*
+ * Fused lm-head + cross-entropy backward, first half: the gradient of the
+ * mean loss with respect to the logits, written without materialising the
+ * logits first:
+ *   grad_logits[i, v] = (softmax(hidden[i] . weight^T)[v] - [v == target[i]])
+ *                       * grad_loss[0] / denom[0]
+ * (0 for ignored rows, NaN for targets outside [0, vocab)). The logits are
+ * recomputed tile by tile on the matrix cores from lse (the forward's
+ * logsumexp output) and converted in registers; the target entries come from
+ * fp32 dot products. grad_hidden = grad_logits @ weight and
+ * grad_weight = grad_logits^T @ hidden are then plain GEMMs. Replaces the
+ * per-chunk F.linear + cross_entropy_bwd_tiny_hip of
+ * kernels/hip/chunked_linear_cross_entropy.py:150-175 (forward-side
+ * gradient :97-132). grad_loss and denom are device pointers (no host
+ * synchronisation). Same shape rules as ak_lmhead_ce_fwd; ld_gl >= vocab and
+ * a multiple of 4, grad_logits 8-byte aligned, element type dtype.
+ */
+int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
+                     const float* lse, const float* grad_loss, const float* denom,
+                     void* grad_logits, int64_t ld_gl,
+                     int64_t n_rows, int64_t vocab, int64_t d,
+                     int64_t ld_h, int64_t ld_w, int64_t ignore_index,
+                     int dtype, void* stream);
+
+/*
  * Mamba-1 selective scan forward (selective_scan_fn semantics).
  * Replaces selective_scan_cuda.fwd, external/mamba/csrc/selective_scan/
  * selective_scan.cpp:227-335, as called by

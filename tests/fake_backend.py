@@ -99,6 +99,19 @@ def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_inde
         n_valid.copy_((targets != ignore_index).sum().reshape(1))
 
 
+def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ignore_index):
+    z = hidden.double() @ weight.double().t()
+    p = torch.exp(z - lse.double()[:, None])
+    t = targets.long()
+    V = weight.shape[0]
+    ok = (t >= 0) & (t < V)
+    p = p - F.one_hot(torch.where(ok, t, torch.zeros_like(t)), V).double() * ok[:, None]
+    g = p * (float(grad_loss.reshape(-1)[0]) / float(denom.reshape(-1)[0]))
+    g = torch.where((t == ignore_index)[:, None], torch.zeros_like(g), g)
+    g = torch.where((~ok & (t != ignore_index))[:, None], torch.full_like(g, math.nan), g)
+    grad_logits[:, :V].copy_(g)
+
+
 def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus):
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
                                      return_last_state=True)
@@ -124,5 +137,6 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "ce_bwd_tiny", _ce_bwd_tiny)
     monkeypatch.setattr(_lib, "lmhead_ce", _lmhead)
     monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
+    monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)
     monkeypatch.setattr(_lib, "selective_scan", _scan)
     monkeypatch.setattr(_lib, "diag_scan", _diag)

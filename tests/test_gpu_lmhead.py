@@ -122,3 +122,153 @@ def test_chunked_linear_ce_fwd_bwd(dtype, softcap, zw):
     for got, want in ((h.grad, hr.grad), (W.grad, Wr.grad)):
         rel = float((got.double().cpu() - want).norm() / want.norm())
         assert rel < 5e-2, rel
+
+
+# ---------------------------------------------------------------------------
+# Fused backward: dL/dlogits from the matrix cores, then two GEMMs
+# ---------------------------------------------------------------------------
+
+def _dz_ref(h, W, t, lse, scale, ignore_index=-100):
+    """float64 softmax(h W^T) - onehot, times scale, from the GPU forward's lse."""
+    z = h.double() @ W.double().t()
+    p = torch.exp(z - lse.double()[:, None])
+    tc = t.clamp(min=0)
+    p[torch.arange(len(t)), tc] -= 1.0
+    p = p * scale
+    p[t == ignore_index] = 0.0
+    return p
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,vocab,d", [(5, 300, 64), (300, 1000, 128), (257, 4097, 768), (1000, 256, 192),
+                                       (300, 1152, 128), (2000, 2432, 192), (512, 50304, 768)])
+def test_lmhead_ce_grad_logits(dtype, n, vocab, d):
+    """ak_lmhead_ce_bwd against float64 softmax - onehot: each entry within one
+    rounding of the element type (plus 1e-6 of the scale, and fp16's subnormal
+    half-spacing); ignored rows exactly 0."""
+    need_gpu()
+    from kernels.hip import _lib
+    g = torch.Generator().manual_seed(n + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = (0.05 * torch.randn(vocab, d, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[: max(0, n // 10)] = -100
+    say("lmhead_ce grad logits", dtype, n, vocab, d)
+    loss, lse, nv, _ = _run(h, W, t)
+    denom = nv.to(torch.float32).clamp(min=1.0).reshape(1)
+    gl = torch.tensor([0.75], device=DEV)
+    ldv = (vocab + 3) // 4 * 4
+    dz = torch.full((n, ldv), 5.0, dtype=dtype, device=DEV)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, gl, denom, dz, -100)
+    scale = 0.75 / float(denom)
+    ref = _dz_ref(h, W, t, lse.cpu(), scale)
+    got = dz[:, :vocab].double().cpu()
+    err = (got - ref).abs()
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    # fp16 entries below 2^-14 are subnormal: absolute spacing 2^-24
+    floor = 1e-6 * scale + (2.0 ** -25 if dtype == torch.float16 else 0.0)
+    assert bool((err <= eps * ref.abs() + floor).all()), float((err / (eps * ref.abs() + floor)).max())
+    assert bool((got[t == -100] == 0).all())
+    if ldv > vocab:
+        assert bool((dz[:, vocab:].float().cpu() == 5.0).all())  # row padding untouched
+
+
+def test_lmhead_ce_grad_logits_pitch_fallback():
+    """A grad_logits pitch that is a multiple of 4 but not of 8 takes the
+    element-wise store path; the result is the same as the vector path's."""
+    need_gpu()
+    from kernels.hip import _lib
+    g = torch.Generator().manual_seed(21)
+    h = torch.randn(600, 128, generator=g).bfloat16()
+    W = (0.05 * torch.randn(1152, 128, generator=g)).bfloat16()
+    t = torch.randint(0, 1152, (600,), generator=g)
+    say("lmhead grad logits pitch 1156")
+    _, lse, nv, _ = _run(h, W, t)
+    den = nv.to(torch.float32).clamp(min=1.0).reshape(1)
+    one = torch.ones(1, device=DEV)
+    a = torch.empty(600, 1152, dtype=torch.bfloat16, device=DEV)
+    b = torch.empty(600, 1156, dtype=torch.bfloat16, device=DEV)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, one, den, a, -100)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, one, den, b, -100)
+    assert torch.equal(a, b[:, :1152])
+
+
+def test_lmhead_ce_grad_bad_target_rows_are_nan():
+    need_gpu()
+    from kernels.hip import _lib
+    g = torch.Generator().manual_seed(8)
+    h = torch.randn(64, 128, generator=g).bfloat16()
+    W = (0.05 * torch.randn(500, 128, generator=g)).bfloat16()
+    t = torch.randint(0, 500, (64,), generator=g)
+    t[3] = 500
+    t[5] = -100
+    say("lmhead grad bad target")
+    _, lse, nv, _ = _run(h, W, t)
+    dz = torch.empty(64, 500, dtype=torch.bfloat16, device=DEV)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, torch.ones(1, device=DEV),
+                       torch.full((1,), 62.0, device=DEV), dz, -100)
+    assert bool(torch.isnan(dz[3].float()).all()) and bool((dz[5].float() == 0).all())
+    assert not bool(torch.isnan(dz[torch.arange(64) != 3].float()).any())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,vocab,d", [(300, 1000, 128), (1000, 4096, 256)])
+def test_lmhead_ce_backward_grads(dtype, n, vocab, d):
+    """grad_hidden and grad_weight of the mean loss against float64 autograd."""
+    need_gpu()
+    from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_backward
+    g = torch.Generator().manual_seed(n * 3 + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = (0.05 * torch.randn(vocab, d, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[::7] = -100
+    say("lmhead_ce backward grads", dtype, n, vocab, d)
+    loss, lse, nv, _ = _run(h, W, t)
+    gh, gw = lmhead_ce_backward(h.to(DEV), W.to(DEV), t.to(DEV), lse,
+                                nv.to(torch.float32).clamp(min=1.0), torch.tensor(1.3, device=DEV))
+    assert gh.dtype == dtype and gw.dtype == dtype
+    hr, Wr = h.double().requires_grad_(), W.double().requires_grad_()
+    (1.3 * F.cross_entropy(hr @ Wr.t(), t)).backward()
+    for got, want in ((gh, hr.grad), (gw, Wr.grad)):
+        got = got.double().cpu()
+        assert float((got - want).norm() / want.norm()) < 5e-3
+        assert torch.allclose(got, want, rtol=2e-2, atol=2e-2 * float(want.abs().max()))
+
+
+def test_c4_full_size_backward():
+    """C4: dlogits rows against float64, grad_hidden rows against float64,
+    grad_weight against an fp32 torch reference on the GPU; deterministic."""
+    need_gpu()
+    import bench
+    from kernels.hip import _lib
+    from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_backward
+    c = bench.gen_c4()
+    h, W, t = c["h"].to(DEV), c["W"].to(DEV), c["t"].to(DEV)
+    say("C4 backward bf16 [8192, 768] x [50304, 768]")
+    loss, lse, nv, _ = _run(c["h"], c["W"], c["t"])
+    denom = nv.to(torch.float32).clamp(min=1.0)
+    one = torch.ones((), device=DEV)
+    gh, gw = lmhead_ce_backward(h, W, t, lse, denom, one)
+    gh2, gw2 = lmhead_ce_backward(h, W, t, lse, denom, one)
+    assert torch.equal(gh, gh2) and torch.equal(gw, gw2)
+    scale = 1.0 / float(denom)
+    idx = torch.randperm(8192, generator=torch.Generator().manual_seed(5))[:128].sort().values
+    dz = torch.empty(8192, 50304, dtype=torch.bfloat16, device=DEV)
+    _lib.lmhead_ce_bwd(h, W, t, lse, one.reshape(1), denom.reshape(1), dz, -100)
+    ref = _dz_ref(c["h"][idx], c["W"], c["t"][idx], lse.cpu()[idx], scale)
+    got = dz[idx.to(DEV)].double().cpu()
+    assert bool(((got - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-6 * scale).all())
+    ghr = ref @ c["W"].double()
+    rel = float((gh.cpu()[idx].double() - ghr).norm() / ghr.norm())
+    assert rel < 5e-3, rel
+    # grad_weight: fp32 torch reference (logits materialised in fp32 on the GPU)
+    z = h.float() @ W.float().t()
+    p = torch.softmax(z, dim=-1)
+    del z
+    valid = t != -100
+    p[torch.arange(8192, device=DEV)[valid], t[valid]] -= 1.0
+    p[~valid] = 0.0
+    gwr = (p.t().contiguous() @ h.float()) * scale
+    del p
+    rel = float((gw.float() - gwr).norm() / gwr.norm())
+    assert rel < 5e-3, rel
