@@ -807,14 +807,14 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
   if (ld_h < d || ld_w < d || ld_h % 8 || ld_w % 8 || ld_h >= (1 << 23) || ld_w >= (1 << 23))
     return ak_set_error(AK_ERR_INVALID_ARG,
                         "%s: row pitches must be >= d, multiples of 8 and < 2^23 elements", name);
-  if (ld_gl < vocab || ld_gl % 4)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grad_logits pitch must be >= vocab and a multiple of 4", name);
+  if (ld_gl < vocab)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grad_logits pitch must be >= vocab", name);
   if (!hidden || !weight || !targets || !lse || !grad_loss || !denom || !grad_logits)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   if (!ak::aligned16(hidden) || !ak::aligned16(weight) ||
-      (reinterpret_cast<uintptr_t>(grad_logits) & 7u))
+      (reinterpret_cast<uintptr_t>(grad_logits) & 1u))
     return ak_set_error(AK_ERR_INVALID_ARG,
-                        "%s: hidden and weight must be 16-byte, grad_logits 8-byte aligned", name);
+                        "%s: hidden and weight must be 16-byte aligned, grad_logits element-aligned", name);
   const int64_t n_tiles = ((vocab + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
   if (n_tiles > 0x7FFFFFFF) return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many tiles", name);
   ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index};

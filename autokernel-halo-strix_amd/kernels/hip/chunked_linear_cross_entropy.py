@@ -101,19 +101,19 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     targets = targets.contiguous().to(torch.int64)
     n, d = hidden.shape
     vocab = weight.shape[0]
-    ldv = (vocab + 7) // 8 * 8  # 16-byte rows for the kernel's vector stores
     g1 = grad_loss.reshape(1).to(torch.float32).contiguous()
     den1 = denom.reshape(1).to(torch.float32).contiguous()
     lse = lse.contiguous()
-    rows = max(1, min(n, GRAD_LOGITS_BUDGET // (ldv * hidden.element_size())))
+    rows = max(1, min(n, GRAD_LOGITS_BUDGET // (vocab * hidden.element_size())))
     grad_hidden = torch.empty_like(hidden) if need_hidden else None
     grad_w32 = None
     for start in range(0, n, rows):
         end = min(start + rows, n)
-        dz = torch.empty((end - start, ldv), dtype=hidden.dtype, device=hidden.device)
+        # exactly [rows, vocab]: a padded pitch would leave uninitialised
+        # columns that a GEMM may read past K (0 * NaN)
+        g = torch.empty((end - start, vocab), dtype=hidden.dtype, device=hidden.device)
         _lib.lmhead_ce_bwd(hidden[start:end], weight, targets[start:end], lse[start:end], g1, den1,
-                           dz, ignore_index)
-        g = dz[:, :vocab]
+                           g, ignore_index)
         if need_hidden:
             torch.mm(g, weight, out=grad_hidden[start:end])
         if need_weight:

@@ -182,8 +182,10 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
  * per-chunk F.linear + cross_entropy_bwd_tiny_hip of
  * kernels/hip/chunked_linear_cross_entropy.py:150-175 (forward-side
  * gradient :97-132). grad_loss and denom are device pointers (no host
- * synchronisation). Same shape rules as ak_lmhead_ce_fwd; ld_gl >= vocab and
- * a multiple of 4, grad_logits 8-byte aligned, element type dtype.
+ * synchronisation). Same shape rules as ak_lmhead_ce_fwd; ld_gl >= vocab,
+ * element type dtype (16-byte stores when ld_gl is a multiple of 8 and
+ * grad_logits is 16-byte aligned, element stores otherwise). Only the first
+ * vocab entries of each row are written.
  */
 int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
                      const float* lse, const float* grad_loss, const float* denom,
