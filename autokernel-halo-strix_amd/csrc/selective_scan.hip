@@ -571,6 +571,111 @@ diag_scan_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
   }
 }
 
+// Backward of the diagonal recurrence (the gradient of the reference's
+// sequential formula, kernels/hip/_torch_ops.py:346-386, and of its HIP
+// kernel kernels/hip/selective_scan_backward.py:72-311), one lane per
+// (batch, channel), channels coalesced. Pass 1 runs the recurrence forward
+// and parks state[t] in grad_C; pass 2 runs backward in time:
+//   grad_C[t]   = gy[t] * state[t]
+//   g          += gy[t] * C[t]
+//   grad_dA[t]  = g * state[t-1]
+//   grad_dBx[t] = g
+//   g          *= dA[t]
+//   grad_x[t]   = gy[t] * D
+// reading state[t] and state[t-1] from grad_C before step t overwrites
+// entry t (entry t-1 is overwritten only at step t-1, later). Each lane also
+// writes its sum over t of gy * x for the fixed-order batch reduction of
+// grad_D. Loads run 8 steps ahead of the recurrence.
+constexpr int kDiagU = 8;
+
+__global__ void __launch_bounds__(256)
+diag_scan_bwd_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                     const float* __restrict__ C, const float* __restrict__ D,
+                     const float* __restrict__ x, const float* __restrict__ gy,
+                     float* __restrict__ g_dA, float* __restrict__ g_dBx, float* g_C,
+                     float* __restrict__ g_x, float* __restrict__ gD_part, int batch, int seqlen,
+                     int d_inner) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)batch * d_inner) return;
+  const int b = (int)(gid / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int64_t base = (int64_t)b * seqlen * d_inner + d;
+  const int64_t D_ = d_inner;
+
+  float s = 0.0f;
+  int t = 0;
+  for (; t + kDiagU <= seqlen; t += kDiagU) {
+    float a[kDiagU], v[kDiagU];
+#pragma unroll
+    for (int k = 0; k < kDiagU; ++k) {
+      a[k] = dA[base + (t + k) * D_];
+      v[k] = dBx[base + (t + k) * D_];
+    }
+#pragma unroll
+    for (int k = 0; k < kDiagU; ++k) {
+      s = fmaf(a[k], s, v[k]);
+      g_C[base + (t + k) * D_] = s;
+    }
+  }
+  for (; t < seqlen; ++t) {
+    s = fmaf(dA[base + t * D_], s, dBx[base + t * D_]);
+    g_C[base + t * D_] = s;
+  }
+
+  const float dd = D[d];
+  float g = 0.0f, gd = 0.0f;
+  t = seqlen - 1;
+  for (; t - kDiagU + 1 >= 0; t -= kDiagU) {
+    float a[kDiagU], c[kDiagU], yv[kDiagU], xv[kDiagU], st[kDiagU + 1];
+#pragma unroll
+    for (int k = 0; k < kDiagU; ++k) {
+      const int64_t i = base + (int64_t)(t - k) * D_;
+      a[k] = dA[i];
+      c[k] = C[i];
+      yv[k] = gy[i];
+      xv[k] = x[i];
+      st[k] = g_C[i];
+    }
+    st[kDiagU] = t - kDiagU >= 0 ? g_C[base + (int64_t)(t - kDiagU) * D_] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kDiagU; ++k) {
+      const int64_t i = base + (int64_t)(t - k) * D_;
+      g_C[i] = yv[k] * st[k];
+      g = fmaf(yv[k], c[k], g);
+      g_dA[i] = g * st[k + 1];
+      g_dBx[i] = g;
+      g *= a[k];
+      g_x[i] = yv[k] * dd;
+      gd = fmaf(yv[k], xv[k], gd);
+    }
+  }
+  for (; t >= 0; --t) {
+    const int64_t i = base + (int64_t)t * D_;
+    const float st_t = g_C[i];
+    const float st_p = t > 0 ? g_C[i - D_] : 0.0f;
+    const float yv = gy[i];
+    g_C[i] = yv * st_t;
+    g = fmaf(yv, C[i], g);
+    g_dA[i] = g * st_p;
+    g_dBx[i] = g;
+    g *= dA[i];
+    g_x[i] = yv * dd;
+    gd = fmaf(yv, x[i], gd);
+  }
+  gD_part[gid] = gd;
+}
+
+// grad_D[d] = sum over b of gD_part[b][d], b in increasing order.
+__global__ void __launch_bounds__(256)
+diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_D, int batch,
+                    int d_inner) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= d_inner) return;
+  float s = 0.0f;
+  for (int b = 0; b < batch; ++b) s += gD_part[(int64_t)b * d_inner + d];
+  grad_D[d] = s;
+}
+
 // Whether the fast kernel's layout assumptions hold: whole 64-step tiles,
 // whole 16-channel workgroups, 4-element aligned rows for the vector loads,
 // and every buffer resource's extent (16 channel rows, or dstate B / C rows)
@@ -681,5 +786,42 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const unsigned grid = (unsigned)((lanes + 255) / 256);
   ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, ak_stream(stream)>>>(dA, dBx, C, D, x, y, (int)batch,
                                                                       (int)seqlen, (int)d_inner);
+  return ak_check_launch(name);
+}
+
+extern "C" size_t ak_diag_scan_bwd_workspace_bytes(int64_t batch, int64_t d_inner) {
+  if (batch <= 0 || d_inner <= 0) return 0;
+  return (size_t)(((batch * d_inner * 4) + 255) & ~(int64_t)255);
+}
+
+extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* C, const float* D,
+                                const float* x, const float* grad_y, float* grad_dA,
+                                float* grad_dBx, float* grad_C, float* grad_D, float* grad_x,
+                                void* workspace, size_t workspace_bytes, int64_t batch,
+                                int64_t seqlen, int64_t d_inner, void* stream) {
+  const char* name = "ak_diag_scan_bwd";
+  if (batch < 0 || seqlen < 0 || d_inner <= 0) return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
+  if (batch * d_inner > 0x7FFFFFFFll || seqlen > 0x7FFFFFFFll)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  if (!grad_D) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null grad_D", name);
+  hipStream_t s = ak_stream(stream);
+  if (batch == 0 || seqlen == 0) {
+    // no steps: grad_D is a sum over nothing
+    ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
+        nullptr, grad_D, 0, (int)d_inner);
+    return ak_check_launch(name);
+  }
+  if (!dA || !dBx || !C || !D || !x || !grad_y || !grad_dA || !grad_dBx || !grad_C || !grad_x)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  if (!workspace || workspace_bytes < ak_diag_scan_bwd_workspace_bytes(batch, d_inner))
+    return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
+                        workspace_bytes, ak_diag_scan_bwd_workspace_bytes(batch, d_inner));
+  float* part = static_cast<float*>(workspace);
+  const int64_t lanes = batch * d_inner;
+  ak::diag_scan_bwd_kernel<<<dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s>>>(
+      dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx, grad_C, grad_x, part, (int)batch, (int)seqlen,
+      (int)d_inner);
+  ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
+      part, grad_D, (int)batch, (int)d_inner);
   return ak_check_launch(name);
 }

@@ -63,12 +63,15 @@ _SIGNATURES = {
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_int, _c_void_p],
     "ak_selective_scan_fwd": [_c_void_p] * 10 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
+    "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
+    "ak_diag_scan_bwd": [_c_void_p] * 12 + [ctypes.c_size_t] + [_i64] * 3 + [_c_void_p],
 }
 _RESTYPES = {
     "ak_last_error": ctypes.c_char_p,
     "ak_target_arch": ctypes.c_char_p,
     "ak_lmhead_ce_workspace_bytes": ctypes.c_size_t,
     "ak_rmsnorm_bwd_workspace_bytes": ctypes.c_size_t,
+    "ak_diag_scan_bwd_workspace_bytes": ctypes.c_size_t,
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -322,3 +325,18 @@ def diag_scan(dA, dBx, C, D, x, y) -> None:
         rc = load().ak_diag_scan_fwd(_ptr(dA), _ptr(dBx), _ptr(C), _ptr(D), _ptr(x), _ptr(y),
                                      batch, seqlen, d_inner, _stream(dA))
     _check(rc, "ak_diag_scan_fwd")
+
+
+def diag_scan_bwd(dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx, grad_C, grad_D, grad_x) -> None:
+    """Backward of :func:`diag_scan`; all fp32, contiguous ``[batch, seq, d_inner]``."""
+    require_device(dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx, grad_C, grad_D, grad_x)
+    batch, seqlen, d_inner = dA.shape
+    lib = load()
+    ws = torch.empty(int(lib.ak_diag_scan_bwd_workspace_bytes(batch, d_inner)), dtype=torch.uint8,
+                     device=dA.device)
+    with torch.cuda.device(dA.device):
+        rc = lib.ak_diag_scan_bwd(_ptr(dA), _ptr(dBx), _ptr(C), _ptr(D), _ptr(x), _ptr(grad_y),
+                                  _ptr(grad_dA), _ptr(grad_dBx), _ptr(grad_C), _ptr(grad_D),
+                                  _ptr(grad_x), _ptr(ws), ws.numel(), batch, seqlen, d_inner,
+                                  _stream(dA))
+    _check(rc, "ak_diag_scan_bwd")

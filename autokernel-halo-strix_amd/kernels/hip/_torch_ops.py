@@ -18,8 +18,9 @@ fp16 (``_torch_ops.py:77-80``, ``:266-271``); ``AUTOKERNEL_NO_BWD_HIP=1``
 selects the same gradient as fp32 PyTorch formulas on the GPU instead (the
 gradient of ``rmsnorm_backward.py:166-168`` /
 ``fused_residual_rmsnorm_backward.py:168-170``). The diagonal scan's backward
-is the reference's sequential formula (``_torch_ops.py:346-386``). Importing
-this module registers the ops.
+runs ``kernels.hip.selective_scan_backward`` (the gradient of the reference's
+sequential formula, ``_torch_ops.py:346-386``, which is also the formula
+path). Importing this module registers the ops.
 
 Autocast: under ``torch.autocast("cuda", dtype=...)`` floating inputs are
 cast to the active autocast dtype (fp16 or bf16) before the kernel runs.
@@ -199,6 +200,12 @@ def _selective_scan_setup(ctx, inputs, output):
 
 def _selective_scan_backward(ctx, grad_y):
     dA, dBx, C, D, x, _ = ctx.saved_tensors
+    if _use_hip_backward() and dA.is_cuda and dA.dtype == torch.float32:
+        # the gfx950 backward kernel, as the reference's _torch_ops.py:338-350
+        from kernels.hip.selective_scan_backward import kernel_fn as scan_bwd_fn
+        g_dA, g_dBx, g_C, g_D, g_x = scan_bwd_fn(dA, dBx, C, D, x, grad_y.float())
+        return (g_dA.to(dA.dtype), g_dBx.to(dBx.dtype), g_C.to(C.dtype), g_D.to(D.dtype),
+                g_x.to(x.dtype))
     gy = grad_y.float()
     dA_f, dBx_f, C_f, D_f, x_f = dA.float(), dBx.float(), C.float(), D.float(), x.float()
     batch, seqlen, d_inner = dA.shape

@@ -234,6 +234,24 @@ int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* C,
                      const float* D, const float* x, float* y,
                      int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
 
+/*
+ * Backward of the diagonal recurrence of ak_diag_scan_fwd, all fp32
+ * [batch, seqlen, d_inner] (grad_D [d_inner]):
+ *   grad_C[t] = gy[t] * state[t];  g += gy[t] * C[t];  grad_dA[t] = g * state[t-1];
+ *   grad_dBx[t] = g;  g *= dA[t];  grad_x[t] = gy[t] * D;  grad_D = sum_{b,t} gy * x
+ * Replaces kernels/hip/selective_scan_backward.py:393-421 (kernel_fn) and its
+ * kernels :72-311 (the gradient of kernels/hip/_torch_ops.py:346-386).
+ * grad_C doubles as the recomputed-state buffer (no extra allocation).
+ * workspace: ak_diag_scan_bwd_workspace_bytes(batch, d_inner) bytes for the
+ * per-(batch, channel) partial sums of grad_D, reduced in batch order.
+ */
+size_t ak_diag_scan_bwd_workspace_bytes(int64_t batch, int64_t d_inner);
+int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* C, const float* D,
+                     const float* x, const float* grad_y,
+                     float* grad_dA, float* grad_dBx, float* grad_C, float* grad_D,
+                     float* grad_x, void* workspace, size_t workspace_bytes,
+                     int64_t batch, int64_t seqlen, int64_t d_inner, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -261,3 +261,26 @@ def diag_scan_ref(dA, dBx, C, D, x):
         s = dA[:, t] * s + dBx[:, t]
         ys.append(C[:, t] * s + D.float() * x[:, t])
     return torch.stack(ys, dim=1)
+
+
+def diag_scan_bwd_ref(dA, dBx, C, D, x, grad_y):
+    """Backward of :func:`diag_scan_ref`, the sequential formula of
+    ``kernels/hip/_torch_ops.py:346-386`` (float64). Returns
+    ``(grad_dA, grad_dBx, grad_C, grad_D, grad_x)``."""
+    dA, dBx, C, x, gy = (t.double() for t in (dA, dBx, C, x, grad_y))
+    Dd = D.double()
+    batch, seqlen, d = dA.shape
+    states = torch.zeros(batch, seqlen + 1, d, dtype=torch.float64)
+    for t in range(seqlen):
+        states[:, t + 1] = dA[:, t] * states[:, t] + dBx[:, t]
+    g_dA, g_dBx, g_C = torch.zeros_like(dA), torch.zeros_like(dA), torch.zeros_like(dA)
+    g_D = torch.zeros(d, dtype=torch.float64)
+    g = torch.zeros(batch, d, dtype=torch.float64)
+    for t in range(seqlen - 1, -1, -1):
+        g_C[:, t] = gy[:, t] * states[:, t + 1]
+        g = g + gy[:, t] * C[:, t]
+        g_D = g_D + (gy[:, t] * x[:, t]).sum(0)
+        g_dA[:, t] = g * states[:, t]
+        g_dBx[:, t] = g
+        g = g * dA[:, t]
+    return g_dA, g_dBx, g_C, g_D, gy * Dd

@@ -124,6 +124,12 @@ def _diag(dA, dBx, C, D, x, y):
     y.copy_(ops.diag_scan_ref(dA, dBx, C, D, x))
 
 
+def _diag_bwd(dA, dBx, C, D, x, gy, g_dA, g_dBx, g_C, g_D, g_x):
+    outs = ops.diag_scan_bwd_ref(dA, dBx, C, D, x, gy)
+    for dst, src in zip((g_dA, g_dBx, g_C, g_D, g_x), outs):
+        dst.copy_(src.float())
+
+
 def install(monkeypatch):
     from kernels.hip import _lib
     monkeypatch.setattr(_lib, "require_device", lambda *tensors: None)
@@ -140,3 +146,4 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)
     monkeypatch.setattr(_lib, "selective_scan", _scan)
     monkeypatch.setattr(_lib, "diag_scan", _diag)
+    monkeypatch.setattr(_lib, "diag_scan_bwd", _diag_bwd)

@@ -182,3 +182,44 @@ def test_diag_scan_known_answer_and_random():
     say("diag scan random", shp)
     y = kernel_fn(dA.to(DEV), dBx.to(DEV), C.to(DEV), D.to(DEV), x.to(DEV)).cpu()
     assert torch.allclose(y, ops.diag_scan_ref(dA, dBx, C, D, x), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("shp", [(8, 512, 384), (2, 1000, 33), (1, 1, 5), (3, 7, 1), (4, 4096, 64)])
+def test_diag_scan_backward(shp):
+    """ak_diag_scan_bwd against the float64 sequential backward
+    (_torch_ops.py:346-386): fp32 bar 1e-5 relative (plus 1e-6 of the
+    tensor's scale for entries that cancel)."""
+    need_gpu()
+    from kernels.hip.selective_scan_backward import kernel_fn
+    g = torch.Generator().manual_seed(sum(shp))
+    dA = torch.sigmoid(torch.randn(*shp, generator=g))
+    dBx = 0.1 * torch.randn(*shp, generator=g)
+    C = torch.randn(*shp, generator=g)
+    D = torch.randn(shp[2], generator=g)
+    x = torch.randn(*shp, generator=g)
+    gy = torch.randn(*shp, generator=g)
+    say("diag scan backward", shp)
+    outs = kernel_fn(*(t.to(DEV) for t in (dA, dBx, C, D, x, gy)))
+    refs = ops.diag_scan_bwd_ref(dA, dBx, C, D, x, gy)
+    for got, ref in zip(outs, refs):
+        got = got.double().cpu()
+        bound = 1e-5 * ref.abs() + 1e-6 * float(ref.abs().max())
+        assert bool(((got - ref).abs() <= bound).all()), float(((got - ref).abs() / bound).max())
+
+
+def test_diag_scan_op_autograd_on_gpu():
+    """torch.ops.autokernel.selective_scan backward on the GPU (the gfx950
+    backward kernel) against the float64 sequential backward."""
+    need_gpu()
+    import kernels.hip._torch_ops  # noqa: F401
+    g = torch.Generator().manual_seed(77)
+    shp = (2, 300, 48)
+    ins = [torch.sigmoid(torch.randn(*shp, generator=g)), 0.1 * torch.randn(*shp, generator=g),
+           torch.randn(*shp, generator=g), torch.randn(48, generator=g), torch.randn(*shp, generator=g)]
+    say("diag scan op autograd")
+    dev = [t.to(DEV).requires_grad_() for t in ins]
+    torch.ops.autokernel.selective_scan(*dev).pow(2).sum().backward()
+    gy = 2 * ops.diag_scan_ref(*ins).double()  # d/dy of sum(y^2)
+    refs = ops.diag_scan_bwd_ref(*ins, gy)
+    for got, want in zip(dev, refs):
+        assert torch.allclose(got.grad.double().cpu(), want, rtol=1e-4, atol=1e-4)

@@ -350,3 +350,25 @@ def test_silu_dtype_choice_is_rounding_only():
     a = ops.selective_scan_ref(u, delta, A, B, C, D, zb, silu_fp32=True)
     b = ops.selective_scan_ref(u, delta, A, B, C, D, zb, silu_fp32=False)
     assert torch.allclose(a, b, rtol=1e-2, atol=1e-2)
+
+
+def test_diag_scan_bwd_matches_autograd():
+    """The restated sequential backward (_torch_ops.py:346-386) equals torch
+    autograd of the float64 forward recurrence."""
+    g = torch.Generator().manual_seed(31)
+    shp = (3, 17, 5)
+    ins = [torch.rand(*shp, generator=g).double(), torch.randn(*shp, generator=g).double(),
+           torch.randn(*shp, generator=g).double(), torch.randn(5, generator=g).double(),
+           torch.randn(*shp, generator=g).double()]
+    gy = torch.randn(*shp, generator=g).double()
+    req = [t.clone().requires_grad_() for t in ins]
+    dA, dBx, C, D, x = req
+    s = torch.zeros(3, 5, dtype=torch.float64)
+    ys = []
+    for t in range(17):
+        s = dA[:, t] * s + dBx[:, t]
+        ys.append(C[:, t] * s + D * x[:, t])
+    torch.stack(ys, 1).backward(gy)
+    outs = ops.diag_scan_bwd_ref(*ins, gy)
+    for got, t in zip(outs, req):
+        assert torch.allclose(got, t.grad, rtol=1e-12, atol=1e-12)
