@@ -32,6 +32,7 @@ constexpr int kBStride = kScanT + 4; // Bs[n][l] row pitch (floats)
 constexpr int kCStride = 20;        // Cs[l][n] row pitch (floats)
 constexpr int kHJ = 20;             // hbuf[c][j][n] step pitch (floats)
 constexpr int kHC = 16 * kHJ + 16;  // hbuf channel pitch: 336 = 16 mod 64
+constexpr int kCk = 16;             // steps between the states saved for the backward
 
 struct ScanParams {
   const void* u;
@@ -47,6 +48,19 @@ struct ScanParams {
   int batch, dim, seqlen, dstate, ngroups, ch_per_group, tiles_per_group;
   int64_t u_bs, u_ds, d_bs, d_ds, A_ds, B_bs, B_gs, B_ns, C_bs, C_gs, C_ns, z_bs, z_ds, o_bs, o_ds;
   int softplus;
+  // backward only (the preparation pass and the reverse pass)
+  const void* dout;            // [batch, dim, seqlen], element type of u, strides go_bs / go_ds
+  void* dz;                    // [batch, dim, seqlen], strides of out
+  void* du;                    // [batch, dim, seqlen], strides of out
+  void* ddelta;                // [batch, dim, seqlen] in delta's type, strides of out
+  float* ck;                   // [batch, nchunks, dim, dstate] states before each 16-step block
+  float* dB_part;              // [tiles, batch, ngroups, dstate, seqlen]
+  float* dC_part;              // [tiles, batch, ngroups, dstate, seqlen]
+  float* dA_part;              // [batch, dim, dstate]
+  float* dD_part;              // [batch, dim]
+  float* dbias_part;           // [batch, dim]
+  int64_t go_bs, go_ds;
+  int nchunks;
 };
 
 // v * m, with v taken from lane K of each 16-lane row (DPP row_newbcast:K
@@ -73,7 +87,10 @@ __device__ __forceinline__ float silu_fast(float z) {
   return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
 }
 
-template <typename TU, typename TD, typename TBC>
+// kPrep: the preparation pass of the backward. Instead of the output it
+// writes the state before every 64-step tile to p.ck and, with a gate,
+// dz = dout * y * silu'(z) (y the output before the gate).
+template <typename TU, typename TD, typename TBC, bool kPrep = false>
 __global__ void __launch_bounds__(256)
 mamba_scan_fwd_kernel(ScanParams p) {
   __shared__ float Bs[16 * kBStride];
@@ -103,6 +120,7 @@ mamba_scan_fwd_kernel(ScanParams p) {
   const int64_t d_row = (int64_t)b * p.d_bs + (int64_t)d * p.d_ds;
   const int64_t z_row = (int64_t)b * p.z_bs + (int64_t)d * p.z_ds;
   const int64_t o_row = (int64_t)b * p.o_bs + (int64_t)d * p.o_ds;
+  const int64_t go_row = (int64_t)b * p.go_bs + (int64_t)d * p.go_ds;
   const int64_t B_base = (int64_t)b * p.B_bs + (int64_t)g * p.B_gs;
   const int64_t C_base = (int64_t)b * p.C_bs + (int64_t)g * p.C_gs;
 
@@ -120,6 +138,7 @@ mamba_scan_fwd_kernel(ScanParams p) {
     TD dv[4];          // this lane's broadcast steps 4n..4n+3
     TU uv[4];
     TU uo[4], zo[4];   // output steps 16*blk + n, blk = 0..3
+    TU go[4];          // kPrep: dout at the same steps
   };
   const int sn = tid / 16, q = tid % 16;
   const int sn_c = min(sn, p.dstate - 1);
@@ -145,6 +164,7 @@ mamba_scan_fwd_kernel(ScanParams p) {
       const int l = min(l0 + 16 * blk + n, last_l);
       r.uo[blk] = static_cast<const TU*>(p.u)[u_row + l];
       r.zo[blk] = zsrc[zrow + l];
+      if constexpr (kPrep) r.go[blk] = static_cast<const TU*>(p.dout)[go_row + l];
     }
   };
 
@@ -152,7 +172,7 @@ mamba_scan_fwd_kernel(ScanParams p) {
   // transpose reads are issued right after the states are written and are
   // consumed after the next block's recurrence, which hides their latency.
   float ph[16] = {}, pc[16] = {};  // pending block: h[c][j][0..15] and C[j][0..15]
-  float p_uo = 0.0f, p_zo = 0.0f;
+  float p_uo = 0.0f, p_zo = 0.0f, p_go = 0.0f;
   int p_l = -1;              // pending output step (-1: none)
   auto finish_pending = [&]() {
     float y = 0.0f;
@@ -160,8 +180,17 @@ mamba_scan_fwd_kernel(ScanParams p) {
     for (int s = 0; s < 16; ++s) y = fmaf(ph[s], pc[s], y);
     if (ch_ok && p_l >= 0 && p_l < p.seqlen) {
       float o = fmaf(dskip, p_uo, y);
-      if (p.z) o *= silu_fast(p_zo);
-      static_cast<TU*>(p.out)[o_row + p_l] = from_f32<TU>(o);
+      if constexpr (kPrep) {
+        if (p.z) {
+          // d(y * silu(z)) / dz = y * s * (1 + z (1 - s)),  s = sigmoid(z)
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p_zo * kLog2e));
+          const float dzv = p_go * o * sg * fmaf(p_zo, 1.0f - sg, 1.0f);
+          static_cast<TU*>(p.dz)[o_row + p_l] = from_f32<TU>(dzv);
+        }
+      } else {
+        if (p.z) o *= silu_fast(p_zo);
+        static_cast<TU*>(p.out)[o_row + p_l] = from_f32<TU>(o);
+      }
     }
   };
 
@@ -199,6 +228,12 @@ mamba_scan_fwd_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
+      if constexpr (kPrep) {
+        // state before the block: the reverse pass restarts from it
+        const int lb = l0 + 16 * blk;
+        if (ch_ok && n_ok && lb < p.seqlen)
+          p.ck[(((int64_t)b * p.nchunks + lb / kCk) * p.dim + d) * p.dstate + n] = h;
+      }
       float hv[16];
       // Steps 16 blk + 4 j4 + k come from lane src = 4 blk + j4 of the row.
       // All decay factors and inputs of the block are formed first (they do
@@ -258,12 +293,13 @@ mamba_scan_fwd_kernel(ScanParams p) {
       __builtin_amdgcn_wave_barrier();
       p_uo = to_f32(cur.uo[blk]);
       p_zo = p.z ? to_f32(cur.zo[blk]) : 0.0f;
+      if constexpr (kPrep) p_go = to_f32(cur.go[blk]);
       p_l = l0 + 16 * blk + n;
     }
     cur = nxt;
   }
   finish_pending();
-  if (p.last_state && ch_ok && n_ok) {
+  if (!kPrep && p.last_state && ch_ok && n_ok) {
     p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
   }
 }
@@ -676,6 +712,310 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
   grad_D[d] = s;
 }
 
+// ---------------------------------------------------------------------------
+// Mamba-1 backward (the gradient of selective_scan_ref; the reference's
+// kernel is external/mamba/csrc/selective_scan/selective_scan_bwd_kernel.cuh,
+// entry point selective_scan.cpp:339-490). With delta' = softplus?(delta +
+// bias), a_l = exp(delta'_l A_n), dy_l = dout_l * silu(z_l), and g_l the
+// gradient of the state h_l:
+//   g_l        = a_{l+1} g_{l+1} + dy_l C_l
+//   dB[n, l]  += g_l delta'_l u_l                    (summed over channels)
+//   dC[n, l]  += dy_l h_l                            (summed over channels)
+//   du_l       = D dy_l + sum_n g_l delta'_l B_l
+//   ddelta'_l  = sum_n g_l (u_l B_l + A_n a_l h_{l-1})
+//   dA[n]     += g_l delta'_l a_l h_{l-1}
+//   dD        += dy_l u_l,  dz_l = dout_l y_l silu'(z_l)
+//   ddelta_l   = ddelta'_l * sigmoid(delta_l + bias) with softplus below its
+//                threshold 20, else ddelta'_l;  dbias += ddelta_l
+// Three launches. The preparation pass (mamba_scan_fwd_kernel<..., true>)
+// runs the recurrence forward, saves the state before every 16-step block
+// and writes dz. The reverse pass (mamba_scan_bwd_kernel) walks the 64-step
+// tiles from last to first with the forward's lane decomposition (lane =
+// channel c x state n): per 16-step block it recomputes a_l and h_l from the
+// saved state, then runs g backwards. Sums over states (du, ddelta) go
+// through a per-wave LDS transpose as in the forward; sums over the four
+// channels of a wave (dB, dC) through two permlane swaps that also
+// distribute the results over the lanes, then over the four waves through
+// LDS, and over channel tiles in the final pass (scan_bwd_finalize_kernel)
+// in a fixed order, so every gradient is deterministic.
+// ---------------------------------------------------------------------------
+constexpr int kTJ = 36;             // tbuf[c][j][n] step pitch: (cu, cdl) pairs, b128 reads conflict-free
+constexpr int kTC = 16 * kTJ + 32;  // tbuf channel pitch: 608 = 32 mod 64
+constexpr int kWP = 33;             // wbuf[lane][pair] lane pitch
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// a + b over lanes i and i ^ 32 for x, and the same for y, with x's sums
+// landing in lanes 0..31 and y's in lanes 32..63.
+__device__ __forceinline__ float swap32_sum(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Row pairs (0, 1) and (2, 3): x's sums land in rows 0 and 2, y's in rows 1 and 3.
+__device__ __forceinline__ float swap16_sum(float x, float y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
+}
+
+template <typename TU, typename TD, typename TBC>
+__global__ void __launch_bounds__(256)
+mamba_scan_bwd_kernel(ScanParams p) {
+  __shared__ float Bs[16 * kBStride];                  // B[n][t] of the tile
+  __shared__ float Cs[16 * kBStride];                  // C[n][t] of the tile
+  __shared__ __align__(16) float tbuf[4][4 * kTC];     // per wave: (cu, cdl)[c][j][n]
+  __shared__ float wbuf[4][64 * kWP];                  // per wave: (dB, dC) channel sums [lane][pair]
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int c = lane / 16;
+  const int n = lane % 16;
+
+  const int per_batch = p.ngroups * p.tiles_per_group;
+  const int b = blockIdx.x / per_batch;
+  const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
+  const int tile = blockIdx.x % p.tiles_per_group;
+  const int ch_local = tile * kScanCh + wave * 4 + c;
+  const bool ch_ok = ch_local < p.ch_per_group;
+  const int d = g * p.ch_per_group + (ch_ok ? ch_local : 0);
+  const bool n_ok = n < p.dstate;
+  const int n_c = min(n, p.dstate - 1);
+
+  const float a_nat = (ch_ok && n_ok) ? p.A[(int64_t)d * p.A_ds + n] : 0.0f;
+  const float a_scaled = a_nat * kLog2e;
+  const float dbias = p.delta_bias ? p.delta_bias[d] : 0.0f;
+  const float dskip = p.D ? p.D[d] : 0.0f;
+
+  const int64_t u_row = (int64_t)b * p.u_bs + (int64_t)d * p.u_ds;
+  const int64_t d_row = (int64_t)b * p.d_bs + (int64_t)d * p.d_ds;
+  const int64_t z_row = (int64_t)b * p.z_bs + (int64_t)d * p.z_ds;
+  const int64_t o_row = (int64_t)b * p.o_bs + (int64_t)d * p.o_ds;
+  const int64_t go_row = (int64_t)b * p.go_bs + (int64_t)d * p.go_ds;
+  const int64_t B_base = (int64_t)b * p.B_bs + (int64_t)g * p.B_gs;
+  const int64_t C_base = (int64_t)b * p.C_bs + (int64_t)g * p.C_gs;
+  const int sn = tid / 16, q = tid % 16;
+  const int sn_c = min(sn, p.dstate - 1);
+  const int last_l = p.seqlen - 1;
+
+  float* tb = tbuf[wave];
+  float* wb = wbuf[wave];
+
+  // dy = dout * silu(z) (dout without a gate), delta' = softplus?(delta + bias)
+  auto load_dy = [&](int l) {
+    const float go = to_f32(static_cast<const TU*>(p.dout)[go_row + l]);
+    if (!p.z) return go;
+    const float zv = to_f32(static_cast<const TU*>(p.z)[z_row + l]);
+    return go * zv * sigmoid_f32(zv);
+  };
+
+  float gs = 0.0f;       // gradient of the state after the step being processed
+  float a_next = 0.0f;   // decay of the step after it
+  float dA_acc = 0.0f;
+  float dD_acc = 0.0f, dbias_acc = 0.0f;  // reducer role: channel c, steps 16 blk + n
+
+  for (int l0 = (last_l / kScanT) * kScanT; l0 >= 0; l0 -= kScanT) {
+    __syncthreads();  // the previous tile's readers of Bs / Cs / wbuf are done
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int l = l0 + 4 * q + k;
+      const bool ok = sn < p.dstate && l < p.seqlen;
+      const int lc = min(l, last_l);
+      const float bv = to_f32(static_cast<const TBC*>(p.B)[B_base + (int64_t)sn_c * p.B_ns + lc]);
+      const float cv = to_f32(static_cast<const TBC*>(p.C)[C_base + (int64_t)sn_c * p.C_ns + lc]);
+      Bs[sn * kBStride + 4 * q + k] = ok ? bv : 0.0f;
+      Cs[sn * kBStride + 4 * q + k] = ok ? cv : 0.0f;
+    }
+    // broadcast sources: steps 4n .. 4n + 3 of channel c
+    float bd[4], bu[4], bdu[4], bdy[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int l = l0 + 4 * n + k;
+      const bool ok = ch_ok && l < p.seqlen;
+      const int lc = min(l, last_l);
+      float dv = to_f32(static_cast<const TD*>(p.delta)[d_row + lc]) + dbias;
+      if (p.softplus) dv = softplus_f32(dv);
+      const float uv = to_f32(static_cast<const TU*>(p.u)[u_row + lc]);
+      const float dyv = load_dy(lc);
+      bd[k] = ok ? dv : 0.0f;
+      bu[k] = ok ? uv : 0.0f;
+      bdu[k] = bd[k] * bu[k];
+      bdy[k] = ok ? dyv : 0.0f;
+    }
+    asm volatile("s_nop 1"
+                 : "+v"(bd[0]), "+v"(bd[1]), "+v"(bd[2]), "+v"(bd[3]), "+v"(bu[0]), "+v"(bu[1]),
+                   "+v"(bu[2]), "+v"(bu[3]), "+v"(bdu[0]), "+v"(bdu[1]), "+v"(bdu[2]), "+v"(bdu[3]),
+                   "+v"(bdy[0]), "+v"(bdy[1]), "+v"(bdy[2]), "+v"(bdy[3]));
+    __syncthreads();
+
+    auto block = [&](auto blk_c) {
+      constexpr int BLK = decltype(blk_c)::value;
+      const int lb = l0 + 16 * BLK;
+      if (lb >= p.seqlen) return;  // workgroup-uniform
+      const float h0 = p.ck[(((int64_t)b * p.nchunks + lb / kCk) * p.dim + d) * p.dstate + n_c];
+      const float hstart = (ch_ok && n_ok) ? h0 : 0.0f;
+      float bt[16], ct[16], as[16], hs[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        bt[j] = Bs[n * kBStride + 16 * BLK + j];
+        ct[j] = Cs[n * kBStride + 16 * BLK + j];
+      }
+      // recompute the block's decays and states
+      float xv[16];
+      static_for<0, 16>([&](auto j_c) {
+        constexpr int J = decltype(j_c)::value;
+        constexpr int kSrc = 4 * BLK + J / 4;
+        as[J] = mul_bcast<kSrc>(bd[J % 4], a_scaled);
+        xv[J] = mul_bcast<kSrc>(bdu[J % 4], bt[J]);
+      });
+#pragma unroll
+      for (int j = 0; j < 16; ++j) as[j] = __builtin_amdgcn_exp2f(as[j]);
+      float h = hstart;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        h = fmaf(as[j], h, xv[j]);
+        hs[j] = h;
+      }
+      // reverse over the block; (dB, dC) contributions of steps 2i, 2i + 1
+      // are folded over channels as soon as both exist
+      float pB = 0.0f, pC = 0.0f;
+      static_for<0, 16>([&](auto i_c) {
+        constexpr int J = 15 - decltype(i_c)::value;
+        constexpr int kSrc = 4 * BLK + J / 4;
+        constexpr int K = J % 4;
+        gs = fmaf(gs, a_next, mul_bcast<kSrc>(bdy[K], ct[J]));
+        a_next = as[J];
+        const float hp = J > 0 ? hs[J > 0 ? J - 1 : 0] : hstart;
+        const float ah = as[J] * hp;
+        const float gd = mul_bcast<kSrc>(bd[K], gs);
+        const float cu = gd * bt[J];
+        const float cdl = gs * fmaf(a_nat, ah, mul_bcast<kSrc>(bu[K], bt[J]));
+        dA_acc = fmaf(gd, ah, dA_acc);
+        const float cB = mul_bcast<kSrc>(bdu[K], gs);
+        const float cC = mul_bcast<kSrc>(bdy[K], hs[J]);
+        *reinterpret_cast<float2*>(&tb[c * kTC + J * kTJ + 2 * n]) = make_float2(cu, cdl);
+        if constexpr (J % 2 == 1) {
+          pB = cB;
+          pC = cC;
+        } else {
+          // lanes 16 r + n: r = 0: dB at step J, 1: dB at J + 1, 2: dC at J, 3: dC at J + 1
+          const float s_even = swap32_sum(cB, cC);
+          const float s_odd = swap32_sum(pB, pC);
+          wb[lane * kWP + 8 * BLK + J / 2] = swap16_sum(s_even, s_odd);
+        }
+      });
+      __builtin_amdgcn_wave_barrier();
+      // lane (c, j = n): sums over the 16 states of step lb + n
+      float su = 0.0f, sd = 0.0f;
+#pragma unroll
+      for (int s4 = 0; s4 < 8; ++s4) {
+        const float4 v = *reinterpret_cast<const float4*>(&tb[c * kTC + n * kTJ + 4 * s4]);
+        su += v.x + v.z;
+        sd += v.y + v.w;
+      }
+      __builtin_amdgcn_wave_barrier();
+      const int l = lb + n;
+      if (ch_ok && l < p.seqlen) {
+        const float dyv = load_dy(l);
+        const float uv = to_f32(static_cast<const TU*>(p.u)[u_row + l]);
+        float ddl = sd;
+        if (p.softplus) {
+          const float x = to_f32(static_cast<const TD*>(p.delta)[d_row + l]) + dbias;
+          if (x <= 20.0f) ddl *= sigmoid_f32(x);
+        }
+        static_cast<TU*>(p.du)[o_row + l] = from_f32<TU>(fmaf(dskip, dyv, su));
+        static_cast<TD*>(p.ddelta)[o_row + l] = from_f32<TD>(ddl);
+        dD_acc = fmaf(dyv, uv, dD_acc);
+        dbias_acc += ddl;
+      }
+    };
+    block(std::integral_constant<int, 3>{});
+    block(std::integral_constant<int, 2>{});
+    block(std::integral_constant<int, 1>{});
+    block(std::integral_constant<int, 0>{});
+
+    __syncthreads();  // wbuf holds the tile's per-wave sums
+    {
+      const int t = tid % 64, ng = tid / 64;
+      const int l = l0 + t;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        float* part = v ? p.dC_part : p.dB_part;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n2 = 4 * ng + i;
+          const int L = 16 * (2 * v + (t & 1)) + n2;
+          const float sum = ((wbuf[0][L * kWP + t / 2] + wbuf[1][L * kWP + t / 2]) +
+                             wbuf[2][L * kWP + t / 2]) + wbuf[3][L * kWP + t / 2];
+          if (n2 < p.dstate && l < p.seqlen)
+            part[((((int64_t)tile * p.batch + b) * p.ngroups + g) * p.dstate + n2) * p.seqlen + l] = sum;
+        }
+      }
+    }
+  }
+  if (ch_ok && n_ok) p.dA_part[((int64_t)b * p.dim + d) * p.dstate + n] = dA_acc;
+  dD_acc = row16_sum(dD_acc);
+  dbias_acc = row16_sum(dbias_acc);
+  if (ch_ok && n == 0) {
+    p.dD_part[(int64_t)b * p.dim + d] = dD_acc;
+    p.dbias_part[(int64_t)b * p.dim + d] = dbias_acc;
+  }
+}
+
+// Fixed-order sums of the reverse pass's partial results:
+//   dB / dC [b, g, n, l] = sum over the channel tiles of the group
+//   dA [d, n], dD [d], dbias [d] = sum over the batch
+// nb = 0 (no steps) writes zeros.
+template <typename TBC>
+__global__ void __launch_bounds__(256)
+scan_bwd_finalize_kernel(const float* __restrict__ dB_part, const float* __restrict__ dC_part,
+                         const float* __restrict__ dA_part, const float* __restrict__ dD_part,
+                         const float* __restrict__ dbias_part, TBC* __restrict__ dB,
+                         TBC* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dD,
+                         float* __restrict__ dbias, int64_t nbc, int tiles, int nb, int dim,
+                         int dstate) {
+  const int64_t nA = (int64_t)dim * dstate;
+  const int64_t total = 2 * nbc + nA + 2 * (int64_t)dim;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (i < 2 * nbc) {
+      const bool is_c = i >= nbc;
+      const int64_t e = is_c ? i - nbc : i;
+      const float* part = is_c ? dC_part : dB_part;
+      float s = 0.0f;
+      for (int t = 0; t < tiles; ++t) s += part[(int64_t)t * nbc + e];
+      (is_c ? dC : dB)[e] = from_f32<TBC>(s);
+      continue;
+    }
+    int64_t e = i - 2 * nbc;
+    if (e < nA) {
+      float s = 0.0f;
+      for (int bb = 0; bb < nb; ++bb) s += dA_part[(int64_t)bb * nA + e];
+      dA[e] = s;
+      continue;
+    }
+    e -= nA;
+    const bool is_bias = e >= dim;
+    const int dd = (int)(is_bias ? e - dim : e);
+    float* dst = is_bias ? dbias : dD;
+    if (!dst) continue;
+    const float* part = is_bias ? dbias_part : dD_part;
+    float s = 0.0f;
+    for (int bb = 0; bb < nb; ++bb) s += part[(int64_t)bb * dim + dd];
+    dst[dd] = s;
+  }
+}
+
 // Whether the fast kernel's layout assumptions hold: whole 64-step tiles,
 // whole 16-channel workgroups, 4-element aligned rows for the vector loads,
 // and every buffer resource's extent (16 channel rows, or dstate B / C rows)
@@ -723,6 +1063,53 @@ int dispatch_scan(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtyp
   else if (d32) launch_scan<TU, float, TU>(p, s);
   else if (bc32) launch_scan<TU, TU, float>(p, s);
   else launch_scan<TU, TU, TU>(p, s);
+  return 0;
+}
+
+// Workspace of the Mamba-1 backward, each region 256-byte aligned.
+struct ScanBwdWs {
+  size_t ck, part, dA, dD, total;
+};
+
+inline ScanBwdWs scan_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate,
+                             int64_t ngroups) {
+  auto a256 = [](int64_t v) { return (size_t)((v + 255) & ~(int64_t)255); };
+  const int64_t tiles = (dim / ngroups + kScanCh - 1) / kScanCh;
+  const int64_t nck = (seqlen + kCk - 1) / kCk;
+  ScanBwdWs w;
+  w.ck = a256(batch * nck * dim * dstate * 4);
+  w.part = a256(tiles * batch * ngroups * dstate * seqlen * 4);
+  w.dA = a256(batch * dim * dstate * 4);
+  w.dD = a256(batch * dim * 4);
+  w.total = w.ck + 2 * w.part + w.dA + 2 * w.dD;
+  return w;
+}
+
+template <typename TU, typename TD, typename TBC>
+void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* dD, float* dbias,
+                     hipStream_t s) {
+  const int grid = p.batch * p.ngroups * p.tiles_per_group;
+  mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  mamba_scan_bwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
+  const int64_t nbc = (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen;
+  const int64_t total = 2 * nbc + (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+  scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(
+      p.dB_part, p.dC_part, p.dA_part, p.dD_part, p.dbias_part, static_cast<TBC*>(dB),
+      static_cast<TBC*>(dC), dA, dD, dbias, nbc, p.tiles_per_group, p.batch, p.dim, p.dstate);
+}
+
+template <typename TU>
+int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, void* dB,
+                      void* dC, float* dA, float* dD, float* dbias, hipStream_t s) {
+  const bool d32 = delta_dtype == AK_DTYPE_F32;
+  const bool bc32 = bc_dtype == AK_DTYPE_F32;
+  if (!d32 && delta_dtype != u_dtype) return -1;
+  if (!bc32 && bc_dtype != u_dtype) return -1;
+  if (d32 && bc32) launch_scan_bwd<TU, float, float>(p, dB, dC, dA, dD, dbias, s);
+  else if (d32) launch_scan_bwd<TU, float, TU>(p, dB, dC, dA, dD, dbias, s);
+  else if (bc32) launch_scan_bwd<TU, TU, float>(p, dB, dC, dA, dD, dbias, s);
+  else launch_scan_bwd<TU, TU, TU>(p, dB, dC, dA, dD, dbias, s);
   return 0;
 }
 
@@ -823,5 +1210,94 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
       (int)d_inner);
   ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
       part, grad_D, (int)batch, (int)d_inner);
+  return ak_check_launch(name);
+}
+
+extern "C" size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
+                                                       int64_t dstate, int64_t ngroups) {
+  if (batch <= 0 || dim <= 0 || seqlen <= 0 || dstate <= 0 || ngroups <= 0 || dim % ngroups) return 0;
+  return ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups).total;
+}
+
+extern "C" int ak_selective_scan_bwd(
+    const void* u, const void* delta, const float* A, const void* B, const void* C,
+    const float* D, const void* z, const float* delta_bias, const void* dout, void* du,
+    void* ddelta, float* dA, void* dB, void* dC, float* dD, void* dz, float* ddelta_bias,
+    void* workspace, size_t workspace_bytes, int64_t batch, int64_t dim, int64_t seqlen,
+    int64_t dstate, int64_t ngroups, int64_t u_batch_stride, int64_t u_dim_stride,
+    int64_t delta_batch_stride, int64_t delta_dim_stride, int64_t A_dim_stride,
+    int64_t B_batch_stride, int64_t B_group_stride, int64_t B_state_stride,
+    int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
+    int64_t z_batch_stride, int64_t z_dim_stride, int64_t dout_batch_stride,
+    int64_t dout_dim_stride, int delta_softplus, int u_dtype, int delta_dtype, int bc_dtype,
+    void* stream) {
+  const char* name = "ak_selective_scan_bwd";
+  if (batch < 0 || dim <= 0 || seqlen < 0 || dstate <= 0 || ngroups <= 0)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
+  if (dstate > 16) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dstate=%lld > 16 is not supported", name, (long long)dstate);
+  if (dim % ngroups) return ak_set_error(AK_ERR_INVALID_ARG, "%s: dim %% ngroups != 0", name);
+  if (ak_dtype_size(u_dtype) == 0 || ak_dtype_size(delta_dtype) == 0 || ak_dtype_size(bc_dtype) == 0)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
+  if (batch > 65535 || dim > (1 << 24) || seqlen > ((int64_t)1 << 31) - ak::kScanT)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  if (!dA) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dA", name);
+  if (D && !dD) return ak_set_error(AK_ERR_INVALID_ARG, "%s: D given without dD", name);
+  if (delta_bias && !ddelta_bias) return ak_set_error(AK_ERR_INVALID_ARG, "%s: delta_bias given without ddelta_bias", name);
+  hipStream_t s = ak_stream(stream);
+  const int bc_size = ak_dtype_size(bc_dtype);
+  if (bc_size == 0) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
+  if (batch == 0 || seqlen == 0) {
+    // no steps: dA, dD and ddelta_bias are sums over nothing; dB / dC / du / ... are empty
+    switch (bc_dtype) {
+      case AK_DTYPE_F32:
+        ak::scan_bwd_finalize_kernel<float><<<dim3(64), dim3(256), 0, s>>>(
+            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA, dD, ddelta_bias, 0,
+            0, 0, (int)dim, (int)dstate);
+        break;
+      default:
+        ak::scan_bwd_finalize_kernel<ak::bf16><<<dim3(64), dim3(256), 0, s>>>(
+            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA, dD, ddelta_bias, 0,
+            0, 0, (int)dim, (int)dstate);
+        break;
+    }
+    return ak_check_launch(name);
+  }
+  if (!u || !delta || !A || !B || !C || !dout || !du || !ddelta || !dB || !dC || (z && !dz))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  const ak::ScanBwdWs ws = ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups);
+  if (!workspace || workspace_bytes < ws.total)
+    return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
+                        workspace_bytes, ws.total);
+  ak::ScanParams p{};
+  p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
+  p.delta_bias = delta_bias; p.out = nullptr; p.last_state = nullptr;
+  p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
+  p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
+  p.tiles_per_group = (p.ch_per_group + ak::kScanCh - 1) / ak::kScanCh;
+  if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grid too large", name);
+  p.u_bs = u_batch_stride; p.u_ds = u_dim_stride; p.d_bs = delta_batch_stride; p.d_ds = delta_dim_stride;
+  p.A_ds = A_dim_stride; p.B_bs = B_batch_stride; p.B_gs = B_group_stride; p.B_ns = B_state_stride;
+  p.C_bs = C_batch_stride; p.C_gs = C_group_stride; p.C_ns = C_state_stride;
+  p.z_bs = z_batch_stride; p.z_ds = z_dim_stride;
+  p.o_bs = dim * seqlen; p.o_ds = seqlen;  // du, ddelta, dz: contiguous [batch, dim, seqlen]
+  p.go_bs = dout_batch_stride; p.go_ds = dout_dim_stride;
+  p.softplus = delta_softplus ? 1 : 0;
+  p.dout = dout; p.dz = dz; p.du = du; p.ddelta = ddelta;
+  char* w = static_cast<char*>(workspace);
+  p.ck = reinterpret_cast<float*>(w);
+  p.dB_part = reinterpret_cast<float*>(w + ws.ck);
+  p.dC_part = reinterpret_cast<float*>(w + ws.ck + ws.part);
+  p.dA_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part);
+  p.dD_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA);
+  p.dbias_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA + ws.dD);
+  p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
+  int rc;
+  switch (u_dtype) {
+    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
+    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
+    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
+  }
+  if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and B/C must be fp32 or the dtype of u", name);
   return ak_check_launch(name);
 }

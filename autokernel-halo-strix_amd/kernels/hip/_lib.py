@@ -65,6 +65,9 @@ _SIGNATURES = {
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
     "ak_diag_scan_bwd": [_c_void_p] * 12 + [ctypes.c_size_t] + [_i64] * 3 + [_c_void_p],
+    "ak_selective_scan_bwd_workspace_bytes": [_i64] * 5,
+    "ak_selective_scan_bwd": [_c_void_p] * 18 + [ctypes.c_size_t] + [_i64] * 5 + [_i64] * 15
+    + [_int] * 4 + [_c_void_p],
 }
 _RESTYPES = {
     "ak_last_error": ctypes.c_char_p,
@@ -72,6 +75,7 @@ _RESTYPES = {
     "ak_lmhead_ce_workspace_bytes": ctypes.c_size_t,
     "ak_rmsnorm_bwd_workspace_bytes": ctypes.c_size_t,
     "ak_diag_scan_bwd_workspace_bytes": ctypes.c_size_t,
+    "ak_selective_scan_bwd_workspace_bytes": ctypes.c_size_t,
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -316,6 +320,34 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
             int(bool(delta_softplus)), dtype_code(u.dtype), dtype_code(delta.dtype),
             dtype_code(B.dtype), _stream(u))
     _check(rc, "ak_selective_scan_fwd")
+
+
+def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
+                       ddelta_bias, delta_softplus: bool) -> None:
+    """Mamba-1 backward. u/delta/z/dout [b, d, l] (last dim contiguous); B/C [b, g, n, l];
+    A [d, n]; outputs du/ddelta/dz contiguous [b, d, l], dB/dC contiguous [b, g, n, l] in
+    B's dtype, dA [d, n] / dD [d] / ddelta_bias [d] fp32."""
+    require_device(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
+                   ddelta_bias)
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    ngroups = B.shape[1]
+    zs = (z.stride(0), z.stride(1)) if z is not None else (0, 0)
+    lib = load()
+    ws = torch.empty(int(lib.ak_selective_scan_bwd_workspace_bytes(batch, dim, seqlen, dstate, ngroups)),
+                     dtype=torch.uint8, device=u.device)
+    with torch.cuda.device(u.device):
+        rc = lib.ak_selective_scan_bwd(
+            _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(delta_bias),
+            _ptr(dout), _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz),
+            _ptr(ddelta_bias), _ptr(ws), ws.numel(),
+            batch, dim, seqlen, dstate, ngroups,
+            u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
+            B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),
+            zs[0], zs[1], dout.stride(0), dout.stride(1),
+            int(bool(delta_softplus)), dtype_code(u.dtype), dtype_code(delta.dtype),
+            dtype_code(B.dtype), _stream(u))
+    _check(rc, "ak_selective_scan_bwd")
 
 
 def diag_scan(dA, dBx, C, D, x, y) -> None:

@@ -22,8 +22,10 @@ Two entry points, both drop-ins:
   ``[batch, dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``.
   ``delta`` may be fp32 or ``u``'s dtype; ``B`` / ``C`` fp32 or ``u``'s dtype.
   Complex ``A`` and input-independent (2-D) ``B`` / ``C`` raise
-  ``NotImplementedError``. The backward pass is not implemented on gfx950
-  (calling it raises).
+  ``NotImplementedError``. The backward (``ak_selective_scan_bwd``) returns
+  every input gradient of the reference's ``selective_scan_cuda.bwd``: ``du``,
+  ``ddelta``, ``dA``, ``dB``, ``dC``, ``dD``, ``dz``, ``ddelta_bias``, each
+  computed deterministically (fixed summation order).
 """
 
 import os
@@ -111,26 +113,68 @@ def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last
     last_state = (torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device)
                   if want_last_state else None)
     _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus)
-    return out, last_state
+    return out, last_state, (u, delta, A, B, C, D, z, delta_bias)
+
+
+def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+    """Gradients of the Mamba-1 scan for the layouts ``_scan_forward`` produced
+    (``ak_selective_scan_bwd``; the reference's ``selective_scan_cuda.bwd``,
+    external/mamba/csrc/selective_scan/selective_scan.cpp:339-490)."""
+    if dout.dtype != u.dtype:
+        dout = dout.to(u.dtype)
+    if dout.stride(-1) != 1:
+        dout = dout.contiguous()
+    batch, dim, seqlen = u.shape
+    dev = u.device
+    du = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=dev)
+    ddelta = torch.empty((batch, dim, seqlen), dtype=delta.dtype, device=dev)
+    dA = torch.empty(A.shape, dtype=torch.float32, device=dev)
+    dB = torch.empty(B.shape, dtype=B.dtype, device=dev)
+    dC = torch.empty(C.shape, dtype=C.dtype, device=dev)
+    dD = torch.empty(dim, dtype=torch.float32, device=dev) if D is not None else None
+    dz = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=dev) if z is not None else None
+    dbias = torch.empty(dim, dtype=torch.float32, device=dev) if delta_bias is not None else None
+    _lib.selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD,
+                            dz, dbias, delta_softplus)
+    return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 
 class SelectiveScanFn(torch.autograd.Function):
-    """Forward on gfx950; the backward pass is not available yet and raises."""
+    """Forward and backward on gfx950 (mirrors the reference's
+    ``SelectiveScanFn``, external/mamba/mamba_ssm/ops/selective_scan_interface.py:20-83:
+    the backward recomputes the states from the saved inputs)."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                 return_last_state=False):
-        out, last_state = _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
-                                        return_last_state)
+        out, last_state, saved = _scan_forward(u, delta, A, B, C, D, z, delta_bias,
+                                               delta_softplus, return_last_state)
+        ctx.delta_softplus = bool(delta_softplus)
+        ctx.squeeze_B = B.dim() == 3
+        ctx.squeeze_C = C.dim() == 3
+        ctx.has_D = D is not None
+        ctx.has_z = z is not None
+        ctx.has_bias = delta_bias is not None
+        ctx.save_for_backward(*(t for t in saved if t is not None))
         if return_last_state:
             ctx.mark_non_differentiable(last_state)
             return out, last_state
         return out
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "selective_scan_fn backward is not implemented on gfx950 (forward only)")
+    def backward(ctx, dout, *args):
+        it = iter(ctx.saved_tensors)
+        u, delta, A, B, C = (next(it) for _ in range(5))
+        D = next(it) if ctx.has_D else None
+        z = next(it) if ctx.has_z else None
+        delta_bias = next(it) if ctx.has_bias else None
+        du, ddelta, dA, dB, dC, dD, dz, dbias = _scan_backward(
+            dout, u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus)
+        if ctx.squeeze_B:
+            dB = dB.squeeze(1)
+        if ctx.squeeze_C:
+            dC = dC.squeeze(1)
+        return du, ddelta, dA, dB, dC, dD, dz, dbias, None, None
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,

@@ -226,6 +226,43 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           int u_dtype, int delta_dtype, int bc_dtype, void* stream);
 
 /*
+ * Mamba-1 selective scan backward: every input gradient of
+ * ak_selective_scan_fwd's output given dout. Replaces selective_scan_cuda.bwd,
+ * external/mamba/csrc/selective_scan/selective_scan.cpp:339-490, as called by
+ * external/mamba/mamba_ssm/ops/selective_scan_interface.py:59-83 (its
+ * recompute_out_z option and the saved chunk states x are not needed: the
+ * states are recomputed here).
+ *   inputs as for ak_selective_scan_fwd; dout [batch, dim, seqlen] in u_dtype
+ *   du, dz    : contiguous [batch, dim, seqlen], u_dtype (dz only with z)
+ *   ddelta    : contiguous [batch, dim, seqlen], delta_dtype
+ *   dA        : contiguous [dim, dstate] fp32
+ *   dB, dC    : contiguous [batch, ngroups, dstate, seqlen], bc_dtype
+ *   dD, ddelta_bias : [dim] fp32, required when D / delta_bias are given
+ * workspace: ak_selective_scan_bwd_workspace_bytes(...) bytes (saved states
+ * every 16 steps and the partial sums of dB / dC / dA / dD / ddelta_bias,
+ * reduced in a fixed order: results are bitwise reproducible).
+ */
+size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
+                                             int64_t dstate, int64_t ngroups);
+int ak_selective_scan_bwd(const void* u, const void* delta, const float* A,
+                          const void* B, const void* C, const float* D,
+                          const void* z, const float* delta_bias, const void* dout,
+                          void* du, void* ddelta, float* dA, void* dB, void* dC,
+                          float* dD, void* dz, float* ddelta_bias,
+                          void* workspace, size_t workspace_bytes,
+                          int64_t batch, int64_t dim, int64_t seqlen,
+                          int64_t dstate, int64_t ngroups,
+                          int64_t u_batch_stride, int64_t u_dim_stride,
+                          int64_t delta_batch_stride, int64_t delta_dim_stride,
+                          int64_t A_dim_stride,
+                          int64_t B_batch_stride, int64_t B_group_stride, int64_t B_state_stride,
+                          int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
+                          int64_t z_batch_stride, int64_t z_dim_stride,
+                          int64_t dout_batch_stride, int64_t dout_dim_stride,
+                          int delta_softplus,
+                          int u_dtype, int delta_dtype, int bc_dtype, void* stream);
+
+/*
  * Diagonal linear recurrence over [batch, seqlen, d_inner] fp32 tensors:
  *   s[t] = dA[t] * s[t-1] + dBx[t];  y[t] = C[t] * s[t] + D * x[t]
  * Replaces kernels/hip/selective_scan.py:165-201 (selective_scan_hip).

@@ -206,32 +206,36 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
 
 def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                        return_last_state=False, initial_state: Optional[torch.Tensor] = None,
-                       silu_fp32: bool = True):
+                       silu_fp32: bool = True, compute_dtype: torch.dtype = torch.float32):
     """``external/mamba/mamba_ssm/ops/selective_scan_interface.py:115-181`` (real A).
 
     fp32 state; B / C given as [b, n, l] or [b, g, n, l] (groups repeated over
     dim). ``silu_fp32=True`` evaluates silu(z) in fp32 (the gfx950 kernel's
     choice); ``False`` evaluates it in z's dtype as the reference does (:179).
     ``initial_state`` [b, d, n] (fp32) starts the recurrence from a given
-    state; the reference starts from zeros.
+    state; the reference starts from zeros. ``compute_dtype=torch.float64``
+    runs every step in float64 and returns float64 (for autograd checks of
+    the backward).
     """
-    dtype_in = u.dtype
-    u = u.float()
-    delta = delta.float()
+    cd = compute_dtype
+    dtype_in = u.dtype if cd == torch.float32 else cd
+    u = u.to(cd)
+    delta = delta.to(cd)
     if delta_bias is not None:
-        delta = delta + delta_bias[..., None].float()
+        delta = delta + delta_bias[..., None].to(cd)
     if delta_softplus:
         delta = F.softplus(delta)
     batch, dim, dstate = u.shape[0], A.shape[0], A.shape[1]
-    Bf, Cf = B.float(), C.float()
+    Bf, Cf = B.to(cd), C.to(cd)
     if Bf.dim() == 3:
         Bf = Bf.unsqueeze(1)
     if Cf.dim() == 3:
         Cf = Cf.unsqueeze(1)
     Bf = Bf.repeat_interleave(dim // Bf.shape[1], dim=1)  # [b, d, n, l]
     Cf = Cf.repeat_interleave(dim // Cf.shape[1], dim=1)
-    x = torch.zeros(batch, dim, dstate) if initial_state is None else initial_state.float().clone()
-    deltaA = torch.exp(delta[:, :, :, None] * A.float()[None, :, None, :])        # [b, d, l, n]
+    x = (torch.zeros(batch, dim, dstate, dtype=cd) if initial_state is None
+         else initial_state.to(cd).clone())
+    deltaA = torch.exp(delta[:, :, :, None] * A.to(cd)[None, :, None, :])         # [b, d, l, n]
     deltaB_u = (delta * u)[:, :, :, None] * Bf.permute(0, 1, 3, 2)                 # [b, d, l, n]
     Cl = Cf.permute(0, 1, 3, 2)                                                   # [b, d, l, n]
     ys = []
@@ -239,12 +243,89 @@ def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
         x = deltaA[:, :, i] * x + deltaB_u[:, :, i]
         ys.append((x * Cl[:, :, i]).sum(-1))
     y = torch.stack(ys, dim=2)
-    out = y if D is None else y + u * D.float()[:, None]
+    out = y if D is None else y + u * D.to(cd)[:, None]
     if z is not None:
-        gate = F.silu(z.float()) if silu_fp32 else F.silu(z).float()
+        gate = F.silu(z.to(cd)) if (silu_fp32 or cd != torch.float32) else F.silu(z).float()
         out = out * gate
     out = out.to(dtype_in)
     return (out, x) if return_last_state else out
+
+
+def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None,
+                           delta_softplus=False):
+    """Gradients of :func:`selective_scan_ref` (real A, variable B / C), in
+    float64, by the reverse recurrence of the reference's backward kernel
+    (``external/mamba/csrc/selective_scan/selective_scan_bwd_kernel.cuh``:
+    dz and the gated dout :189-197, dD :219, the per-step terms :284-300,
+    the softplus derivative :452-455). With delta' = softplus?(delta + bias),
+    a_l = exp(delta'_l A), g_l the gradient of the state after step l:
+
+        g_l       = a_{l+1} g_{l+1} + dy_l C_l          (dy = dout * silu(z))
+        du_l      = D dy_l + sum_n g_l delta'_l B_l
+        ddelta'_l = sum_n g_l (u_l B_l + A a_l h_{l-1})
+        dA       += g_l delta'_l a_l h_{l-1};  dB_l += g_l delta'_l u_l;  dC_l += dy_l h_l
+
+    Returns ``(du, ddelta, dA, dB, dC, dD, dz, ddelta_bias)`` as float64
+    tensors (``dB`` / ``dC`` in B's / C's layout; None for absent inputs).
+    """
+    f = torch.float64
+    u64, dout64 = u.to(f), dout.to(f)
+    draw = delta.to(f) + (delta_bias.to(f)[..., None] if delta_bias is not None else 0.0)
+    dl = F.softplus(draw) if delta_softplus else draw
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    A64 = A.to(f)
+    B4 = B.to(f).unsqueeze(1) if B.dim() == 3 else B.to(f)
+    C4 = C.to(f).unsqueeze(1) if C.dim() == 3 else C.to(f)
+    ngroups = B4.shape[1]
+    Bd = B4.repeat_interleave(dim // ngroups, dim=1)  # [b, d, n, l]
+    Cd = C4.repeat_interleave(dim // ngroups, dim=1)
+    a = torch.exp(dl[:, :, None, :] * A64[None, :, :, None])  # [b, d, n, l]
+    x = (dl * u64)[:, :, None, :] * Bd
+    h = torch.empty(batch, dim, dstate, seqlen, dtype=f)
+    s = torch.zeros(batch, dim, dstate, dtype=f)
+    for l in range(seqlen):
+        s = a[..., l] * s + x[..., l]
+        h[..., l] = s
+    y = (h * Cd).sum(2)
+    if D is not None:
+        y = y + u64 * D.to(f)[:, None]
+    if z is not None:
+        z64 = z.to(f)
+        sg = torch.sigmoid(z64)
+        dz = dout64 * y * sg * (1 + z64 * (1 - sg))
+        dy = dout64 * z64 * sg
+    else:
+        dz, dy = None, dout64
+    g = torch.zeros(batch, dim, dstate, dtype=f)
+    gh = torch.empty_like(h)
+    for l in range(seqlen - 1, -1, -1):
+        if l + 1 < seqlen:
+            g = g * a[..., l + 1]
+        g = g + dy[:, :, None, l] * Cd[..., l]
+        gh[..., l] = g
+    hprev = torch.cat([torch.zeros_like(h[..., :1]), h[..., :-1]], dim=-1)
+    ah = a * hprev
+    du = (gh * dl[:, :, None] * Bd).sum(2)
+    if D is not None:
+        du = du + dy * D.to(f)[:, None]
+    ddl = (gh * (u64[:, :, None] * Bd + A64[None, :, :, None] * ah)).sum(2)
+    dA = (gh * dl[:, :, None] * ah).sum((0, 3))
+    dB_d = gh * (dl * u64)[:, :, None]  # [b, d, n, l]
+    dC_d = dy[:, :, None] * h
+    dB = dB_d.reshape(batch, ngroups, dim // ngroups, dstate, seqlen).sum(2)
+    dC = dC_d.reshape(batch, ngroups, dim // ngroups, dstate, seqlen).sum(2)
+    if B.dim() == 3:
+        dB = dB.squeeze(1)
+    if C.dim() == 3:
+        dC = dC.squeeze(1)
+    if delta_softplus:
+        ddelta = torch.where(draw <= 20.0, ddl * torch.sigmoid(draw), ddl)
+    else:
+        ddelta = ddl
+    dD = (dy * u64).sum((0, 2)) if D is not None else None
+    dbias = ddelta.sum((0, 2)) if delta_bias is not None else None
+    return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 
 def diag_scan_ref(dA, dBx, C, D, x):

@@ -120,6 +120,14 @@ def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus):
         last_state.copy_(last)
 
 
+def _scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz, dbias,
+              delta_softplus):
+    outs = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, delta_bias, delta_softplus)
+    for dst, src in zip((du, ddelta, dA, dB, dC, dD, dz, dbias), outs):
+        if dst is not None:
+            dst.copy_(src.to(dst.dtype))
+
+
 def _diag(dA, dBx, C, D, x, y):
     y.copy_(ops.diag_scan_ref(dA, dBx, C, D, x))
 
@@ -145,5 +153,6 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
     monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)
     monkeypatch.setattr(_lib, "selective_scan", _scan)
+    monkeypatch.setattr(_lib, "selective_scan_bwd", _scan_bwd)
     monkeypatch.setattr(_lib, "diag_scan", _diag)
     monkeypatch.setattr(_lib, "diag_scan_bwd", _diag_bwd)

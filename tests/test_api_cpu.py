@@ -200,9 +200,23 @@ def test_selective_scan_fn_api(fake_backend):
     assert torch.allclose(out, ref) and torch.allclose(last, rl)
     with pytest.raises(NotImplementedError):
         selective_scan_fn(u, delta, A, torch.randn(4, 8), C)
+    # backward: the autograd function hands the layouts it normalised to the
+    # backward entry point and maps the gradients back (dB / dC squeezed to
+    # B's / C's [b, n, l], dtype casts by autograd)
+    D, z, bias = torch.randn(4, generator=g), torch.randn(2, 4, 20, generator=g), torch.rand(4, generator=g)
+    dout = torch.randn(2, 4, 20, generator=g)
+    leaves = [t.clone().requires_grad_() for t in (u, delta, A, B, C, D, z, bias)]
+    selective_scan_fn(*leaves[:5], D=leaves[5], z=leaves[6], delta_bias=leaves[7],
+                      delta_softplus=True).backward(dout)
+    ref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    order = (0, 1, 2, 3, 4, 5, 6, 7)  # du ddelta dA dB dC dD dz dbias
+    for leaf, i in zip(leaves, order):
+        assert leaf.grad.shape == leaf.shape
+        assert torch.allclose(leaf.grad.double(), ref[i], rtol=1e-5, atol=1e-6)
     uu = u.clone().requires_grad_()
-    with pytest.raises(NotImplementedError):
-        selective_scan_fn(uu, delta, A, B, C).sum().backward()
+    selective_scan_fn(uu, delta, A, B, C).backward(dout)
+    assert torch.allclose(uu.grad.double(), ops.selective_scan_bwd_ref(u, delta, A, B, C, dout)[0],
+                          rtol=1e-5, atol=1e-6)
 
 
 # ---------------------------------------------------------------------------

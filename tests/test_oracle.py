@@ -372,3 +372,57 @@ def test_diag_scan_bwd_matches_autograd():
     outs = ops.diag_scan_bwd_ref(*ins, gy)
     for got, t in zip(outs, req):
         assert torch.allclose(got, t.grad, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("softplus,gated,groups", [(False, False, 1), (True, True, 1), (True, True, 2),
+                                                    (False, True, 2)])
+def test_selective_scan_bwd_matches_autograd(softplus, gated, groups):
+    """The restated reverse recurrence (selective_scan_bwd_kernel.cuh:189-300,
+    :452-455) equals torch autograd of the float64 forward oracle, every
+    gradient, with and without gate, skip, bias and softplus."""
+    u, delta, A, B, C, D, z, bias = _scan_inputs(d=4, l=37, g=groups, seed=41 + groups)
+    if softplus:
+        delta = delta - 1.0  # around softplus' bend
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(5))
+    opt = (D, z, bias) if gated else (None, None, None)
+    leaves = [t.double().requires_grad_() for t in (u, delta, A, B, C)]
+    oleaves = [None if t is None else t.double().requires_grad_() for t in opt]
+    out = ops.selective_scan_ref(*leaves, D=oleaves[0], z=oleaves[1], delta_bias=oleaves[2],
+                                 delta_softplus=softplus, compute_dtype=torch.float64)
+    assert out.dtype == torch.float64
+    out.backward(dout.double())
+    ref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, *opt, delta_softplus=softplus)
+    auto = [t.grad for t in leaves] + [None if t is None else t.grad for t in oleaves]
+    for name, r, a in zip("du ddelta dA dB dC dD dz dbias".split(), ref, auto):
+        if a is None:
+            assert r is None, name
+            continue
+        assert r.shape == a.shape, name
+        assert torch.allclose(r, a, rtol=1e-10, atol=1e-12), name
+
+
+def test_selective_scan_bwd_softplus_threshold_and_closed_forms():
+    """Special cases fixed by the mathematics: above softplus' threshold
+    (20) ddelta = ddelta'; with A = 0 and one step, du = D dy + dy sum_n C B
+    delta and dB = dy C delta u (dC = dy delta u B); with dout = 0 every
+    gradient is zero; a 3-D B / C gives 3-D dB / dC."""
+    u, delta, A, B, C, D, z, bias = _scan_inputs(l=9)
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(6))
+    big = delta + 25.0
+    sp = ops.selective_scan_bwd_ref(u, big, A, B, C, dout, delta_softplus=True)
+    nosp = ops.selective_scan_bwd_ref(u, big, A, B, C, dout, delta_softplus=False)
+    assert torch.allclose(sp[1], nosp[1], rtol=1e-12, atol=1e-12)
+    u1, d1, B1, C1 = u[..., :1], delta[..., :1], B[..., :1], C[..., :1]
+    g1 = dout[..., :1]
+    du, ddl, dA, dB, dC, dD, dz, db = ops.selective_scan_bwd_ref(u1, d1, torch.zeros_like(A), B1, C1, g1, D)
+    cb = (C1 * B1).sum(2).double()                                     # [b, 1, 1] (g = 1)
+    assert torch.allclose(du, D[:, None].double() * g1.double() + g1.double() * cb * d1.double())
+    assert torch.allclose(ddl, g1.double() * u1.double() * cb)
+    assert torch.allclose(dB[:, 0], (g1.double() * d1.double() * u1.double()).sum(1, keepdim=True)
+                          * C1[:, 0].double())
+    assert torch.allclose(dC[:, 0], (g1.double() * d1.double() * u1.double()).sum(1, keepdim=True)
+                          * B1[:, 0].double())
+    zero = ops.selective_scan_bwd_ref(u, delta, A, B, C, torch.zeros_like(dout), D, z, bias, True)
+    assert all(float(t.abs().max()) == 0.0 for t in zero)
+    out3 = ops.selective_scan_bwd_ref(u, delta, A, B[:, 0], C[:, 0], dout)
+    assert out3[3].shape == B[:, 0].shape and out3[4].shape == C[:, 0].shape
