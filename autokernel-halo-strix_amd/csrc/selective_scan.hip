@@ -76,9 +76,17 @@ __device__ __forceinline__ float mul_bcast(float v, float m) {
   return r;
 }
 
+// torch.nn.functional.softplus with beta=1, threshold=20: x above 20, else
+// log1p(e^x). e^x and log2 come from the hardware (about 1 ulp each);
+// log1p(t) = log(1 + t) * t / ((1 + t) - 1) corrects the rounding of 1 + t
+// (D. Goldberg, "What every computer scientist should know about
+// floating-point arithmetic", 1991, Theorem 4), so small results keep their
+// relative accuracy. About 8 instructions instead of a library log1p / exp.
 __device__ __forceinline__ float softplus_f32(float x) {
-  // torch.nn.functional.softplus with beta=1, threshold=20.
-  return x > 20.0f ? x : log1pf(expf(x));
+  const float t = __builtin_amdgcn_exp2f(fminf(x, 20.0f) * kLog2e);
+  const float u = 1.0f + t;
+  const float lp = u == 1.0f ? t : __builtin_amdgcn_logf(u) * kLn2 * (t * __builtin_amdgcn_rcpf(u - 1.0f));
+  return x > 20.0f ? x : lp;
 }
 
 // silu(z) = z / (1 + exp(-z)) with the hardware exp2 and reciprocal (about
@@ -380,7 +388,8 @@ __device__ __forceinline__ void bstore1(Rsrc r, uint32_t voff, float v) {
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, (int)voff, 0, 0);
 }
 
-template <typename TU, typename TD, typename TBC, bool kSoftplus>
+// kPrep: the backward's preparation pass (as in mamba_scan_fwd_kernel).
+template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false>
 __global__ void __launch_bounds__(256)
 mamba_scan_fast_kernel(ScanParams p) {
   __shared__ float Bs[2][16 * kBStride];
@@ -417,7 +426,10 @@ mamba_scan_fast_kernel(ScanParams p) {
   const Rsrc rs_d = row_rsrc(p.delta, p.d_bs, p.d_ds, sizeof(TD));
   const Rsrc rs_z = p.z ? row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU)) : rs_u;
   const int64_t zds = p.z ? p.z_ds : p.u_ds;
-  const Rsrc rs_o = row_rsrc(p.out, p.o_bs, p.o_ds, sizeof(TU));
+  // the forward's output, or the preparation pass's dz (with a gate)
+  const Rsrc rs_o = row_rsrc(kPrep ? p.dz : p.out, p.o_bs, p.o_ds, sizeof(TU));
+  const Rsrc rs_go = kPrep ? row_rsrc(p.dout, p.go_bs, p.go_ds, sizeof(TU)) : rs_u;
+  const uint32_t vo_go1 = kPrep ? (uint32_t)(wc * p.go_ds + n) * sizeof(TU) : 0u;
   const uint32_t bc_bytes_B = (uint32_t)(((p.dstate - 1) * p.B_ns + L) * sizeof(TBC));
   const uint32_t bc_bytes_C = (uint32_t)(((p.dstate - 1) * p.C_ns + L) * sizeof(TBC));
   const Rsrc rs_B = make_rsrc(static_cast<const TBC*>(p.B) + (int64_t)b * p.B_bs + (int64_t)g * p.B_gs, bc_bytes_B);
@@ -441,6 +453,7 @@ mamba_scan_fast_kernel(ScanParams p) {
     Raw4<TD> dv;
     Raw4<TU> uv;
     Raw1<TU> uo[4], zo[4];
+    Raw1<TU> go[kPrep ? 4 : 1];
   };
   struct Stage {
     Raw4<TBC> bv, cv;
@@ -454,6 +467,7 @@ mamba_scan_fast_kernel(ScanParams p) {
     for (int blk = 0; blk < 4; ++blk) {
       r.uo[blk] = bload1<TU>(rs_u, vo_u1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
       r.zo[blk] = bload1<TU>(rs_z, vo_z1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+      if constexpr (kPrep) r.go[blk] = bload1<TU>(rs_go, vo_go1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
     }
   };
   auto load_stage = [&](int t, Stage& s) {
@@ -473,7 +487,7 @@ mamba_scan_fast_kernel(ScanParams p) {
   float h = 0.0f;
   float* hb = hbuf[wave];
   float ph[16] = {}, pc[16] = {};  // pending block: h[c][j][0..15] and C[j][0..15]
-  float p_uo = 0.0f, p_zo = 0.0f;
+  float p_uo = 0.0f, p_zo = 0.0f, p_go = 0.0f;
   uint32_t p_off = 0;     // byte offset of the pending output element
   bool pending = false;   // wave-uniform
   auto finish_pending = [&]() {
@@ -481,8 +495,15 @@ mamba_scan_fast_kernel(ScanParams p) {
 #pragma unroll
     for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
     float o = fmaf(dskip, p_uo, (y4[0] + y4[1]) + (y4[2] + y4[3]));
-    if (p.z) o *= silu_fast(p_zo);
-    bstore1<TU>(rs_o, p_off, o);
+    if constexpr (kPrep) {
+      if (p.z) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p_zo * kLog2e));
+        bstore1<TU>(rs_o, p_off, p_go * o * sg * fmaf(p_zo, 1.0f - sg, 1.0f));
+      }
+    } else {
+      if (p.z) o *= silu_fast(p_zo);
+      bstore1<TU>(rs_o, p_off, o);
+    }
   };
 
   auto compute = [&](int t, const Regs& cur) {
@@ -505,6 +526,10 @@ mamba_scan_fast_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
+      if constexpr (kPrep) {
+        if (n_ok)
+          p.ck[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
+      }
       float hv[16], av[16], xv[16];
       auto steps4 = [&](auto src_c, int j4) {
         constexpr int kSrc = decltype(src_c)::value;
@@ -553,6 +578,7 @@ mamba_scan_fast_kernel(ScanParams p) {
       __builtin_amdgcn_wave_barrier();
       p_uo = raw_f32<TU>(cur.uo[blk]);
       p_zo = p.z ? raw_f32<TU>(cur.zo[blk]) : 0.0f;
+      if constexpr (kPrep) p_go = raw_f32<TU>(cur.go[blk]);
       p_off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
       pending = true;
     }
@@ -581,7 +607,7 @@ mamba_scan_fast_kernel(ScanParams p) {
     if (t + 1 < nt) tile_body(t + 1, rb, ra);
   }
   finish_pending();
-  if (p.last_state && n_ok) {
+  if (!kPrep && p.last_state && n_ok) {
     p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
   }
 }
@@ -739,7 +765,7 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
 // LDS, and over channel tiles in the final pass (scan_bwd_finalize_kernel)
 // in a fixed order, so every gradient is deterministic.
 // ---------------------------------------------------------------------------
-constexpr int kTJ = 36;             // tbuf[c][j][n] step pitch: (cu, cdl) pairs, b128 reads conflict-free
+constexpr int kTJ = 36;             // tbuf[c][j][n] step pitch: float pairs, b128 reads conflict-free
 constexpr int kTC = 16 * kTJ + 32;  // tbuf channel pitch: 608 = 32 mod 64
 constexpr int kWP = 33;             // wbuf[lane][pair] lane pitch
 
@@ -764,16 +790,25 @@ __device__ __forceinline__ float swap16_sum(float x, float y) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// acc + v * m, v from lane K of each 16-lane row (DPP as in mul_bcast).
+template <int K>
+__device__ __forceinline__ float fma_bcast(float v, float m, float acc) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(v), "v"(m), "i"(K));
+  return acc;
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
 
-template <typename TU, typename TD, typename TBC>
+template <typename TU, typename TD, typename TBC, bool kSoftplus>
 __global__ void __launch_bounds__(256)
 mamba_scan_bwd_kernel(ScanParams p) {
   __shared__ float Bs[16 * kBStride];                  // B[n][t] of the tile
   __shared__ float Cs[16 * kBStride];                  // C[n][t] of the tile
-  __shared__ __align__(16) float tbuf[4][4 * kTC];     // per wave: (cu, cdl)[c][j][n]
+  __shared__ __align__(16) float tbuf[4][4 * kTC];     // per wave: (g B, A w)[c][j][n]
   __shared__ float wbuf[4][64 * kWP];                  // per wave: (dB, dC) channel sums [lane][pair]
 
   const int tid = threadIdx.x;
@@ -811,59 +846,87 @@ mamba_scan_bwd_kernel(ScanParams p) {
   float* tb = tbuf[wave];
   float* wb = wbuf[wave];
 
-  // dy = dout * silu(z) (dout without a gate), delta' = softplus?(delta + bias)
-  auto load_dy = [&](int l) {
-    const float go = to_f32(static_cast<const TU*>(p.dout)[go_row + l]);
-    if (!p.z) return go;
-    const float zv = to_f32(static_cast<const TU*>(p.z)[z_row + l]);
-    return go * zv * sigmoid_f32(zv);
+  // Global loads of one 64-step tile, issued a tile ahead of their use
+  // (clamped, always-valid addresses; masking and conversion at the use).
+  struct TileRegs {
+    TBC bv[4], cv[4];                    // staging: state sn, steps 4q .. 4q + 3
+    TD dv[4];                            // broadcast sources: steps 4n .. 4n + 3
+    TU uv[4], gv[4], zv[4];
+    TD dr[4];                            // reducer role: steps 16 blk + n
+    TU ur[4], gr[4], zr[4];
+    float ck[4];                         // states before the tile's four blocks
   };
+  const TU* const zsrc = static_cast<const TU*>(p.z ? p.z : p.u);  // without z: unused u loads
+  const int64_t zrow = p.z ? z_row : u_row;
+  const int64_t ck_row = (int64_t)d * p.dstate + n_c;
+  auto load_tile = [&](int l0, TileRegs& r) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int lc = min(l0 + 4 * q + k, last_l);
+      r.bv[k] = static_cast<const TBC*>(p.B)[B_base + (int64_t)sn_c * p.B_ns + lc];
+      r.cv[k] = static_cast<const TBC*>(p.C)[C_base + (int64_t)sn_c * p.C_ns + lc];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int lc = min(l0 + 4 * n + k, last_l);
+      r.dv[k] = static_cast<const TD*>(p.delta)[d_row + lc];
+      r.uv[k] = static_cast<const TU*>(p.u)[u_row + lc];
+      r.gv[k] = static_cast<const TU*>(p.dout)[go_row + lc];
+      r.zv[k] = zsrc[zrow + lc];
+    }
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      const int lc = min(l0 + 16 * blk + n, last_l);
+      r.dr[blk] = static_cast<const TD*>(p.delta)[d_row + lc];
+      r.ur[blk] = static_cast<const TU*>(p.u)[u_row + lc];
+      r.gr[blk] = static_cast<const TU*>(p.dout)[go_row + lc];
+      r.zr[blk] = zsrc[zrow + lc];
+      const int chunk = min((l0 + 16 * blk) / kCk, p.nchunks - 1);
+      r.ck[blk] = p.ck[((int64_t)b * p.nchunks + chunk) * p.dim * p.dstate + ck_row];
+    }
+  };
+  // dy = dout * silu(z) (dout without a gate)
+  auto gated = [&](float go, float zv) { return p.z ? go * zv * sigmoid_f32(zv) : go; };
 
   float gs = 0.0f;       // gradient of the state after the step being processed
   float a_next = 0.0f;   // decay of the step after it
   float dA_acc = 0.0f;
   float dD_acc = 0.0f, dbias_acc = 0.0f;  // reducer role: channel c, steps 16 blk + n
 
+  TileRegs cur, nxt{};
+  load_tile((last_l / kScanT) * kScanT, cur);
   for (int l0 = (last_l / kScanT) * kScanT; l0 >= 0; l0 -= kScanT) {
     __syncthreads();  // the previous tile's readers of Bs / Cs / wbuf are done
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int l = l0 + 4 * q + k;
-      const bool ok = sn < p.dstate && l < p.seqlen;
-      const int lc = min(l, last_l);
-      const float bv = to_f32(static_cast<const TBC*>(p.B)[B_base + (int64_t)sn_c * p.B_ns + lc]);
-      const float cv = to_f32(static_cast<const TBC*>(p.C)[C_base + (int64_t)sn_c * p.C_ns + lc]);
-      Bs[sn * kBStride + 4 * q + k] = ok ? bv : 0.0f;
-      Cs[sn * kBStride + 4 * q + k] = ok ? cv : 0.0f;
+      const bool ok = sn < p.dstate && l0 + 4 * q + k < p.seqlen;
+      Bs[sn * kBStride + 4 * q + k] = ok ? to_f32(cur.bv[k]) : 0.0f;
+      Cs[sn * kBStride + 4 * q + k] = ok ? to_f32(cur.cv[k]) : 0.0f;
     }
     // broadcast sources: steps 4n .. 4n + 3 of channel c
-    float bd[4], bu[4], bdu[4], bdy[4];
+    float bd[4], bdu[4], bdy[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int l = l0 + 4 * n + k;
-      const bool ok = ch_ok && l < p.seqlen;
-      const int lc = min(l, last_l);
-      float dv = to_f32(static_cast<const TD*>(p.delta)[d_row + lc]) + dbias;
-      if (p.softplus) dv = softplus_f32(dv);
-      const float uv = to_f32(static_cast<const TU*>(p.u)[u_row + lc]);
-      const float dyv = load_dy(lc);
+      const bool ok = ch_ok && l0 + 4 * n + k < p.seqlen;
+      float dv = to_f32(cur.dv[k]) + dbias;
+      if constexpr (kSoftplus) dv = softplus_f32(dv);
       bd[k] = ok ? dv : 0.0f;
-      bu[k] = ok ? uv : 0.0f;
-      bdu[k] = bd[k] * bu[k];
-      bdy[k] = ok ? dyv : 0.0f;
+      bdu[k] = bd[k] * to_f32(cur.uv[k]);
+      bdy[k] = ok ? gated(to_f32(cur.gv[k]), to_f32(cur.zv[k])) : 0.0f;
     }
     asm volatile("s_nop 1"
-                 : "+v"(bd[0]), "+v"(bd[1]), "+v"(bd[2]), "+v"(bd[3]), "+v"(bu[0]), "+v"(bu[1]),
-                   "+v"(bu[2]), "+v"(bu[3]), "+v"(bdu[0]), "+v"(bdu[1]), "+v"(bdu[2]), "+v"(bdu[3]),
-                   "+v"(bdy[0]), "+v"(bdy[1]), "+v"(bdy[2]), "+v"(bdy[3]));
+                 : "+v"(bd[0]), "+v"(bd[1]), "+v"(bd[2]), "+v"(bd[3]), "+v"(bdu[0]), "+v"(bdu[1]),
+                   "+v"(bdu[2]), "+v"(bdu[3]), "+v"(bdy[0]), "+v"(bdy[1]), "+v"(bdy[2]), "+v"(bdy[3]));
+    if (l0 > 0) load_tile(l0 - kScanT, nxt);
+    // keep the compiler from sinking the prefetch towards its use
+    asm volatile("" ::: "memory");
     __syncthreads();
 
     auto block = [&](auto blk_c) {
       constexpr int BLK = decltype(blk_c)::value;
       const int lb = l0 + 16 * BLK;
       if (lb >= p.seqlen) return;  // workgroup-uniform
-      const float h0 = p.ck[(((int64_t)b * p.nchunks + lb / kCk) * p.dim + d) * p.dstate + n_c];
-      const float hstart = (ch_ok && n_ok) ? h0 : 0.0f;
+      const float hstart = (ch_ok && n_ok) ? cur.ck[BLK] : 0.0f;
       float bt[16], ct[16], as[16], hs[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -896,14 +959,15 @@ mamba_scan_bwd_kernel(ScanParams p) {
         gs = fmaf(gs, a_next, mul_bcast<kSrc>(bdy[K], ct[J]));
         a_next = as[J];
         const float hp = J > 0 ? hs[J > 0 ? J - 1 : 0] : hstart;
-        const float ah = as[J] * hp;
-        const float gd = mul_bcast<kSrc>(bd[K], gs);
-        const float cu = gd * bt[J];
-        const float cdl = gs * fmaf(a_nat, ah, mul_bcast<kSrc>(bu[K], bt[J]));
-        dA_acc = fmaf(gd, ah, dA_acc);
+        // w = g a h_{l-1}: dA += delta' w; the state sums of g B and A w
+        // give du = delta' sum(g B) + D dy and ddelta' = u sum(g B) + sum(A w)
+        // (delta' and u are common to the 16 states of a step)
+        const float w = gs * (as[J] * hp);
+        const float gB = gs * bt[J];
+        dA_acc = fma_bcast<kSrc>(bd[K], w, dA_acc);
         const float cB = mul_bcast<kSrc>(bdu[K], gs);
         const float cC = mul_bcast<kSrc>(bdy[K], hs[J]);
-        *reinterpret_cast<float2*>(&tb[c * kTC + J * kTJ + 2 * n]) = make_float2(cu, cdl);
+        *reinterpret_cast<float2*>(&tb[c * kTC + J * kTJ + 2 * n]) = make_float2(gB, a_nat * w);
         if constexpr (J % 2 == 1) {
           pB = cB;
           pC = cC;
@@ -916,24 +980,25 @@ mamba_scan_bwd_kernel(ScanParams p) {
       });
       __builtin_amdgcn_wave_barrier();
       // lane (c, j = n): sums over the 16 states of step lb + n
-      float su = 0.0f, sd = 0.0f;
+      float sgb = 0.0f, saw = 0.0f;
 #pragma unroll
       for (int s4 = 0; s4 < 8; ++s4) {
         const float4 v = *reinterpret_cast<const float4*>(&tb[c * kTC + n * kTJ + 4 * s4]);
-        su += v.x + v.z;
-        sd += v.y + v.w;
+        sgb += v.x + v.z;
+        saw += v.y + v.w;
       }
       __builtin_amdgcn_wave_barrier();
       const int l = lb + n;
       if (ch_ok && l < p.seqlen) {
-        const float dyv = load_dy(l);
-        const float uv = to_f32(static_cast<const TU*>(p.u)[u_row + l]);
-        float ddl = sd;
-        if (p.softplus) {
-          const float x = to_f32(static_cast<const TD*>(p.delta)[d_row + l]) + dbias;
+        const float dyv = gated(to_f32(cur.gr[BLK]), to_f32(cur.zr[BLK]));
+        const float uv = to_f32(cur.ur[BLK]);
+        const float x = to_f32(cur.dr[BLK]) + dbias;
+        float dlt = x, ddl = fmaf(uv, sgb, saw);
+        if constexpr (kSoftplus) {
+          dlt = softplus_f32(x);
           if (x <= 20.0f) ddl *= sigmoid_f32(x);
         }
-        static_cast<TU*>(p.du)[o_row + l] = from_f32<TU>(fmaf(dskip, dyv, su));
+        static_cast<TU*>(p.du)[o_row + l] = from_f32<TU>(fmaf(dskip, dyv, dlt * sgb));
         static_cast<TD*>(p.ddelta)[o_row + l] = from_f32<TD>(ddl);
         dD_acc = fmaf(dyv, uv, dD_acc);
         dbias_acc += ddl;
@@ -962,6 +1027,7 @@ mamba_scan_bwd_kernel(ScanParams p) {
         }
       }
     }
+    cur = nxt;
   }
   if (ch_ok && n_ok) p.dA_part[((int64_t)b * p.dim + d) * p.dstate + n] = dA_acc;
   dD_acc = row16_sum(dD_acc);
@@ -1021,7 +1087,7 @@ scan_bwd_finalize_kernel(const float* __restrict__ dB_part, const float* __restr
 // and every buffer resource's extent (16 channel rows, or dstate B / C rows)
 // below 2 GiB.
 template <typename TU, typename TD, typename TBC>
-bool scan_fast_ok(const ScanParams& p) {
+bool scan_fast_ok(const ScanParams& p, bool prep = false) {
   auto al4 = [](const void* ptr, int64_t s0, int64_t s1, int64_t s2, size_t esz) {
     return (reinterpret_cast<uintptr_t>(ptr) % (4 * esz)) == 0 && s0 % 4 == 0 && s1 % 4 == 0 &&
            s2 % 4 == 0;
@@ -1037,6 +1103,7 @@ bool scan_fast_ok(const ScanParams& p) {
   if (p.u_bs < 0 || p.d_bs < 0 || p.o_bs < 0 || p.z_bs < 0 || p.B_bs < 0 || p.C_bs < 0 ||
       p.B_gs < 0 || p.C_gs < 0)
     return false;
+  if (prep && (p.go_bs < 0 || !fits(kScanCh, p.go_ds, sizeof(TU)))) return false;
   return fits(kScanCh, p.u_ds, sizeof(TU)) && fits(kScanCh, p.d_ds, sizeof(TD)) &&
          fits(kScanCh, p.o_ds, sizeof(TU)) && (!p.z || fits(kScanCh, p.z_ds, sizeof(TU))) &&
          fits(p.dstate, p.B_ns, sizeof(TBC)) && fits(p.dstate, p.C_ns, sizeof(TBC));
@@ -1089,8 +1156,16 @@ template <typename TU, typename TD, typename TBC>
 void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* dD, float* dbias,
                      hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
-  mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
-  mamba_scan_bwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
+  if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
+    mamba_scan_fast_kernel<TU, TD, TBC, true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p, true))
+    mamba_scan_fast_kernel<TU, TD, TBC, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else
+    mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  if (p.softplus)
+    mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else
+    mamba_scan_bwd_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
   const int64_t nbc = (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen;
   const int64_t total = 2 * nbc + (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
   const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);

@@ -122,6 +122,10 @@ C4_MIN_BYTES = 8192 * 768 * 2 + 50304 * 768 * 2 + 8192 * 8 + 8192 * 4 + 4
 # grad_weight GEMMs: three products of 2 N V D flop each
 C4B_FLOP = 3 * C4_FLOP
 C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2 + 2048 * 16 * 4 + 2048 * 4
+# Mamba-1 backward at the C5 shape: read u, z, dout (bf16), delta (fp32), B, C,
+# A, D; write du, dz (bf16), ddelta (fp32), dB, dC (bf16), dA, dD (fp32)
+C5B_BYTES = (4 * 2048 * 4096 * (2 + 2 + 2 + 4 + 2 + 2 + 4) + 4 * 4 * 16 * 4096 * 2
+             + 2 * (2048 * 16 * 4 + 2048 * 4))
 
 
 # ---------------------------------------------------------------------------
@@ -230,6 +234,24 @@ def make_case(name):
                                                s["z"], None, s["out"], None, False)
         return Case(name, "C5 Mamba-1 selective scan B4 L4096 D2048 N16", "hbm", C5_BYTES, 4 * 4096,
                     launch, sets, "mamba_scan_fast_kernel")
+    if name == "c5b":
+        cpu = gen_c5()
+        cpu["dout"] = torch.randn(cpu["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+        sets = _replicate(cpu, 2)
+        for s in sets:
+            for k in ("du", "dz"):
+                s[k] = torch.empty_like(s["u"])
+            s["ddelta"] = torch.empty_like(s["delta"])
+            s["dA"] = torch.empty_like(s["A"])
+            s["dB"] = torch.empty_like(s["B"])
+            s["dC"] = torch.empty_like(s["C"])
+            s["dD"] = torch.empty_like(s["D"])
+        launch = lambda s: _lib.selective_scan_bwd(
+            s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"], s["z"], None, s["dout"], s["du"],
+            s["ddelta"], s["dA"], s["dB"], s["dC"], s["dD"], s["dz"], None, False)
+        return Case(name, "C5-shape Mamba-1 selective scan backward B4 L4096 D2048 N16", "hbm",
+                    C5B_BYTES, 4 * 4096, launch, sets,
+                    "mamba_scan_fwd_kernel (prep) + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
     raise ValueError(name)
 
 
@@ -318,6 +340,12 @@ def cpu_baseline(name, budget_s=4.0):
                                                  c["z"]), 1)
         # tokens/s of the full problem = (channel-steps/s) / dim
         return (64 * 4096) / t / 2048 / 1e6, "Mtok/s", "batch 1, 64 of 2048 channels, full L=4096"
+    if name == "c5b":
+        c = gen_c5(b=1, d=32)
+        dout = torch.randn(c["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+        t = timed(lambda: ops.selective_scan_bwd_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], dout,
+                                                     c["D"], c["z"]), 2)
+        return (32 * 4096) / t / 2048 / 1e6, "Mtok/s", "batch 1, 32 of 2048 channels, full L=4096 (float64 oracle)"
     raise ValueError(name)
 
 
@@ -328,7 +356,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4b,c5")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4b,c5,c5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "
@@ -378,7 +406,7 @@ def main(argv=None):
             "input_sets": len(case.sets),
             "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
         }
-        if name == "c5":
+        if name in ("c5", "c5b"):
             rec["Mtok_per_s"] = round(case.tokens / (mean_ms * 1e-3) / 1e6, 2)
         if not args.no_cpu:
             rate, cunit, sample = cpu_baseline(name)
