@@ -66,6 +66,34 @@ def test_argument_errors_return_codes(lib):
     assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0
 
 
+def test_selective_scan_bwd_workspace_and_argument_errors(lib):
+    """Workspace query of the Mamba-1 backward (saved states every 16 steps,
+    per-tile dB / dC partials, per-batch dA / dD / ddelta_bias partials, each
+    256-byte aligned) and its argument checks, all rejected before any HIP
+    call."""
+    a256 = lambda v: (v + 255) // 256 * 256
+    b, d, l, n, g = 2, 40, 100, 16, 2
+    tiles = (d // g + 15) // 16
+    want = (a256(b * ((l + 15) // 16) * d * n * 4) + 2 * a256(tiles * b * g * n * l * 4)
+            + a256(b * d * n * 4) + 2 * a256(b * d * 4))
+    assert lib.ak_selective_scan_bwd_workspace_bytes(b, d, l, n, g) == want
+    assert lib.ak_selective_scan_bwd_workspace_bytes(0, d, l, n, g) == 0
+    assert lib.ak_selective_scan_bwd_workspace_bytes(b, 41, l, n, g) == 0  # dim % ngroups
+    fn = _lib.load().ak_selective_scan_bwd
+    strides = [0] * 15
+    rc = fn(*([None] * 17), None, 0, 2, 4, 16, 32, 1, *strides, 0, 2, 0, 2, None)
+    assert rc == -2 and b"dstate" in lib.ak_last_error()
+    fake = 4096  # never dereferenced: every check below fails first
+    ptrs = [fake] * 17
+    ptrs[14] = None  # dD missing while D is given
+    rc = fn(*ptrs, None, 0, 2, 4, 16, 8, 1, *strides, 0, 2, 0, 2, None)
+    assert rc == -1 and b"dD" in lib.ak_last_error()
+    rc = fn(*([fake] * 17), fake, 1024, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
+    assert rc < 0 and b"workspace" in lib.ak_last_error()
+    rc = fn(*([fake] * 17), fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 3, 2, None)
+    assert rc == -2 and b"dtype" in lib.ak_last_error()  # delta neither fp32 nor u's type
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("AUTOKERNEL_GFX950_LIB", str(tmp_path / "nope.so"))
     monkeypatch.setattr(_lib, "_lib", None)
