@@ -1038,6 +1038,51 @@ mamba_scan_bwd_kernel(ScanParams p) {
   }
 }
 
+// dB / dC = sum over channel tiles of the partial rows, 4 elements per
+// thread (16-byte loads, 8 tiles in flight), tiles in increasing order: the
+// same order, hence the same bits, as scan_bwd_finalize_kernel.
+template <typename TBC>
+__global__ void __launch_bounds__(256)
+scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restrict__ dC_part,
+                        TBC* __restrict__ dB, TBC* __restrict__ dC, int64_t n4, int tiles) {
+  struct alignas(4 * sizeof(TBC)) Out4 {
+    TBC v[4];
+  };
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const bool is_c = i >= n4;
+    const int64_t e4 = is_c ? i - n4 : i;
+    const float4* part = reinterpret_cast<const float4*>(is_c ? dC_part : dB_part) + e4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int t = 0;
+    for (; t + 8 <= tiles; t += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = part[(int64_t)(t + k) * n4];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc.x += v[k].x;
+        acc.y += v[k].y;
+        acc.z += v[k].z;
+        acc.w += v[k].w;
+      }
+    }
+    for (; t < tiles; ++t) {
+      const float4 v = part[(int64_t)t * n4];
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    Out4 o;
+    o.v[0] = from_f32<TBC>(acc.x);
+    o.v[1] = from_f32<TBC>(acc.y);
+    o.v[2] = from_f32<TBC>(acc.z);
+    o.v[3] = from_f32<TBC>(acc.w);
+    reinterpret_cast<Out4*>(is_c ? dC : dB)[e4] = o;
+  }
+}
+
 // Fixed-order sums of the reverse pass's partial results:
 //   dB / dC [b, g, n, l] = sum over the channel tiles of the group
 //   dA [d, n], dD [d], dbias [d] = sum over the batch
@@ -1166,7 +1211,16 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
     mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else
     mamba_scan_bwd_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
-  const int64_t nbc = (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen;
+  int64_t nbc = (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen;
+  const size_t out4 = 4 * sizeof(TBC);
+  if (nbc % 4 == 0 && reinterpret_cast<uintptr_t>(dB) % out4 == 0 &&
+      reinterpret_cast<uintptr_t>(dC) % out4 == 0) {
+    const int64_t n4 = nbc / 4;
+    const unsigned blocks4 = (unsigned)std::min<int64_t>((2 * n4 + 255) / 256, 65535);
+    scan_bwd_bc_sum4_kernel<TBC><<<dim3(blocks4), dim3(256), 0, s>>>(
+        p.dB_part, p.dC_part, static_cast<TBC*>(dB), static_cast<TBC*>(dC), n4, p.tiles_per_group);
+    nbc = 0;  // the scalar pass below then covers dA / dD / ddelta_bias only
+  }
   const int64_t total = 2 * nbc + (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
   const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
   scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(
