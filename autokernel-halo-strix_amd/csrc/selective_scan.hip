@@ -33,6 +33,7 @@ constexpr int kCStride = 20;        // Cs[l][n] row pitch (floats)
 constexpr int kHJ = 20;             // hbuf[c][j][n] step pitch (floats)
 constexpr int kHC = 16 * kHJ + 16;  // hbuf channel pitch: 336 = 16 mod 64
 constexpr int kCk = 16;             // steps between the states saved for the backward
+constexpr int kXChunk = 2048;       // steps per chunk-state entry (the reference's chunk)
 
 struct ScanParams {
   const void* u;
@@ -45,6 +46,9 @@ struct ScanParams {
   const float* delta_bias;
   void* out;
   float* last_state;
+  void* out_prez;              // optional: y + D u before the gate (strides of out)
+  float* chunk_states;         // optional: [batch, dim, xchunks, dstate, 2] (decay product, state)
+  int xchunks;                 // 2048-step chunks of chunk_states
   int batch, dim, seqlen, dstate, ngroups, ch_per_group, tiles_per_group;
   int64_t u_bs, u_ds, d_bs, d_ds, A_ds, B_bs, B_gs, B_ns, C_bs, C_gs, C_ns, z_bs, z_ds, o_bs, o_ds;
   int softplus;
@@ -196,12 +200,14 @@ mamba_scan_fwd_kernel(ScanParams p) {
           static_cast<TU*>(p.dz)[o_row + p_l] = from_f32<TU>(dzv);
         }
       } else {
+        if (p.out_prez) static_cast<TU*>(p.out_prez)[o_row + p_l] = from_f32<TU>(o);
         if (p.z) o *= silu_fast(p_zo);
         static_cast<TU*>(p.out)[o_row + p_l] = from_f32<TU>(o);
       }
     }
   };
 
+  float dsum = 0.0f;  // sum of delta' since step 0 (chunk states)
   TileRegs cur, nxt{};
   load_tile(0, cur);
   for (int l0 = 0; l0 < p.seqlen; l0 += kScanT) {
@@ -303,6 +309,17 @@ mamba_scan_fwd_kernel(ScanParams p) {
       p_zo = p.z ? to_f32(cur.zo[blk]) : 0.0f;
       if constexpr (kPrep) p_go = to_f32(cur.go[blk]);
       p_l = l0 + 16 * blk + n;
+    }
+    if (!kPrep && p.chunk_states) {
+      // the channel's delta' over the tile (invalid steps hold 0)
+      dsum += row16_sum((dl[0] + dl[1]) + (dl[2] + dl[3]));
+      const int l1 = l0 + kScanT;
+      if ((l1 % kXChunk == 0 || l1 >= p.seqlen) && ch_ok && n_ok) {
+        float* xs = p.chunk_states +
+                    ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + n) * 2;
+        xs[0] = __builtin_amdgcn_exp2f(a_scaled * dsum);
+        xs[1] = h;
+      }
     }
     cur = nxt;
   }
@@ -428,6 +445,7 @@ mamba_scan_fast_kernel(ScanParams p) {
   const int64_t zds = p.z ? p.z_ds : p.u_ds;
   // the forward's output, or the preparation pass's dz (with a gate)
   const Rsrc rs_o = row_rsrc(kPrep ? p.dz : p.out, p.o_bs, p.o_ds, sizeof(TU));
+  const Rsrc rs_oz = (!kPrep && p.out_prez) ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
   const Rsrc rs_go = kPrep ? row_rsrc(p.dout, p.go_bs, p.go_ds, sizeof(TU)) : rs_u;
   const uint32_t vo_go1 = kPrep ? (uint32_t)(wc * p.go_ds + n) * sizeof(TU) : 0u;
   const uint32_t bc_bytes_B = (uint32_t)(((p.dstate - 1) * p.B_ns + L) * sizeof(TBC));
@@ -501,10 +519,12 @@ mamba_scan_fast_kernel(ScanParams p) {
         bstore1<TU>(rs_o, p_off, p_go * o * sg * fmaf(p_zo, 1.0f - sg, 1.0f));
       }
     } else {
+      if (p.out_prez) bstore1<TU>(rs_oz, p_off, o);
       if (p.z) o *= silu_fast(p_zo);
       bstore1<TU>(rs_o, p_off, o);
     }
   };
+  float dsum = 0.0f;  // sum of delta' since step 0 (chunk states)
 
   auto compute = [&](int t, const Regs& cur) {
     const int buf = t & 1;
@@ -581,6 +601,16 @@ mamba_scan_fast_kernel(ScanParams p) {
       if constexpr (kPrep) p_go = raw_f32<TU>(cur.go[blk]);
       p_off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
       pending = true;
+    }
+    if (!kPrep && p.chunk_states) {
+      dsum += row16_sum((dl[0] + dl[1]) + (dl[2] + dl[3]));
+      const int l1 = (t + 1) * kScanT;
+      if ((l1 % kXChunk == 0 || l1 >= p.seqlen) && n_ok) {
+        float* xs = p.chunk_states +
+                    ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + n) * 2;
+        xs[0] = __builtin_amdgcn_exp2f(a_scaled * dsum);
+        xs[1] = h;
+      }
     }
   };
 
@@ -1248,7 +1278,7 @@ int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_
 extern "C" int ak_selective_scan_fwd(
     const void* u, const void* delta, const float* A, const void* B, const void* C,
     const float* D, const void* z, const float* delta_bias, void* out, float* last_state,
-    int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate, int64_t ngroups,
+    void* out_prez, float* chunk_states, int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate, int64_t ngroups,
     int64_t u_batch_stride, int64_t u_dim_stride, int64_t delta_batch_stride,
     int64_t delta_dim_stride, int64_t A_dim_stride, int64_t B_batch_stride,
     int64_t B_group_stride, int64_t B_state_stride, int64_t C_batch_stride,
@@ -1269,6 +1299,8 @@ extern "C" int ak_selective_scan_fwd(
   ak::ScanParams p;
   p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
   p.delta_bias = delta_bias; p.out = out; p.last_state = last_state;
+  p.out_prez = out_prez; p.chunk_states = chunk_states;
+  p.xchunks = (int)((seqlen + ak::kXChunk - 1) / ak::kXChunk);
   p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
   p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
   p.tiles_per_group = (p.ch_per_group + ak::kScanCh - 1) / ak::kScanCh;

@@ -61,7 +61,7 @@ _SIGNATURES = {
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _int,
                          _c_void_p],
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_int, _c_void_p],
-    "ak_selective_scan_fwd": [_c_void_p] * 10 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
+    "ak_selective_scan_fwd": [_c_void_p] * 12 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
     "ak_diag_scan_bwd": [_c_void_p] * 12 + [ctypes.c_size_t] + [_i64] * 3 + [_c_void_p],
@@ -302,9 +302,13 @@ def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
     _check(rc, "ak_lmhead_ce_bwd")
 
 
-def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool) -> None:
-    """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l]; A [d, n]."""
-    require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state)
+def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool,
+                   out_prez=None, chunk_states=None) -> None:
+    """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l]; A [d, n]; optional
+    out_prez (pre-gate output, strides of out) and chunk_states [b, d, ceil(l/2048), n, 2]."""
+    require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state, out_prez, chunk_states)
+    if out_prez is not None and out_prez.stride() != out.stride():
+        raise ValueError("out_prez must have out's strides")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     ngroups = B.shape[1]
@@ -312,7 +316,7 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
     with torch.cuda.device(u.device):
         rc = load().ak_selective_scan_fwd(
             _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(delta_bias),
-            _ptr(out), _ptr(last_state),
+            _ptr(out), _ptr(last_state), _ptr(out_prez), _ptr(chunk_states),
             batch, dim, seqlen, dstate, ngroups,
             u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
             B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),

@@ -39,6 +39,10 @@ BACKEND = "hip"
 
 HIP_SRC = os.path.join(_lib.CSRC_DIR, "selective_scan.hip")
 
+# steps per entry of the chunk-state output (the reference binding's chunk,
+# external/mamba/csrc/selective_scan/selective_scan.cpp:307)
+CHUNK = 2048
+
 
 def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Tensor,
               x: torch.Tensor) -> torch.Tensor:
@@ -61,7 +65,10 @@ def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Ten
     return y
 
 
-def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last_state):
+def _normalise(u, delta, A, B, C, D, z, delta_bias):
+    """Checks shapes and brings the inputs to the layouts the kernels take:
+    last dims contiguous, B / C 4-D, A / D / delta_bias fp32, z in u's dtype,
+    delta and B / C in fp32 or u's dtype."""
     _lib.require_device(u, delta, A, B, C, D, z, delta_bias)
     if A.is_complex():
         raise NotImplementedError("complex A is not supported by the gfx950 selective scan")
@@ -109,11 +116,26 @@ def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last
         B = B.float()
     if C.dtype != B.dtype:
         C = C.to(B.dtype)
+    return u, delta, A, B, C, D, z, delta_bias
+
+
+def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last_state,
+                  want_prez=False, want_chunk_states=False):
+    u, delta, A, B, C, D, z, delta_bias = _normalise(u, delta, A, B, C, D, z, delta_bias)
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
     out = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=u.device)
     last_state = (torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device)
                   if want_last_state else None)
-    _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus)
-    return out, last_state, (u, delta, A, B, C, D, z, delta_bias)
+    prez = torch.empty_like(out) if want_prez else None
+    chunks = (torch.empty((batch, dim, (seqlen + CHUNK - 1) // CHUNK, dstate, 2), dtype=torch.float32,
+                          device=u.device) if want_chunk_states else None)
+    _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus,
+                        out_prez=prez, chunk_states=chunks)
+    saved = (u, delta, A, B, C, D, z, delta_bias)
+    if want_prez or want_chunk_states:
+        return out, last_state, saved, prez, chunks
+    return out, last_state, saved
 
 
 def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus):

@@ -207,12 +207,18 @@ int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targ
  *   B, C      : [batch, ngroups, dstate, seqlen], element type bc_dtype
  *   D, delta_bias : [dim] fp32 or NULL;  z may be NULL
  *   last_state: [batch, dim, dstate] fp32 or NULL
+ *   out_prez  : y + D u before the gate, like out (strides of out), or NULL
+ *               (the reference binding's `out` when z is given)
+ *   chunk_states: [batch, dim, ceil(seqlen / 2048), dstate, 2] fp32 or NULL:
+ *               per 2048-step chunk, the scan's running prefix from step 0 to
+ *               the chunk's last step, (prod exp(delta' A), h) per state (the
+ *               reference binding's `x`, selective_scan.cpp:307-313)
  * Strides are in elements. dim must be a multiple of ngroups; dstate <= 16.
  */
 int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           const void* B, const void* C, const float* D,
                           const void* z, const float* delta_bias,
-                          void* out, float* last_state,
+                          void* out, float* last_state, void* out_prez, float* chunk_states,
                           int64_t batch, int64_t dim, int64_t seqlen,
                           int64_t dstate, int64_t ngroups,
                           int64_t u_batch_stride, int64_t u_dim_stride,

@@ -251,6 +251,36 @@ def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     return (out, x) if return_last_state else out
 
 
+def selective_scan_chunk_states_ref(u, delta, A, B, delta_bias=None, delta_softplus=False,
+                                    chunk: int = 2048):
+    """The chunk-state output ``x`` of the reference's forward binding
+    (``selective_scan.cpp:307-313``; written at
+    ``selective_scan_fwd_kernel.cuh:241-258``): for every 2048-step chunk,
+    the running prefix of the scan from step 0 to the chunk's last step, the
+    pair (prod_s exp(delta'_s A), h) per state. float64, shape
+    ``[batch, dim, n_chunks, dstate, 2]`` (the reference's ``[batch, dim,
+    n_chunks, 2 * dstate]`` with interleaved pairs)."""
+    f = torch.float64
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    draw = delta.to(f) + (delta_bias.to(f)[..., None] if delta_bias is not None else 0.0)
+    dl = F.softplus(draw) if delta_softplus else draw
+    B4 = B.to(f).unsqueeze(1) if B.dim() == 3 else B.to(f)
+    Bd = B4.repeat_interleave(dim // B4.shape[1], dim=1)  # [b, d, n, l]
+    nch = (seqlen + chunk - 1) // chunk
+    out = torch.empty(batch, dim, nch, dstate, 2, dtype=f)
+    prod = torch.ones(batch, dim, dstate, dtype=f)
+    h = torch.zeros(batch, dim, dstate, dtype=f)
+    for l in range(seqlen):
+        a = torch.exp(dl[:, :, l, None] * A.to(f)[None])
+        prod = prod * a
+        h = a * h + (dl[:, :, l] * u[:, :, l].to(f))[..., None] * Bd[..., l]
+        if (l + 1) % chunk == 0 or l + 1 == seqlen:
+            out[:, :, l // chunk, :, 0] = prod
+            out[:, :, l // chunk, :, 1] = h
+    return out
+
+
 def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None,
                            delta_softplus=False):
     """Gradients of :func:`selective_scan_ref` (real A, variable B / C), in

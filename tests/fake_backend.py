@@ -112,12 +112,17 @@ def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ign
     grad_logits[:, :V].copy_(g)
 
 
-def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus):
+def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, out_prez=None,
+          chunk_states=None):
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
                                      return_last_state=True)
     out.copy_(o)
     if last_state is not None:
         last_state.copy_(last)
+    if out_prez is not None:
+        out_prez.copy_(ops.selective_scan_ref(u, delta, A, B, C, D, None, delta_bias, delta_softplus))
+    if chunk_states is not None:
+        chunk_states.copy_(ops.selective_scan_chunk_states_ref(u, delta, A, B, delta_bias, delta_softplus))
 
 
 def _scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz, dbias,

@@ -219,6 +219,40 @@ def test_selective_scan_fn_api(fake_backend):
                           rtol=1e-5, atol=1e-6)
 
 
+def test_selective_scan_cuda_binding_api(fake_backend):
+    """kernels.hip.selective_scan_cuda mirrors the reference binding's fwd /
+    bwd argument order and return lists (selective_scan.cpp:227-335, :339-490)."""
+    from kernels.hip import selective_scan_cuda
+    g = torch.Generator().manual_seed(5)
+    u = torch.randn(2, 4, 20, generator=g)
+    delta = 0.5 * torch.rand(2, 4, 20, generator=g)
+    A = -torch.rand(4, 8, generator=g)
+    B = torch.randn(2, 8, 20, generator=g)
+    C = torch.randn(2, 8, 20, generator=g)
+    D, z, bias = torch.randn(4, generator=g), torch.randn(2, 4, 20, generator=g), torch.rand(4, generator=g)
+    out, x, out_z = selective_scan_cuda.fwd(u, delta, A, B, C, D, z, bias, True)
+    assert x.shape == (2, 4, 1, 16) and x.dtype == torch.float32
+    assert torch.allclose(out, ops.selective_scan_ref(u, delta, A, B, C, D, None, bias, True))
+    assert torch.allclose(out_z, ops.selective_scan_ref(u, delta, A, B, C, D, z, bias, True))
+    xs = ops.selective_scan_chunk_states_ref(u, delta, A, B, bias, True)
+    assert torch.allclose(x.double(), xs.reshape(2, 4, 1, 16), rtol=1e-5, atol=1e-6)
+    out2, x2 = selective_scan_cuda.fwd(u, delta, A, B, C, None, None, None, False)
+    assert x2.shape == (2, 4, 1, 16)
+    dout = torch.randn(2, 4, 20, generator=g)
+    dz_buf = torch.empty(2, 4, 20)
+    res = selective_scan_cuda.bwd(u, delta, A, B, C, D, z, bias, dout, x, out, dz_buf, True, True)
+    assert len(res) == 9
+    ref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    for got, want in zip(res[:5], ref[:5]):
+        assert got.shape == want.shape and torch.allclose(got.double(), want, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(res[5].double(), ref[5], rtol=1e-5, atol=1e-6)   # dD
+    assert torch.allclose(res[6].double(), ref[7], rtol=1e-5, atol=1e-6)   # ddelta_bias
+    assert res[7] is dz_buf and torch.allclose(res[7].double(), ref[6], rtol=1e-5, atol=1e-6)
+    assert torch.allclose(res[8], out_z)
+    res = selective_scan_cuda.bwd(u, delta, A, B, C, None, None, None, dout, x2, out2, None, False, False)
+    assert len(res) == 7 and res[5] is None and res[6] is None
+
+
 # ---------------------------------------------------------------------------
 # Registry
 # ---------------------------------------------------------------------------

@@ -60,7 +60,7 @@ def test_argument_errors_return_codes(lib):
     assert rc == -2 and b"multiple" in lib.ak_last_error()
     rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0, None)
     assert rc == -2  # fp32 is not a matrix-core input type here
-    rc = _lib.load().ak_selective_scan_fwd(*([None] * 10), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
+    rc = _lib.load().ak_selective_scan_fwd(*([None] * 12), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     # zero-size work is a no-op success
     assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0

@@ -190,3 +190,54 @@ def test_c5_shape_backward():
         gv, rv = part[i].double(), refc[i]
         rt, at = tol[name]
         assert bool(((gv - rv).abs() <= at + rt * rv.abs()).all()), name
+
+
+@pytest.mark.parametrize("seqlen,fast", [(4196, False), (4096, True)])
+def test_binding_fwd_chunk_states_and_prez(seqlen, fast):
+    """kernels.hip.selective_scan_cuda.fwd on the GPU: ``out`` (before the
+    gate), ``out_z`` and the chunk states ``x`` over 3 (ragged) or 2 chunks of
+    2048 steps, against the oracles (float64 chunk states; the forward's
+    tolerance of the reference grid). The state entries at rtol 1e-3 of the
+    float64 prefix scan, the decay products at 1e-4 relative (they are
+    exp2(A log2(e) sum delta') rather than a product of exps)."""
+    need_gpu()
+    from kernels.hip import selective_scan_cuda
+    dim = 16 if fast else 5
+    u, delta, A, B, C, D, z, bias, _ = _inputs(2, dim, 16, seqlen, 1, torch.float32, 21)
+    A = A * 0.05  # keep the running decay products above fp32 underflow
+    say("binding fwd chunk states", seqlen, fast)
+    d = lambda t: t.to(DEV)
+    out, x, out_z = selective_scan_cuda.fwd(d(u), d(delta), d(A), d(B), d(C), d(D), d(z), d(bias), True)
+    nch = (seqlen + 2047) // 2048
+    assert x.shape == (2, dim, nch, 32) and x.dtype == torch.float32
+    xs = ops.selective_scan_chunk_states_ref(u, delta, A, B, bias, True).reshape(2, dim, nch, 32)
+    xg = x.double().cpu()
+    assert torch.allclose(xg[..., 1::2], xs[..., 1::2], rtol=1e-3, atol=1e-3)
+    assert torch.allclose(xg[..., 0::2], xs[..., 0::2], rtol=1e-4, atol=1e-30)
+    rt, at = GRID["tolerances"]["float32"]
+    ref_prez = ops.selective_scan_ref(u, delta, A, B, C, D, None, bias, True)
+    ref_z = ops.selective_scan_ref(u, delta, A, B, C, D, z, bias, True)
+    assert torch.allclose(out.cpu(), ref_prez, rtol=rt, atol=at)
+    assert torch.allclose(out_z.cpu(), ref_z, rtol=rt, atol=at)
+
+
+def test_binding_bwd_matches_autograd():
+    """selective_scan_cuda.bwd (the reference binding's return list) gives the
+    gradients selective_scan_fn's autograd gives, bit for bit (same kernels),
+    and writes dz into a caller buffer."""
+    need_gpu()
+    from kernels.hip import selective_scan_cuda
+    u, delta, A, B, C, D, z, bias, dout = _inputs(2, 32, 16, 512, 1, torch.bfloat16, 22)
+    B3, C3 = B[:, 0], C[:, 0]
+    say("binding bwd vs autograd")
+    auto = _gpu_grads(u, delta, A, B3, C3, D, z, bias, dout, True)
+    d = lambda t: t.to(DEV)
+    out, x, out_z = selective_scan_cuda.fwd(d(u), d(delta), d(A), d(B3), d(C3), d(D), d(z), d(bias), True)
+    dz_buf = torch.empty_like(d(z))
+    res = selective_scan_cuda.bwd(d(u), d(delta), d(A), d(B3), d(C3), d(D), d(z), d(bias), d(dout), x, out,
+                                  dz_buf, True, True)
+    order = (0, 1, 2, 3, 4, 5, 7, 6)  # binding: du ddelta dA dB dC dD ddelta_bias dz
+    for i, name in enumerate(NAMES):
+        assert torch.equal(res[order[i]].cpu(), auto[i]), name
+    assert res[7] is dz_buf
+    assert torch.equal(res[8], out_z)

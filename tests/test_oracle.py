@@ -426,3 +426,24 @@ def test_selective_scan_bwd_softplus_threshold_and_closed_forms():
     assert all(float(t.abs().max()) == 0.0 for t in zero)
     out3 = ops.selective_scan_bwd_ref(u, delta, A, B[:, 0], C[:, 0], dout)
     assert out3[3].shape == B[:, 0].shape and out3[4].shape == C[:, 0].shape
+
+
+def test_selective_scan_chunk_states_pinned():
+    """Chunk states (selective_scan.cpp:307-313): the state entry of chunk k
+    is the forward oracle's last_state over the prefix ending at chunk k; the
+    decay entry is the last_state of a scan with u = 0 started from ones
+    (h = prod a * h0). Chunk length 16 here, 2048 in the kernels."""
+    u, delta, A, B, C, D, z, bias = _scan_inputs(l=40, g=2, seed=12)
+    xs = ops.selective_scan_chunk_states_ref(u, delta, A, B, bias, True, chunk=16)
+    assert xs.shape == (2, 4, 3, 8, 2)
+    for k, end in enumerate((16, 32, 40)):
+        _, last = ops.selective_scan_ref(u[..., :end], delta[..., :end], A, B[..., :end], C[..., :end],
+                                         None, None, bias, True, return_last_state=True,
+                                         compute_dtype=torch.float64)
+        assert torch.allclose(xs[:, :, k, :, 1], last, rtol=1e-12, atol=1e-12)
+        _, prod = ops.selective_scan_ref(torch.zeros_like(u[..., :end]), delta[..., :end], A,
+                                         B[..., :end], C[..., :end], None, None, bias, True,
+                                         return_last_state=True,
+                                         initial_state=torch.ones(2, 4, 8, dtype=torch.float64),
+                                         compute_dtype=torch.float64)
+        assert torch.allclose(xs[:, :, k, :, 0], prod, rtol=1e-12, atol=1e-300)
