@@ -28,7 +28,10 @@
 namespace ak {
 namespace {
 
-constexpr int kBwdMaxGrid = 512;   // workgroups of the row pass
+// workgroups of the row pass: one per CU (a sweep at the C3 shape measured
+// 256 / 384 / 512 / 1024 workgroups at 94.8 / 104.4 / 97.3 / 99.9 us; fewer
+// workgroups also mean fewer partial weight-gradient rows to sum)
+constexpr int kBwdMaxGrid = 256;
 constexpr int kBwdMaxParts = 2048; // partial dw rows (kBwdMaxGrid x at most 4 row slots)
 
 template <typename T, bool ADD_DH, int VPT, int TPR>
