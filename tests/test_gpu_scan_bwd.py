@@ -241,3 +241,31 @@ def test_binding_bwd_matches_autograd():
         assert torch.equal(res[order[i]].cpu(), auto[i]), name
     assert res[7] is dz_buf
     assert torch.equal(res[8], out_z)
+
+
+def test_backward_strided_views():
+    """Inputs that are views (channel slices of wider tensors, B / C sliced
+    from a wider state axis): the forward and backward take their strides as
+    they are; gradients land in the viewed leaves' shapes."""
+    need_gpu()
+    u, delta, A, B, C, D, z, bias, dout = _inputs(2, 48, 16, 200, 1, torch.float32, 23)
+    say("mamba bwd strided views")
+    wide = lambda t: torch.cat([t, torch.zeros_like(t)], dim=1).to(DEV)
+    uw, dw, zw = wide(u), wide(delta), wide(z)
+    Bw = torch.cat([B, torch.zeros_like(B)], dim=2).to(DEV)   # [b, 1, 2n, l]
+    Cw = torch.cat([C, torch.zeros_like(C)], dim=2).to(DEV)
+    from kernels.hip.selective_scan import selective_scan_fn
+    uw.requires_grad_(); dw.requires_grad_(); zw.requires_grad_(); Bw.requires_grad_(); Cw.requires_grad_()
+    uv, dv, zv = uw[:, :48], dw[:, :48], zw[:, :48]
+    Bv, Cv = Bw[:, :, :16], Cw[:, :, :16]
+    assert not uv.is_contiguous() and not Bv.is_contiguous()
+    Ad, Dd, bd = A.to(DEV).requires_grad_(), D.to(DEV).requires_grad_(), bias.to(DEV).requires_grad_()
+    out = selective_scan_fn(uv, dv, Ad, Bv, Cv, Dd, zv, bd, True)
+    out.backward(dout.to(DEV))
+    ref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    got = [uw.grad[:, :48], dw.grad[:, :48], Ad.grad, Bw.grad[:, :, :16], Cw.grad[:, :, :16], Dd.grad,
+           zw.grad[:, :48], bd.grad]
+    _check([t.cpu() for t in got], ref, _tols("float32", True), (u, delta, A, B, C, D, z, bias))
+    for t in (uw, dw, zw):
+        assert float(t.grad[:, 48:].abs().max()) == 0.0
+    assert float(Bw.grad[:, :, 16:].abs().max()) == 0.0 and float(Cw.grad[:, :, 16:].abs().max()) == 0.0
