@@ -1,4 +1,5 @@
-// Mamba-1 selective scan forward and the diagonal linear recurrence, gfx950.
+// Mamba-1 selective scan forward and backward, and the diagonal linear
+// recurrence with its backward, gfx950.
 //
 // Mamba-1 (semantics of selective_scan_ref, external/mamba/mamba_ssm/ops/
 // selective_scan_interface.py:115-181, fp32 state):
@@ -21,6 +22,10 @@
 // tile in LDS as fp32, converted once per workgroup; each lane reads its
 // state's 64 B values once per tile. exp uses exp2 with A pre-scaled by
 // log2(e), like the reference kernel (selective_scan_fwd_kernel.cuh:173-177).
+// On request the forward also writes y + D u before the gate and, per
+// 2048-step chunk, the running prefix (decay product, state) of every state
+// (the reference binding's chunk-state tensor x). The backward's design is
+// described above mamba_scan_bwd_kernel.
 #include "ak_common.h"
 
 namespace ak {
