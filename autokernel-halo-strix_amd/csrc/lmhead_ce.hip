@@ -158,6 +158,17 @@ struct GradArgs {
   void* dz;                // [n_rows, ld_dz] element type T
   int64_t ld_dz;
   int64_t ignore_index;
+  float cap;               // logit softcap (> 0 with kCap; the forward uses it too)
+};
+
+// Logit softcap z' = cap * tanh(z / cap), evaluated without cancellation
+// through q = exp(2 z / cap) and r = 1 / (q + 1):
+//   z' - cap = -2 cap r,   1 - tanh^2 = 4 q r^2.
+// k2 = 2 log2(e) / cap and nc = -2 cap log2(e) are per-call constants.
+struct Cap {
+  float k2, nc;
+  __device__ __forceinline__ explicit Cap(float cap) : k2(2.0f * kLog2e / cap), nc(-2.0f * cap * kLog2e) {}
+  __device__ __forceinline__ float q(float z) const { return __builtin_amdgcn_exp2f(z * k2); }
 };
 
 // Partial of vocab tile vt, vocab half h (0/1), token t: part[(2 vt + h) * n_rows + t].
@@ -166,7 +177,9 @@ struct GradArgs {
 // half (vocab % 128 != 0, or unshifted tail tiles), so the epilogue masks
 // element by element; otherwise a wave's half is either wholly owned or
 // wholly skipped.
-template <typename T, bool kShift, bool kFineMask, bool kGrad>
+// kCap: logit softcap ga.cap. The forward partial of a tile is then (cap,
+// sum exp(z' - cap)): z' <= cap, so no max pass is needed.
+template <typename T, bool kShift, bool kFineMask, bool kGrad, bool kCap = false>
 __global__ void __launch_bounds__(kLThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* __restrict__ part,
                       int n_rows, int vocab, int d, int64_t ldh, int64_t ldw, int n_vt, int n_tt,
@@ -387,6 +400,7 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
         const int tok_c = min(tok, n_rows - 1);
         const bool tok_ok = tok >= t_own && tok < n_rows;
         const float lse2 = ga.lse[tok_c] * kLog2e;
+        const float cl2 = kCap ? ga.cap * kLog2e - lse2 : 0.0f;  // log2 of exp(cap - lse)
         const int64_t tg = ga.targets[tok_c];
         const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= vocab) ? NAN : gs);
         T* drow = dzp + (int64_t)tok_c * ga.ld_dz + v_first + wv * 128;
@@ -397,8 +411,19 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
           for (int g4 = 0; g4 < 4; ++g4) {
             float e[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              e[j] = __builtin_amdgcn_exp2f(fmaf(acc_read(acc[vb][tb][4 * g4 + j]), kLog2e, -lse2)) * st;
+            for (int j = 0; j < 4; ++j) {
+              const float z = acc_read(acc[vb][tb][4 * g4 + j]);
+              if constexpr (kCap) {
+                // softmax(z')_v * s_t * dz'/dz
+                const Cap cp(ga.cap);
+                const float q = cp.q(z);
+                const float r = __builtin_amdgcn_rcpf(q + 1.0f);
+                const float p = __builtin_amdgcn_exp2f(fmaf(cp.nc, r, cl2));
+                e[j] = p * st * (4.0f * q * r * r);
+              } else {
+                e[j] = __builtin_amdgcn_exp2f(fmaf(z, kLog2e, -lse2)) * st;
+              }
+            }
             const int x0 = vb * 32 + 8 * g4;  // row of e[0] in the half, as counted by lo / hi
             if constexpr (kFineMask) {
 #pragma unroll
@@ -448,6 +473,24 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
               x[vb][r] = (o >= lo && o < hi) ? x[vb][r] : -INFINITY;
             }
           }
+        if constexpr (kCap) {
+          // (cap, sum exp(z' - cap)) with exp(z' - cap) = exp2(nc r); masked
+          // rows (x = -inf) would give exp(-2 cap) and are dropped
+          const Cap cp(ga.cap);
+          float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const float e = __builtin_amdgcn_exp2f(cp.nc * __builtin_amdgcn_rcpf(cp.q(x[vb][r]) + 1.0f));
+              s4[r & 3] += (kTail && x[vb][r] == -INFINITY) ? 0.0f : e;
+            }
+          float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+          s += __shfl_xor(s, 32, 64);
+          res[tb] = MSPair{ga.cap, s};
+          __builtin_amdgcn_sched_barrier(0);
+          continue;
+        }
         float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int vb = 0; vb < 4; ++vb)
@@ -512,7 +555,7 @@ __global__ void __launch_bounds__(kRowsPerBlock * kRowGroups)
 lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
                       const MSPair* __restrict__ part, const int64_t* __restrict__ targets,
                       float* __restrict__ lse, float* __restrict__ losses, int n_rows, int vocab,
-                      int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index) {
+                      int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index, float cap) {
   constexpr int kPerWave = kRowsPerBlock / (kRowsPerBlock * kRowGroups / 64);  // tokens per wave
   __shared__ MSPair red[kRowGroups][kRowsPerBlock];
   __shared__ float tl[kRowsPerBlock];
@@ -604,7 +647,14 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
   float loss;
   if (t == ignore_index) loss = 0.0f;
   else if (t < 0 || t >= vocab) loss = NAN;
-  else loss = l - tl[r];
+  else {
+    float zt = tl[r];
+    if (cap > 0.0f) {
+      const Cap cp(cap);
+      zt = cap + cp.nc * kLn2 * __builtin_amdgcn_rcpf(cp.q(zt) + 1.0f);  // cap * tanh(zt / cap)
+    }
+    loss = l - zt;
+  }
   losses[row] = loss;
 }
 
@@ -663,8 +713,18 @@ lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, G
   acc = wave_sum(acc);
   if (lane == 0) {
     const float gs = ga.grad_loss[0] / ga.denom[0];
-    const float p = __builtin_amdgcn_exp2f((acc - ga.lse[tok]) * kLog2e);
-    static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tg] = from_f32<T>((p - 1.0f) * gs);
+    float g;
+    if (ga.cap > 0.0f) {
+      const Cap cp(ga.cap);
+      const float q = cp.q(acc);
+      const float r = __builtin_amdgcn_rcpf(q + 1.0f);
+      const float p = __builtin_amdgcn_exp2f(fmaf(cp.nc, r, (ga.cap - ga.lse[tok]) * kLog2e));
+      g = (p - 1.0f) * gs * (4.0f * q * r * r);
+    } else {
+      const float p = __builtin_amdgcn_exp2f((acc - ga.lse[tok]) * kLog2e);
+      g = (p - 1.0f) * gs;
+    }
+    static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tg] = from_f32<T>(g);
   }
 }
 
@@ -696,10 +756,22 @@ int cu_count() {
   return cached[dev];
 }
 
+template <typename T, bool kCap>
+void launch_tiles_fwd(const T* hp, const T* wp, MSPair* part, int n_rows, int vocab, int d,
+                      int64_t ldh, int64_t ldw, int n_vt, int n_tt, const GradArgs& ga, dim3 gd,
+                      dim3 bd, hipStream_t s) {
+  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0)
+    lmhead_ce_tile_kernel<T, true, false, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else if (vocab >= kTV && n_rows >= kTT)
+    lmhead_ce_tile_kernel<T, true, true, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else
+    lmhead_ce_tile_kernel<T, false, true, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+}
+
 template <typename T>
 void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* loss, float* lse,
                    float* losses, int64_t* n_valid, void* ws, int n_rows, int vocab, int d,
-                   int64_t ldh, int64_t ldw, int64_t ignore_index, hipStream_t s) {
+                   int64_t ldh, int64_t ldw, int64_t ignore_index, float cap, hipStream_t s) {
   const int n_vt = (vocab + kTV - 1) / kTV;
   const int n_tt = (n_rows + kTT - 1) / kTT;
   const int grid = min(n_vt * n_tt, cu_count());
@@ -710,17 +782,29 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
   const T* hp = static_cast<const T*>(h);
   const T* wp = static_cast<const T*>(w);
   const dim3 gd(grid), bd(kLThreads);
-  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0)
-    lmhead_ce_tile_kernel<T, true, false, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
-  else if (vocab >= kTV && n_rows >= kTT)
-    lmhead_ce_tile_kernel<T, true, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
+  GradArgs ga{};
+  ga.cap = cap;
+  if (cap > 0.0f)
+    launch_tiles_fwd<T, true>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
   else
-    lmhead_ce_tile_kernel<T, false, true, false><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, GradArgs{});
+    launch_tiles_fwd<T, false>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
   lmhead_ce_rows_kernel<T><<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
                              dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
-      hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index);
+      hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index, cap);
   lmhead_ce_mean_kernel<<<dim3(1), dim3(1024), 0, s>>>(lrow, targets, loss, n_valid, n_rows,
                                                       ignore_index);
+}
+
+template <typename T, bool kCap>
+void launch_tiles_bwd(const T* hp, const T* wp, int n_rows, int vocab, int d, int64_t ldh,
+                      int64_t ldw, int n_vt, int n_tt, const GradArgs& ga, bool vec_ok, dim3 gd,
+                      dim3 bd, hipStream_t s) {
+  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0 && vec_ok)
+    lmhead_ce_tile_kernel<T, true, false, true, kCap><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else if (vocab >= kTV && n_rows >= kTT)
+    lmhead_ce_tile_kernel<T, true, true, true, kCap><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  else
+    lmhead_ce_tile_kernel<T, false, true, true, kCap><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
 }
 
 template <typename T>
@@ -733,12 +817,10 @@ void launch_lmhead_bwd(const void* h, const void* w, const GradArgs& ga, int n_r
   const T* wp = static_cast<const T*>(w);
   const dim3 gd(grid), bd(kLThreads);
   const bool vec_ok = ga.ld_dz % 8 == 0 && aligned16(ga.dz);
-  if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0 && vec_ok)
-    lmhead_ce_tile_kernel<T, true, false, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
-  else if (vocab >= kTV && n_rows >= kTT)
-    lmhead_ce_tile_kernel<T, true, true, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+  if (ga.cap > 0.0f)
+    launch_tiles_bwd<T, true>(hp, wp, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, vec_ok, gd, bd, s);
   else
-    lmhead_ce_tile_kernel<T, false, true, true><<<gd, bd, 0, s>>>(hp, wp, nullptr, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+    launch_tiles_bwd<T, false>(hp, wp, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, vec_ok, gd, bd, s);
   lmhead_ce_grad_target_kernel<T><<<dim3((n_rows + 3) / 4), dim3(256), 0, s>>>(hp, wp, ga, n_rows, vocab, d, ldh, ldw);
 }
 
@@ -754,8 +836,10 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
                                 float* loss, float* lse, float* losses, int64_t* n_valid,
                                 void* workspace, size_t workspace_bytes, int64_t n_rows,
                                 int64_t vocab, int64_t d, int64_t ld_h, int64_t ld_w,
-                                int64_t ignore_index, int dtype, void* stream) {
+                                int64_t ignore_index, float softcap, int dtype, void* stream) {
   const char* name = "ak_lmhead_ce_fwd";
+  if (!(softcap >= 0.0f) || softcap == INFINITY)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: softcap must be finite and >= 0", name);
   if (dtype != AK_DTYPE_BF16 && dtype != AK_DTYPE_F16)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dtype must be bf16 or fp16", name);
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
@@ -781,10 +865,10 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
   hipStream_t s = ak_stream(stream);
   if (dtype == AK_DTYPE_BF16)
     ak::launch_lmhead<ak::bf16>(hidden, weight, targets, loss, lse, losses, n_valid, workspace,
-                                (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, s);
+                                (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap, s);
   else
     ak::launch_lmhead<ak::f16>(hidden, weight, targets, loss, lse, losses, n_valid, workspace,
-                               (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, s);
+                               (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap, s);
   return ak_check_launch(name);
 }
 
@@ -792,8 +876,10 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
                                 const float* lse, const float* grad_loss, const float* denom,
                                 void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
                                 int64_t d, int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                                int dtype, void* stream) {
+                                float softcap, int dtype, void* stream) {
   const char* name = "ak_lmhead_ce_bwd";
+  if (!(softcap >= 0.0f) || softcap == INFINITY)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: softcap must be finite and >= 0", name);
   if (dtype != AK_DTYPE_BF16 && dtype != AK_DTYPE_F16)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dtype must be bf16 or fp16", name);
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
@@ -817,7 +903,7 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
                         "%s: hidden and weight must be 16-byte aligned, grad_logits element-aligned", name);
   const int64_t n_tiles = ((vocab + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
   if (n_tiles > 0x7FFFFFFF) return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many tiles", name);
-  ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index};
+  ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index, softcap};
   hipStream_t s = ak_stream(stream);
   if (dtype == AK_DTYPE_BF16)
     ak::launch_lmhead_bwd<ak::bf16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);

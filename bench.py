@@ -213,6 +213,19 @@ def make_case(name):
                                           s["ws"], -100)
         return Case(name, "C4 lm-head + CE bf16 [8192, 768] x [50304, 768]", "mfma", C4_FLOP, 8192,
                     launch, sets, "lmhead_ce_tile_kernel")
+    if name == "c4s":
+        cpu = gen_c4()
+        sets = _replicate(cpu, 2)
+        wsb = _lib.lmhead_ce_workspace_bytes(8192, 50304)
+        for s in sets:
+            s["loss"] = torch.empty((), dtype=torch.float32, device="cuda")
+            s["lse"] = torch.empty(8192, dtype=torch.float32, device="cuda")
+            s["nv"] = torch.empty(1, dtype=torch.int64, device="cuda")
+            s["ws"] = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        launch = lambda s: _lib.lmhead_ce(s["h"], s["W"], s["t"], s["loss"], s["lse"], None, s["nv"],
+                                          s["ws"], -100, 30.0)
+        return Case(name, "C4 lm-head + CE bf16 with logit softcap 30 (the reference's usual setting)",
+                    "mfma", C4_FLOP, 8192, launch, sets, "lmhead_ce_tile_kernel (softcap)")
     if name == "c4b":
         from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_backward, lmhead_ce_forward
         cpu = gen_c4()
@@ -335,6 +348,12 @@ def cpu_baseline(name, budget_s=4.0):
         h, t_ = c["h"][:rows], c["t"][:rows]
         t = timed(lambda: ops.lmhead_ce_ref(h, c["W"], t_), 3)
         return 2 * rows * 50304 * 768 / t / 1e12, "TFLOP/s", f"{rows} of 8192 rows of C4 (fp32 GEMM per 4096-column vocab chunk)"
+    if name == "c4s":
+        c = gen_c4()
+        rows = 64
+        h, t_ = c["h"][:rows], c["t"][:rows]
+        t = timed(lambda: ops.lmhead_ce_ref(h, c["W"], t_, softcap=30.0), 3)
+        return 2 * rows * 50304 * 768 / t / 1e12, "TFLOP/s", f"{rows} of 8192 rows of C4 with softcap 30 (fp32 GEMM per 4096-column vocab chunk)"
     if name == "c4b":
         c = gen_c4()
         rows = 32
@@ -371,7 +390,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4b,c5,c5b")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "

@@ -158,7 +158,10 @@ int ak_ce_bwd_tiny(const void* logits, const int64_t* targets,
  * accepted; d must be a multiple of 64, the rows of hidden and weight
  * 16-byte aligned and their pitches below 2^23 elements. workspace must
  * hold ak_lmhead_ce_workspace_bytes() bytes. logit[i, target[i]] is
- * computed as its own fp32-accumulated dot product.
+ * computed as its own fp32-accumulated dot product. softcap > 0 replaces
+ * every logit z by softcap * tanh(z / softcap) before the logsumexp and the
+ * target term (the logit_softcap of kernels/ce_fused.py:236-260 and
+ * chunked_linear_cross_entropy.py:20, 185); 0 disables it.
  */
 size_t ak_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab);
 int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targets,
@@ -166,7 +169,7 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
                      void* workspace, size_t workspace_bytes,
                      int64_t n_rows, int64_t vocab, int64_t d,
                      int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                     int dtype, void* stream);
+                     float softcap, int dtype, void* stream);
 
 /*
  * Fused lm-head + cross-entropy backward, first half: the gradient of the
@@ -185,14 +188,16 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
  * synchronisation). Same shape rules as ak_lmhead_ce_fwd; ld_gl >= vocab,
  * element type dtype (16-byte stores when ld_gl is a multiple of 8 and
  * grad_logits is 16-byte aligned, element stores otherwise). Only the first
- * vocab entries of each row are written.
+ * vocab entries of each row are written. With softcap > 0 the gradient is
+ * taken through the softcap (times 1 - tanh^2(z / softcap)), lse being the
+ * forward's logsumexp of the capped logits.
  */
 int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
                      const float* lse, const float* grad_loss, const float* denom,
                      void* grad_logits, int64_t ld_gl,
                      int64_t n_rows, int64_t vocab, int64_t d,
                      int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                     int dtype, void* stream);
+                     float softcap, int dtype, void* stream);
 
 /*
  * Mamba-1 selective scan forward (selective_scan_fn semantics).

@@ -167,13 +167,14 @@ def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int =
 
 
 def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
-                  ignore_index: int = -100, vocab_chunk: int = 4096):
+                  ignore_index: int = -100, vocab_chunk: int = 4096, softcap: float = 0.0):
     """Linear + CE without materialising all logits (fp32 arithmetic).
 
     Follows ``kernels/hip/chunked_linear_cross_entropy.py:72-75`` (n_valid),
     ``:135-140`` (loss = sum / n_valid) and ``kernels/ce_fused.py:236-260``
-    (per-row loss), streaming the vocabulary in ``vocab_chunk`` columns with an
-    online (max, sum) merge. Returns ``(loss, lse, losses)``.
+    (per-row loss, logit softcap ``softcap * tanh(z / softcap)`` when
+    ``softcap > 0``), streaming the vocabulary in ``vocab_chunk`` columns with
+    an online (max, sum) merge. Returns ``(loss, lse, losses)``.
     """
     h = hidden.float()
     V = weight.shape[0]
@@ -184,7 +185,7 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
     xt = torch.zeros(n)
     for v0 in range(0, V, vocab_chunk):
         v1 = min(V, v0 + vocab_chunk)
-        logits = h @ weight[v0:v1].float().t()
+        logits = _capped(h @ weight[v0:v1].float().t(), softcap)
         cm = logits.max(dim=-1).values
         nm = torch.maximum(m, cm)
         s = s * torch.exp(m - nm) + torch.exp(logits - nm[:, None]).sum(-1)

@@ -56,10 +56,14 @@ def test_argument_errors_return_codes(lib):
     assert rc == -2 and b"dtype" in lib.ak_last_error()
     rc = lib.ak_softmax_fwd(None, None, 4, 8, 4, 8, 0, None)   # pitch < cols
     assert rc == -1 and b"pitch" in lib.ak_last_error()
-    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 100, 100, 100, -100, 2, None)
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 100, 100, 100, -100, 0.0, 2, None)
     assert rc == -2 and b"multiple" in lib.ak_last_error()
-    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0, None)
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0.0, 0, None)
     assert rc == -2  # fp32 is not a matrix-core input type here
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, -1.0, 2, None)
+    assert rc == -1 and b"softcap" in lib.ak_last_error()
+    rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, float("nan"), 2, None)
+    assert rc == -1 and b"softcap" in lib.ak_last_error()
     rc = _lib.load().ak_selective_scan_fwd(*([None] * 12), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     # zero-size work is a no-op success

@@ -19,9 +19,10 @@ pytestmark = gpu
 DEV = "cuda"
 
 
-def _run(h, W, t, ignore_index=-100):
+def _run(h, W, t, ignore_index=-100, softcap=0.0):
     from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_forward
-    return lmhead_ce_forward(h.to(DEV), W.to(DEV), t.to(DEV), ignore_index, return_losses=True)
+    return lmhead_ce_forward(h.to(DEV), W.to(DEV), t.to(DEV), ignore_index, return_losses=True,
+                             softcap=softcap)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -43,6 +44,30 @@ def test_lmhead_ce_matches_oracle(dtype, n, vocab, d):
     say("lmhead_ce", dtype, n, vocab, d)
     loss, lse, nv, losses = _run(h, W, t)
     rloss, rlse, rlosses = ops.lmhead_ce_ref(h, W, t)
+    assert int(nv) == int((t != -100).sum())
+    assert torch.allclose(lse.double().cpu(), rlse.double(), rtol=1e-4, atol=1e-4)
+    assert torch.allclose(losses.double().cpu(), rlosses.double(), rtol=1e-3, atol=1e-3)
+    assert abs(float(loss) - float(rloss)) <= 1e-3 * abs(float(rloss)) + 1e-6
+    assert bool((losses.cpu()[t == -100] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cap", [30.0, 2.0])
+@pytest.mark.parametrize("n,vocab,d", [(5, 300, 64), (257, 4097, 768), (300, 1152, 128), (700, 640, 64),
+                                       (512, 50304, 768)])
+def test_lmhead_ce_softcap_matches_oracle(dtype, cap, n, vocab, d):
+    """The logit softcap in the fused kernel (every tile-kernel variant)
+    against the streamed fp32 oracle with the same softcap; cap 2 saturates
+    most logits (weights scaled up), cap 30 is the reference's usual value."""
+    need_gpu()
+    g = torch.Generator().manual_seed(n * 5 + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = ((0.5 if cap < 10 else 0.05) * torch.randn(vocab, d, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[: max(0, n // 10)] = -100
+    say("lmhead_ce softcap", dtype, cap, n, vocab, d)
+    loss, lse, nv, losses = _run(h, W, t, softcap=cap)
+    rloss, rlse, rlosses = ops.lmhead_ce_ref(h, W, t, softcap=cap)
     assert int(nv) == int((t != -100).sum())
     assert torch.allclose(lse.double().cpu(), rlse.double(), rtol=1e-4, atol=1e-4)
     assert torch.allclose(losses.double().cpu(), rlosses.double(), rtol=1e-3, atol=1e-3)
@@ -128,13 +153,18 @@ def test_chunked_linear_ce_fwd_bwd(dtype, softcap, zw):
 # Fused backward: dL/dlogits from the matrix cores, then two GEMMs
 # ---------------------------------------------------------------------------
 
-def _dz_ref(h, W, t, lse, scale, ignore_index=-100):
-    """float64 softmax(h W^T) - onehot, times scale, from the GPU forward's lse."""
+def _dz_ref(h, W, t, lse, scale, ignore_index=-100, softcap=0.0):
+    """float64 softmax(h W^T) - onehot, times scale, from the GPU forward's lse
+    (through the softcap z' = c tanh(z / c), times 1 - tanh^2, when c > 0)."""
     z = h.double() @ W.double().t()
+    dcap = 1.0
+    if softcap > 0:
+        th = torch.tanh(z / softcap)
+        z, dcap = softcap * th, 1 - th * th
     p = torch.exp(z - lse.double()[:, None])
     tc = t.clamp(min=0)
     p[torch.arange(len(t)), tc] -= 1.0
-    p = p * scale
+    p = p * scale * dcap
     p[t == ignore_index] = 0.0
     return p
 
@@ -171,6 +201,67 @@ def test_lmhead_ce_grad_logits(dtype, n, vocab, d):
     assert bool((got[t == -100] == 0).all())
     if ldv > vocab:
         assert bool((dz[:, vocab:].float().cpu() == 5.0).all())  # row padding untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,vocab,d", [(5, 300, 64), (257, 4097, 768), (300, 1152, 128), (512, 50304, 768)])
+def test_lmhead_ce_grad_logits_softcap(dtype, n, vocab, d):
+    """dL/dlogits through the softcap (cap 3: logits up to about 3 cap, so
+    1 - tanh^2 spans [0.01, 1]) against float64, to one rounding of the element
+    type plus 2e-6 of the scale (the fp32 arithmetic of q, r and exp)."""
+    need_gpu()
+    from kernels.hip import _lib
+    cap = 3.0
+    g = torch.Generator().manual_seed(n * 3 + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = (0.3 * torch.randn(vocab, d, generator=g) / math.sqrt(d / 64)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[: max(0, n // 10)] = -100
+    say("lmhead_ce grad logits softcap", dtype, n, vocab, d)
+    loss, lse, nv, _ = _run(h, W, t, softcap=cap)
+    denom = nv.to(torch.float32).clamp(min=1.0).reshape(1)
+    gl = torch.tensor([0.75], device=DEV)
+    dz = torch.empty((n, vocab), dtype=dtype, device=DEV)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, gl, denom, dz, -100, cap)
+    scale = 0.75 / float(denom)
+    ref = _dz_ref(h, W, t, lse.cpu(), scale, softcap=cap)
+    got = dz.double().cpu()
+    err = (got - ref).abs()
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    floor = 2e-6 * scale + (2.0 ** -25 if dtype == torch.float16 else 0.0)
+    assert bool((err <= eps * ref.abs() + floor).all()), float((err / (eps * ref.abs() + floor)).max())
+    assert bool((got[t == -100] == 0).all())
+
+
+def test_c4_full_size_softcap():
+    """C4 with the reference's usual logit softcap (30): forward on a row
+    subset against the oracle, the mean from GPU lse and exact capped target
+    logits; backward rows of dlogits against float64; deterministic."""
+    need_gpu()
+    import bench
+    from kernels.hip import _lib
+    c = bench.gen_c4()
+    say("C4 lm-head + CE with softcap 30")
+    loss, lse, nv, losses = _run(c["h"], c["W"], c["t"], softcap=30.0)
+    loss2, lse2, _, _ = _run(c["h"], c["W"], c["t"], softcap=30.0)
+    assert torch.equal(lse, lse2) and torch.equal(loss, loss2)
+    t = c["t"]
+    valid = t != -100
+    idx = torch.randperm(8192, generator=torch.Generator().manual_seed(3))[:256].sort().values
+    _, rlse, rl = ops.lmhead_ce_ref(c["h"][idx], c["W"], t[idx], softcap=30.0)
+    assert torch.allclose(lse.cpu()[idx].double(), rlse.double(), rtol=1e-4)
+    assert torch.allclose(losses.cpu()[idx].double(), rl.double(), rtol=1e-3, atol=1e-3)
+    xt = 30.0 * torch.tanh((c["h"].float() * c["W"][t.clamp(min=0)].float()).sum(-1).double() / 30.0)
+    ref_loss = ((lse.cpu().double() - xt) * valid.double()).sum() / valid.sum()
+    assert abs(float(loss) - float(ref_loss)) <= 1e-3 * abs(float(ref_loss))
+    denom = nv.to(torch.float32).clamp(min=1.0).reshape(1)
+    one = torch.ones(1, device=DEV)
+    dz = torch.empty(8192, 50304, dtype=torch.bfloat16, device=DEV)
+    _lib.lmhead_ce_bwd(c["h"].to(DEV), c["W"].to(DEV), t.to(DEV), lse, one, denom, dz, -100, 30.0)
+    scale = 1.0 / float(denom)
+    ref = _dz_ref(c["h"][idx], c["W"], t[idx], lse.cpu()[idx], scale, softcap=30.0)
+    got = dz[idx.to(DEV)].double().cpu()
+    assert bool(((got - ref).abs() <= 2.0 ** -8 * ref.abs() + 2e-6 * scale).all())
 
 
 def test_lmhead_ce_grad_logits_pitch_fallback():

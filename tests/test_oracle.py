@@ -447,3 +447,24 @@ def test_selective_scan_chunk_states_pinned():
                                          initial_state=torch.ones(2, 4, 8, dtype=torch.float64),
                                          compute_dtype=torch.float64)
         assert torch.allclose(xs[:, :, k, :, 0], prod, rtol=1e-12, atol=1e-300)
+
+
+def test_lmhead_ce_ref_softcap_matches_materialised_ce():
+    """The streamed lm-head oracle with a logit softcap equals the CE row
+    oracle (pinned to F.cross_entropy of the capped logits) on materialised
+    logits, for every vocab chunking."""
+    g = torch.Generator().manual_seed(17)
+    h = torch.randn(40, 32, generator=g)
+    W = 2.0 * torch.randn(300, 32, generator=g)
+    t = torch.randint(0, 300, (40,), generator=g)
+    t[:3] = -100
+    logits = h @ W.t()
+    per, lse, _, _ = ops.ce_rows_ref(logits, t, softcap=5.0)
+    for chunk in (64, 300, 4096):
+        loss, lse2, per2 = ops.lmhead_ce_ref(h, W, t, vocab_chunk=chunk, softcap=5.0)
+        assert torch.allclose(lse2, lse, rtol=1e-5, atol=1e-5)
+        assert torch.allclose(per2, per, rtol=1e-5, atol=1e-5)
+        assert torch.allclose(loss, ops.ce_mean_ref(per, t), rtol=1e-5)
+    capped = 5.0 * torch.tanh(logits / 5.0)
+    ref = F.cross_entropy(capped, t, ignore_index=-100)
+    assert torch.allclose(ops.lmhead_ce_ref(h, W, t, softcap=5.0)[0], ref, rtol=1e-5)
