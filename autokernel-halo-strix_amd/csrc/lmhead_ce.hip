@@ -16,6 +16,9 @@
 // ignored tokens contribute 0 and are excluded from the mean's
 // denominator, which is clamped to >= 1). The logsumexp runs over all
 // `vocab` columns (padded vocab entries are not masked, as in the reference).
+// Options: a logit softcap z' = cap tanh(z / cap), and label smoothing a
+// (loss = lse - (1 - a) z'_t - a mean(z'); the tile kernel then also writes
+// per-partial sums of z', merged by the row kernel in a fixed order).
 //
 // Tile kernel mechanics:
 // * Persistent: one 256-thread workgroup per CU walks its tiles in an
@@ -146,7 +149,8 @@ __device__ __forceinline__ int tile_first(int own, int n) {
   return kShift ? min(own, n - 256) : own;
 }
 
-// Backward (kGrad) outputs: dz[t, v] = softmax(logits)[t, v] * s_t with
+// Backward (kGrad) outputs: dz[t, v] = (softmax(logits)[t, v] - a / vocab) * s_t
+// (a = label smoothing, and times 1 - tanh^2 under a softcap) with
 // s_t = grad_loss / denom for a counted token, 0 for an ignored one and NaN
 // for a target outside [0, vocab); the target entry itself is written
 // afterwards by lmhead_ce_grad_target_kernel.
@@ -159,6 +163,8 @@ struct GradArgs {
   int64_t ld_dz;
   int64_t ignore_index;
   float cap;               // logit softcap (> 0 with kCap; the forward uses it too)
+  float ls;                // label smoothing alpha (0 = off)
+  float* zsum;             // forward with label smoothing: per-partial sums of the logits
 };
 
 // Logit softcap z' = cap * tanh(z / cap), evaluated without cancellation
@@ -179,7 +185,10 @@ struct Cap {
 // wholly skipped.
 // kCap: logit softcap ga.cap. The forward partial of a tile is then (cap,
 // sum exp(z' - cap)): z' <= cap, so no max pass is needed.
-template <typename T, bool kShift, bool kFineMask, bool kGrad, bool kCap = false>
+// kLs (forward): label smoothing; the tile also writes the sum of its (capped)
+// logits per token to ga.zsum, laid out as the partials. A template flag, so
+// that the kernels without it carry no extra register pressure.
+template <typename T, bool kShift, bool kFineMask, bool kGrad, bool kCap = false, bool kLs = false>
 __global__ void __launch_bounds__(kLThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* __restrict__ part,
                       int n_rows, int vocab, int d, int64_t ldh, int64_t ldw, int n_vt, int n_tt,
@@ -403,6 +412,7 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
         const float cl2 = kCap ? ga.cap * kLog2e - lse2 : 0.0f;  // log2 of exp(cap - lse)
         const int64_t tg = ga.targets[tok_c];
         const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= vocab) ? NAN : gs);
+        const float nls = -(ga.ls / (float)vocab) * st;  // label smoothing's uniform term
         T* drow = dzp + (int64_t)tok_c * ga.ld_dz + v_first + wv * 128;
 #pragma unroll
         for (int vb = 0; vb < 4; ++vb) {
@@ -419,9 +429,9 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
                 const float q = cp.q(z);
                 const float r = __builtin_amdgcn_rcpf(q + 1.0f);
                 const float p = __builtin_amdgcn_exp2f(fmaf(cp.nc, r, cl2));
-                e[j] = p * st * (4.0f * q * r * r);
+                e[j] = fmaf(p, st, nls) * (4.0f * q * r * r);
               } else {
-                e[j] = __builtin_amdgcn_exp2f(fmaf(z, kLog2e, -lse2)) * st;
+                e[j] = fmaf(__builtin_amdgcn_exp2f(fmaf(z, kLog2e, -lse2)), st, nls);
               }
             }
             const int x0 = vb * 32 + 8 * g4;  // row of e[0] in the half, as counted by lo / hi
@@ -457,6 +467,7 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
     }
     MSPair* prow = part + (int64_t)(2 * vt + wv) * n_rows;
     MSPair res[4];
+    float zres[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // label smoothing: sums of the (capped) logits
     auto epilogue = [&](auto tail_tag) {
       constexpr bool kTail = decltype(tail_tag)::value;
 #pragma unroll
@@ -475,21 +486,37 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
           }
         if constexpr (kCap) {
           // (cap, sum exp(z' - cap)) with exp(z' - cap) = exp2(nc r); masked
-          // rows (x = -inf) would give exp(-2 cap) and are dropped
+          // rows (x = -inf) would give exp(-2 cap) and are dropped. With label
+          // smoothing the capped logits z' = cap - 2 cap r are summed too.
           const Cap cp(ga.cap);
-          float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, z4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int vb = 0; vb < 4; ++vb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const float e = __builtin_amdgcn_exp2f(cp.nc * __builtin_amdgcn_rcpf(cp.q(x[vb][r]) + 1.0f));
-              s4[r & 3] += (kTail && x[vb][r] == -INFINITY) ? 0.0f : e;
+              const float rr = __builtin_amdgcn_rcpf(cp.q(x[vb][r]) + 1.0f);
+              const bool live = !(kTail && x[vb][r] == -INFINITY);
+              s4[r & 3] += live ? __builtin_amdgcn_exp2f(cp.nc * rr) : 0.0f;
+              if constexpr (kLs) z4[r & 3] += live ? fmaf(-2.0f * ga.cap, rr, ga.cap) : 0.0f;
             }
           float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
           s += __shfl_xor(s, 32, 64);
           res[tb] = MSPair{ga.cap, s};
+          if constexpr (kLs) {
+            const float z = (z4[0] + z4[1]) + (z4[2] + z4[3]);
+            zres[tb] = z + __shfl_xor(z, 32, 64);
+          }
           __builtin_amdgcn_sched_barrier(0);
           continue;
+        }
+        if constexpr (kLs) {
+          float z4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int vb = 0; vb < 4; ++vb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) z4[r & 3] += (kTail && x[vb][r] == -INFINITY) ? 0.0f : x[vb][r];
+          const float z = (z4[0] + z4[1]) + (z4[2] + z4[3]);
+          zres[tb] = z + __shfl_xor(z, 32, 64);
         }
         float m4[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -524,7 +551,10 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
       const int tok = t_first + wt * 128 + tb * 32 + fr;
-      if (lane < 32 && tok >= t_own && tok < n_rows) prow[tok] = res[tb];
+      if (lane < 32 && tok >= t_own && tok < n_rows) {
+        prow[tok] = res[tb];
+        if constexpr (kLs) ga.zsum[(int64_t)(2 * vt + wv) * n_rows + tok] = zres[tb];
+      }
     }
   }
   // drain the ring's trailing (unused) loads before the workgroup exits
@@ -555,9 +585,11 @@ __global__ void __launch_bounds__(kRowsPerBlock * kRowGroups)
 lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
                       const MSPair* __restrict__ part, const int64_t* __restrict__ targets,
                       float* __restrict__ lse, float* __restrict__ losses, int n_rows, int vocab,
-                      int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index, float cap) {
+                      int d, int64_t ldh, int64_t ldw, int n_vt, int64_t ignore_index, float cap,
+                      const float* __restrict__ zsum, float ls) {
   constexpr int kPerWave = kRowsPerBlock / (kRowsPerBlock * kRowGroups / 64);  // tokens per wave
   __shared__ MSPair red[kRowGroups][kRowsPerBlock];
+  __shared__ float redz[kRowGroups][kRowsPerBlock];
   __shared__ float tl[kRowsPerBlock];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -622,6 +654,7 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
   const int grp = threadIdx.x / kRowsPerBlock;
   const int row = row0 + r;
   MSPair st{-INFINITY, 0.0f};
+  float zs = 0.0f;  // label smoothing: sum of the (capped) logits, fixed order
   if (row < n_rows) {
     // 8 partials in flight per thread, then merged in order
     const int n_part = 2 * n_vt;
@@ -635,12 +668,20 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (v0 + i * kRowGroups < n_part) st = ms_merge(st, buf[i]);
+      if (zsum) {
+        for (int i = 0; i < 8; ++i)
+          if (v0 + i * kRowGroups < n_part) zs += zsum[(int64_t)(v0 + i * kRowGroups) * n_rows + row];
+      }
     }
   }
   red[grp][r] = st;
+  redz[grp][r] = zs;
   __syncthreads();
   if (grp != 0 || row >= n_rows) return;
-  for (int g = 1; g < kRowGroups; ++g) st = ms_merge(st, red[g][r]);
+  for (int g = 1; g < kRowGroups; ++g) {
+    st = ms_merge(st, red[g][r]);
+    zs += redz[g][r];
+  }
   const float l = st.m + fast_log(st.s);
   lse[row] = l;
   const int64_t t = targets[row];
@@ -653,7 +694,8 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
       const Cap cp(cap);
       zt = cap + cp.nc * kLn2 * __builtin_amdgcn_rcpf(cp.q(zt) + 1.0f);  // cap * tanh(zt / cap)
     }
-    loss = l - zt;
+    // label smoothing (kernels/ce_fused.py:251-256): lse - (1 - a) z_t - a mean(z)
+    loss = zsum ? l - (1.0f - ls) * zt - ls * zs / (float)vocab : l - zt;
   }
   losses[row] = loss;
 }
@@ -688,7 +730,7 @@ lmhead_ce_mean_kernel(const float* __restrict__ losses, const int64_t* __restric
   }
 }
 
-// Target entries of the backward: dz[t, target[t]] = (exp(z_t - lse_t) - 1) * s_t
+// Target entries of the backward: dz[t, target[t]] = (exp(z_t - lse_t) - (1 - a) - a / vocab) * s_t
 // with z_t = hidden[t] . weight[target[t]] as an fp32 dot product (one wave per
 // token, as the row kernel computes target logits). Ignored tokens and targets
 // outside [0, vocab) keep what the tile kernel wrote (0 and NaN rows).
@@ -719,10 +761,10 @@ lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, G
       const float q = cp.q(acc);
       const float r = __builtin_amdgcn_rcpf(q + 1.0f);
       const float p = __builtin_amdgcn_exp2f(fmaf(cp.nc, r, (ga.cap - ga.lse[tok]) * kLog2e));
-      g = (p - 1.0f) * gs * (4.0f * q * r * r);
+      g = (p - (1.0f - ga.ls) - ga.ls / (float)vocab) * gs * (4.0f * q * r * r);
     } else {
       const float p = __builtin_amdgcn_exp2f((acc - ga.lse[tok]) * kLog2e);
-      g = (p - 1.0f) * gs;
+      g = (p - (1.0f - ga.ls) - ga.ls / (float)vocab) * gs;
     }
     static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tg] = from_f32<T>(g);
   }
@@ -731,7 +773,7 @@ lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, G
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t part, losses, total;
+  size_t part, losses, zsum, total;
 };
 
 WsLayout ws_layout(int64_t n_rows, int64_t vocab) {
@@ -739,7 +781,8 @@ WsLayout ws_layout(int64_t n_rows, int64_t vocab) {
   WsLayout w;
   w.part = 0;
   w.losses = align256((size_t)2 * n_vt * n_rows * sizeof(MSPair));
-  w.total = w.losses + align256((size_t)n_rows * 4);
+  w.zsum = w.losses + align256((size_t)n_rows * 4);
+  w.total = w.zsum + align256((size_t)2 * n_vt * n_rows * 4);
   return w;
 }
 
@@ -756,22 +799,23 @@ int cu_count() {
   return cached[dev];
 }
 
-template <typename T, bool kCap>
+template <typename T, bool kCap, bool kLs>
 void launch_tiles_fwd(const T* hp, const T* wp, MSPair* part, int n_rows, int vocab, int d,
                       int64_t ldh, int64_t ldw, int n_vt, int n_tt, const GradArgs& ga, dim3 gd,
                       dim3 bd, hipStream_t s) {
   if (vocab >= kTV && n_rows >= kTT && vocab % 128 == 0)
-    lmhead_ce_tile_kernel<T, true, false, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+    lmhead_ce_tile_kernel<T, true, false, false, kCap, kLs><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
   else if (vocab >= kTV && n_rows >= kTT)
-    lmhead_ce_tile_kernel<T, true, true, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+    lmhead_ce_tile_kernel<T, true, true, false, kCap, kLs><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
   else
-    lmhead_ce_tile_kernel<T, false, true, false, kCap><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
+    lmhead_ce_tile_kernel<T, false, true, false, kCap, kLs><<<gd, bd, 0, s>>>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga);
 }
 
 template <typename T>
 void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* loss, float* lse,
                    float* losses, int64_t* n_valid, void* ws, int n_rows, int vocab, int d,
-                   int64_t ldh, int64_t ldw, int64_t ignore_index, float cap, hipStream_t s) {
+                   int64_t ldh, int64_t ldw, int64_t ignore_index, float cap, float ls,
+                   hipStream_t s) {
   const int n_vt = (vocab + kTV - 1) / kTV;
   const int n_tt = (n_rows + kTT - 1) / kTT;
   const int grid = min(n_vt * n_tt, cu_count());
@@ -784,13 +828,19 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
   const dim3 gd(grid), bd(kLThreads);
   GradArgs ga{};
   ga.cap = cap;
-  if (cap > 0.0f)
-    launch_tiles_fwd<T, true>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
+  ga.ls = ls;
+  ga.zsum = ls > 0.0f ? reinterpret_cast<float*>(base + L.zsum) : nullptr;
+  if (cap > 0.0f && ls > 0.0f)
+    launch_tiles_fwd<T, true, true>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
+  else if (cap > 0.0f)
+    launch_tiles_fwd<T, true, false>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
+  else if (ls > 0.0f)
+    launch_tiles_fwd<T, false, true>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
   else
-    launch_tiles_fwd<T, false>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
+    launch_tiles_fwd<T, false, false>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
   lmhead_ce_rows_kernel<T><<<dim3((n_rows + kRowsPerBlock - 1) / kRowsPerBlock),
                              dim3(kRowsPerBlock * kRowGroups), 0, s>>>(
-      hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index, cap);
+      hp, wp, part, targets, lse, lrow, n_rows, vocab, d, ldh, ldw, n_vt, ignore_index, cap, ga.zsum, ls);
   lmhead_ce_mean_kernel<<<dim3(1), dim3(1024), 0, s>>>(lrow, targets, loss, n_valid, n_rows,
                                                       ignore_index);
 }
@@ -836,10 +886,13 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
                                 float* loss, float* lse, float* losses, int64_t* n_valid,
                                 void* workspace, size_t workspace_bytes, int64_t n_rows,
                                 int64_t vocab, int64_t d, int64_t ld_h, int64_t ld_w,
-                                int64_t ignore_index, float softcap, int dtype, void* stream) {
+                                int64_t ignore_index, float softcap, float label_smoothing,
+                                int dtype, void* stream) {
   const char* name = "ak_lmhead_ce_fwd";
   if (!(softcap >= 0.0f) || softcap == INFINITY)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: softcap must be finite and >= 0", name);
+  if (!(label_smoothing >= 0.0f && label_smoothing <= 1.0f))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: label_smoothing must be in [0, 1]", name);
   if (dtype != AK_DTYPE_BF16 && dtype != AK_DTYPE_F16)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dtype must be bf16 or fp16", name);
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
@@ -865,10 +918,12 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
   hipStream_t s = ak_stream(stream);
   if (dtype == AK_DTYPE_BF16)
     ak::launch_lmhead<ak::bf16>(hidden, weight, targets, loss, lse, losses, n_valid, workspace,
-                                (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap, s);
+                                (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap,
+                                label_smoothing, s);
   else
     ak::launch_lmhead<ak::f16>(hidden, weight, targets, loss, lse, losses, n_valid, workspace,
-                               (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap, s);
+                               (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, ignore_index, softcap,
+                               label_smoothing, s);
   return ak_check_launch(name);
 }
 
@@ -876,10 +931,12 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
                                 const float* lse, const float* grad_loss, const float* denom,
                                 void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
                                 int64_t d, int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                                float softcap, int dtype, void* stream) {
+                                float softcap, float label_smoothing, int dtype, void* stream) {
   const char* name = "ak_lmhead_ce_bwd";
   if (!(softcap >= 0.0f) || softcap == INFINITY)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: softcap must be finite and >= 0", name);
+  if (!(label_smoothing >= 0.0f && label_smoothing <= 1.0f))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: label_smoothing must be in [0, 1]", name);
   if (dtype != AK_DTYPE_BF16 && dtype != AK_DTYPE_F16)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dtype must be bf16 or fp16", name);
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
@@ -903,7 +960,8 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
                         "%s: hidden and weight must be 16-byte aligned, grad_logits element-aligned", name);
   const int64_t n_tiles = ((vocab + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
   if (n_tiles > 0x7FFFFFFF) return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many tiles", name);
-  ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index, softcap};
+  ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index, softcap,
+                  label_smoothing, nullptr};
   hipStream_t s = ak_stream(stream);
   if (dtype == AK_DTYPE_BF16)
     ak::launch_lmhead_bwd<ak::bf16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);

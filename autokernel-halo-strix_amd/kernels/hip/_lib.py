@@ -58,9 +58,9 @@ _SIGNATURES = {
                        _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
     "ak_lmhead_ce_workspace_bytes": [_i64, _i64],
     "ak_lmhead_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                         _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int,
-                         _c_void_p],
-    "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _int, _c_void_p],
+                         _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
+                         _int, _c_void_p],
+    "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _f32, _int, _c_void_p],
     "ak_selective_scan_fwd": [_c_void_p] * 12 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
@@ -273,7 +273,7 @@ def lmhead_ce_workspace_bytes(n_rows: int, vocab: int) -> int:
 def lmhead_ce(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
               loss: torch.Tensor, lse: torch.Tensor, losses: Optional[torch.Tensor],
               n_valid: Optional[torch.Tensor], workspace: torch.Tensor, ignore_index: int,
-              softcap: float = 0.0) -> None:
+              softcap: float = 0.0, label_smoothing: float = 0.0) -> None:
     require_device(hidden, weight, targets, loss, lse, losses, n_valid, workspace)
     n_rows, d = hidden.shape
     vocab = weight.shape[0]
@@ -282,13 +282,15 @@ def lmhead_ce(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
             _ptr(hidden), _ptr(weight), _ptr(targets), _ptr(loss), _ptr(lse), _ptr(losses),
             _ptr(n_valid), _ptr(workspace), workspace.numel() * workspace.element_size(),
             n_rows, vocab, d, _rows_view(hidden, "hidden"), _rows_view(weight, "weight"),
-            int(ignore_index), float(softcap), dtype_code(hidden.dtype), _stream(hidden))
+            int(ignore_index), float(softcap), float(label_smoothing), dtype_code(hidden.dtype),
+            _stream(hidden))
     _check(rc, "ak_lmhead_ce_fwd")
 
 
 def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                   lse: torch.Tensor, grad_loss: torch.Tensor, denom: torch.Tensor,
-                  grad_logits: torch.Tensor, ignore_index: int, softcap: float = 0.0) -> None:
+                  grad_logits: torch.Tensor, ignore_index: int, softcap: float = 0.0,
+                  label_smoothing: float = 0.0) -> None:
     """dL/dlogits of the mean CE into ``grad_logits`` ``[n_rows, vocab]`` (row pitch a
     multiple of 4); ``grad_loss`` and ``denom`` are 1-element fp32 device tensors."""
     require_device(hidden, weight, targets, lse, grad_loss, denom, grad_logits)
@@ -299,7 +301,7 @@ def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
             _ptr(hidden), _ptr(weight), _ptr(targets), _ptr(lse), _ptr(grad_loss), _ptr(denom),
             _ptr(grad_logits), _rows_view(grad_logits, "grad_logits"), n_rows, vocab, d,
             _rows_view(hidden, "hidden"), _rows_view(weight, "weight"), int(ignore_index),
-            float(softcap), dtype_code(hidden.dtype), _stream(hidden))
+            float(softcap), float(label_smoothing), dtype_code(hidden.dtype), _stream(hidden))
     _check(rc, "ak_lmhead_ce_bwd")
 
 

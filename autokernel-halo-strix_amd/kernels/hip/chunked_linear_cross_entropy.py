@@ -5,7 +5,7 @@ Drop-in for the reference module ``kernels/hip/chunked_linear_cross_entropy.py``
 :50-175): same constructor arguments, same ``forward(hidden, weight,
 targets)`` contract, autograd for ``hidden`` and ``weight``.
 
-Forward (CE with or without the logit softcap, bf16/fp16, ``d % 64 == 0``):
+Forward (bf16/fp16, ``d % 64 == 0``; any softcap and label smoothing):
 one fused kernel,
 ``ak_lmhead_ce_fwd`` (``csrc/lmhead_ce.hip``), computes ``hidden @ weight^T``
 tile by tile on the matrix cores and folds each tile into an online
@@ -14,17 +14,19 @@ host synchronisation. It returns the mean loss over non-ignored rows and
 the per-row logsumexp (used by the z-loss and by the backward). With
 ``softcap`` > 0 every logit ``z`` becomes ``softcap * tanh(z / softcap)`` in
 the kernel's epilogue (the reference's ``logit_softcap``), and the tile
-partials use ``softcap`` as their offset (no max pass).
+partials use ``softcap`` as their offset (no max pass). With
+``label_smoothing`` a the loss is ``lse - (1 - a) z_t - a mean(z)``; the
+tile epilogue then also sums the (capped) logits of each token.
 
-With ``label_smoothing`` set, or for fp32 / unaligned inputs, the forward
-runs the reference's row-chunked algorithm: per ``chunk_size`` rows a GEMM
-(``torch.nn.functional.linear``) feeds the gfx950 CE row kernel.
+For fp32 or unaligned inputs the forward runs the reference's row-chunked
+algorithm: per ``chunk_size`` rows a GEMM (``torch.nn.functional.linear``)
+feeds the gfx950 CE row kernel.
 
 Backward (the fused forward's conditions): ``ak_lmhead_ce_bwd``
 recomputes the logits tile by tile on the matrix cores from the saved
 logsumexp and writes ``dL/dlogits`` (softmax minus one-hot, times the
 upstream gradient over the counted rows, times ``1 - tanh^2`` under the
-softcap) directly from registers in the
+softcap, less ``a / vocab`` under label smoothing) directly from registers in the
 input dtype; the device scalars stay on the device (no host sync). Then
 ``grad_hidden = dlogits @ W`` and ``grad_W = dlogits^T @ h`` are two plain
 GEMMs with fp32 accumulation (hipBLASLt via torch). Rows are processed in
@@ -32,7 +34,7 @@ chunks whose ``dlogits`` block stays under ``GRAD_LOGITS_BUDGET`` bytes (one
 chunk at the C4 shape: 8192 x 50304 bf16 = 824 MB of the 288 GB of HBM), so
 ``grad_W`` is normally one GEMM rounded once to the weight dtype; beyond the
 budget each chunk's product is rounded and the chunks are summed in fp32.
-Otherwise (label smoothing, fp32 or unaligned inputs) per row chunk
+Otherwise (fp32 or unaligned inputs) per row chunk
 the logits are recomputed with a GEMM and turned into ``dL/dlogits`` by the
 CE row kernel from the saved logsumexp, then ``grad_hidden = dlogits @ W``
 and ``grad_W += dlogits^T @ h`` (fp32 accumulation), as in the reference
@@ -55,7 +57,7 @@ from kernels.hip import _lib
 
 def _fused_ok(hidden: torch.Tensor, weight: torch.Tensor, softcap: float,
               label_smoothing: float) -> bool:
-    return (0.0 <= softcap < float("inf") and label_smoothing == 0.0
+    return (0.0 <= softcap < float("inf") and 0.0 <= label_smoothing <= 1.0
             and hidden.dtype in (torch.bfloat16, torch.float16) and weight.dtype == hidden.dtype
             and hidden.shape[1] % 64 == 0
             and hidden.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
@@ -63,7 +65,7 @@ def _fused_ok(hidden: torch.Tensor, weight: torch.Tensor, softcap: float,
 
 def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                       ignore_index: int = -100, return_losses: bool = False,
-                      softcap: float = 0.0):
+                      softcap: float = 0.0, label_smoothing: float = 0.0):
     """Fused forward: returns ``(loss, lse, n_valid)`` (+ per-row losses).
 
     ``loss`` is a 0-d fp32 tensor (mean over non-ignored rows), ``lse`` fp32
@@ -80,7 +82,8 @@ def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch
     n_valid = torch.empty(1, dtype=torch.int64, device=dev)
     losses = torch.empty(n, dtype=torch.float32, device=dev) if return_losses else None
     ws = torch.empty(_lib.lmhead_ce_workspace_bytes(n, weight.shape[0]), dtype=torch.uint8, device=dev)
-    _lib.lmhead_ce(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap)
+    _lib.lmhead_ce(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap,
+                   label_smoothing)
     if return_losses:
         return loss, lse, n_valid, losses
     return loss, lse, n_valid
@@ -93,12 +96,14 @@ GRAD_LOGITS_BUDGET = 4 << 30
 def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                        lse: torch.Tensor, denom: torch.Tensor, grad_loss: torch.Tensor,
                        ignore_index: int = -100, need_hidden: bool = True,
-                       need_weight: bool = True, softcap: float = 0.0):
+                       need_weight: bool = True, softcap: float = 0.0,
+                       label_smoothing: float = 0.0):
     """Fused backward of :func:`lmhead_ce_forward`'s mean loss.
 
     ``lse`` is the forward's logsumexp, ``denom`` the number of counted rows
     (a 0-d or 1-element fp32 tensor, clamped to >= 1) and ``grad_loss`` the
-    upstream gradient of the loss, ``softcap`` the forward's logit softcap.
+    upstream gradient of the loss, ``softcap`` and ``label_smoothing`` the
+    forward's.
     Returns ``(grad_hidden, grad_weight)`` in the input dtype (``None`` where
     not requested).
     """
@@ -120,7 +125,7 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
         # columns that a GEMM may read past K (0 * NaN)
         g = torch.empty((end - start, vocab), dtype=hidden.dtype, device=hidden.device)
         _lib.lmhead_ce_bwd(hidden[start:end], weight, targets[start:end], lse[start:end], g1, den1,
-                           g, ignore_index, softcap)
+                           g, ignore_index, softcap, label_smoothing)
         if need_hidden:
             torch.mm(g, weight, out=grad_hidden[start:end])
         if need_weight:
@@ -158,7 +163,8 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
         targets = targets.contiguous().to(torch.int64)
         if _fused_ok(hidden, weight, softcap, label_smoothing):
             loss, lse, n_valid_i = lmhead_ce_forward(hidden, weight, targets, ignore_index,
-                                                     softcap=float(softcap))
+                                                     softcap=float(softcap),
+                                                     label_smoothing=float(label_smoothing))
             n_valid = n_valid_i.to(torch.float32).clamp(min=1.0).reshape(())
         else:
             loss, lse, n_valid = _chunked_forward(hidden.contiguous(), weight.contiguous(), targets,
@@ -182,7 +188,8 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if ctx.fused and (need_h or need_w):
             gh, gw = lmhead_ce_backward(hidden, weight, targets, lse, n_valid, grad_output,
-                                        ctx.ignore_index, need_h, need_w, ctx.softcap)
+                                        ctx.ignore_index, need_h, need_w, ctx.softcap,
+                                        ctx.label_smoothing)
             return gh, gw, None, None, None, None, None, None
         grad_hidden = torch.empty_like(hidden) if need_h else None
         grad_weight = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device) if need_w else None

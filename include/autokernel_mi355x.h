@@ -162,6 +162,9 @@ int ak_ce_bwd_tiny(const void* logits, const int64_t* targets,
  * every logit z by softcap * tanh(z / softcap) before the logsumexp and the
  * target term (the logit_softcap of kernels/ce_fused.py:236-260 and
  * chunked_linear_cross_entropy.py:20, 185); 0 disables it.
+ * label_smoothing a in [0, 1] gives losses[i] = lse[i] - (1 - a) logit[i,
+ * target[i]] - a mean_j(logit[i, j]) (kernels/ce_fused.py:29, :250-256);
+ * 0 disables it.
  */
 size_t ak_lmhead_ce_workspace_bytes(int64_t n_rows, int64_t vocab);
 int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targets,
@@ -169,7 +172,7 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
                      void* workspace, size_t workspace_bytes,
                      int64_t n_rows, int64_t vocab, int64_t d,
                      int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                     float softcap, int dtype, void* stream);
+                     float softcap, float label_smoothing, int dtype, void* stream);
 
 /*
  * Fused lm-head + cross-entropy backward, first half: the gradient of the
@@ -190,14 +193,16 @@ int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const int64_t* targ
  * grad_logits is 16-byte aligned, element stores otherwise). Only the first
  * vocab entries of each row are written. With softcap > 0 the gradient is
  * taken through the softcap (times 1 - tanh^2(z / softcap)), lse being the
- * forward's logsumexp of the capped logits.
+ * forward's logsumexp of the capped logits. label_smoothing a replaces
+ * softmax - one_hot by softmax - (1 - a) one_hot - a / vocab
+ * (kernels/ce_fused.py:455-466).
  */
 int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
                      const float* lse, const float* grad_loss, const float* denom,
                      void* grad_logits, int64_t ld_gl,
                      int64_t n_rows, int64_t vocab, int64_t d,
                      int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                     float softcap, int dtype, void* stream);
+                     float softcap, float label_smoothing, int dtype, void* stream);
 
 /*
  * Mamba-1 selective scan forward (selective_scan_fn semantics).

@@ -167,13 +167,15 @@ def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int =
 
 
 def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
-                  ignore_index: int = -100, vocab_chunk: int = 4096, softcap: float = 0.0):
+                  ignore_index: int = -100, vocab_chunk: int = 4096, softcap: float = 0.0,
+                  label_smoothing: float = 0.0):
     """Linear + CE without materialising all logits (fp32 arithmetic).
 
     Follows ``kernels/hip/chunked_linear_cross_entropy.py:72-75`` (n_valid),
     ``:135-140`` (loss = sum / n_valid) and ``kernels/ce_fused.py:236-260``
     (per-row loss, logit softcap ``softcap * tanh(z / softcap)`` when
-    ``softcap > 0``), streaming the vocabulary in ``vocab_chunk`` columns with
+    ``softcap > 0``, label smoothing a: ``lse - (1 - a) z_t - a mean(z)``,
+    ``:250-256``), streaming the vocabulary in ``vocab_chunk`` columns with
     an online (max, sum) merge. Returns ``(loss, lse, losses)``.
     """
     h = hidden.float()
@@ -183,6 +185,7 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
     s = torch.zeros(n)
     t = targets.long()
     xt = torch.zeros(n)
+    zsum = torch.zeros(n)
     for v0 in range(0, V, vocab_chunk):
         v1 = min(V, v0 + vocab_chunk)
         logits = _capped(h @ weight[v0:v1].float().t(), softcap)
@@ -190,13 +193,18 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
         nm = torch.maximum(m, cm)
         s = s * torch.exp(m - nm) + torch.exp(logits - nm[:, None]).sum(-1)
         m = nm
+        zsum += logits.sum(-1)
         inside = (t >= v0) & (t < v1)
         if inside.any():
             idx = inside.nonzero().squeeze(1)
             xt[idx] = logits[idx, t[idx] - v0]
     lse = m + torch.log(s)
     ignored = t == ignore_index
-    losses = torch.where(ignored, torch.zeros_like(lse), lse - xt)
+    if label_smoothing > 0:
+        per = lse - (1 - label_smoothing) * xt - label_smoothing * zsum / V
+    else:
+        per = lse - xt
+    losses = torch.where(ignored, torch.zeros_like(lse), per)
     return ce_mean_ref(losses, t, ignore_index), lse, losses
 
 

@@ -86,8 +86,10 @@ def _ce_bwd_tiny(logits, targets, row_max, row_sum, grad, softcap, ignore_index,
     grad.copy_(g)
 
 
-def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap=0.0):
-    lo, ls_, per = ops.lmhead_ce_ref(hidden, weight, targets, ignore_index, softcap=softcap)
+def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap=0.0,
+            label_smoothing=0.0):
+    lo, ls_, per = ops.lmhead_ce_ref(hidden, weight, targets, ignore_index, softcap=softcap,
+                                     label_smoothing=label_smoothing)
     bad = _bad_targets(targets, weight.shape[0], ignore_index)
     per = torch.where(bad, torch.full_like(per, math.nan), per)
     lo = ops.ce_mean_ref(per, targets, ignore_index)
@@ -100,7 +102,7 @@ def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_inde
 
 
 def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ignore_index,
-                softcap=0.0):
+                softcap=0.0, label_smoothing=0.0):
     z = hidden.double() @ weight.double().t()
     dcap = torch.ones_like(z)
     if softcap > 0:
@@ -110,7 +112,8 @@ def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ign
     t = targets.long()
     V = weight.shape[0]
     ok = (t >= 0) & (t < V)
-    p = p - F.one_hot(torch.where(ok, t, torch.zeros_like(t)), V).double() * ok[:, None]
+    oh = F.one_hot(torch.where(ok, t, torch.zeros_like(t)), V).double() * ok[:, None]
+    p = p - (1 - label_smoothing) * oh - label_smoothing / V
     g = p * dcap * (float(grad_loss.reshape(-1)[0]) / float(denom.reshape(-1)[0]))
     g = torch.where((t == ignore_index)[:, None], torch.zeros_like(g), g)
     g = torch.where((~ok & (t != ignore_index))[:, None], torch.full_like(g, math.nan), g)

@@ -122,8 +122,12 @@ def test_ce_full_autograd(fake_backend, mode, softcap, ls, zw):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("softcap,zw", [(0.0, 0.0), (0.0, 1e-3), (10.0, 0.0)])
-def test_chunked_linear_ce(fake_backend, dtype, softcap, zw):
+@pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (0.0, 0.0, 1e-3), (10.0, 0.0, 0.0),
+                                           (0.0, 0.1, 0.0), (10.0, 0.25, 1e-3)])
+def test_chunked_linear_ce(fake_backend, dtype, softcap, ls, zw):
+    """Both the fused path (bf16) and the row-chunked path (fp32) against
+    F.cross_entropy on materialised fp64 logits, with softcap, label
+    smoothing and z-loss."""
     from kernels.hip.chunked_linear_cross_entropy import ChunkedLinearCrossEntropyLoss
     g = torch.Generator().manual_seed(2)
     h0 = torch.randn(2, 20, 64, generator=g)
@@ -132,14 +136,15 @@ def test_chunked_linear_ce(fake_backend, dtype, softcap, zw):
     t[0, :3] = -100
     h = h0.to(dtype).clone().requires_grad_()
     W = W0.to(dtype).clone().requires_grad_()
-    loss = ChunkedLinearCrossEntropyLoss(chunk_size=16, softcap=softcap, z_loss_weight=zw)(h, W, t)
+    loss = ChunkedLinearCrossEntropyLoss(chunk_size=16, softcap=softcap, label_smoothing=ls,
+                                         z_loss_weight=zw)(h, W, t)
     loss.backward()
     hr = h0.to(dtype).double().detach().requires_grad_()
     Wr = W0.to(dtype).double().detach().requires_grad_()
     logits = hr.reshape(-1, 64) @ Wr.t()
     if softcap > 0:
         logits = softcap * torch.tanh(logits / softcap)
-    ref = F.cross_entropy(logits, t.reshape(-1))
+    ref = F.cross_entropy(logits, t.reshape(-1), label_smoothing=ls)
     ref.backward()
     if zw > 0:  # z-loss enters the value only (as in the reference module)
         valid = (t.reshape(-1) != -100).double()

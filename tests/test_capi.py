@@ -45,7 +45,8 @@ def test_version_and_arch(lib):
 def test_workspace_query(lib):
     ws = _lib.lmhead_ce_workspace_bytes(8192, 50304)
     n_vt = (50304 + 255) // 256
-    assert ws >= n_vt * 8192 * 8 + 8192 * 4   # (max, sum) partials + per-row losses
+    # (max, sum) partials + per-row losses + label smoothing's per-partial logit sums
+    assert ws >= n_vt * 8192 * 8 + 8192 * 4 + 2 * n_vt * 8192 * 4
     assert ws % 256 == 0
     assert _lib.lmhead_ce_workspace_bytes(0, 10) == 0
 
@@ -56,14 +57,19 @@ def test_argument_errors_return_codes(lib):
     assert rc == -2 and b"dtype" in lib.ak_last_error()
     rc = lib.ak_softmax_fwd(None, None, 4, 8, 4, 8, 0, None)   # pitch < cols
     assert rc == -1 and b"pitch" in lib.ak_last_error()
-    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 100, 100, 100, -100, 0.0, 2, None)
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 100, 100, 100, -100, 0.0, 0.0, 2, None)
     assert rc == -2 and b"multiple" in lib.ak_last_error()
-    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0.0, 0, None)
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, 0.0, 0.0, 0, None)
     assert rc == -2  # fp32 is not a matrix-core input type here
-    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, -1.0, 2, None)
+    rc = lib.ak_lmhead_ce_fwd(None, None, None, None, None, None, None, None, 0, 8, 16, 64, 64, 64, -100, -1.0, 0.0, 2, None)
     assert rc == -1 and b"softcap" in lib.ak_last_error()
-    rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, float("nan"), 2, None)
+    rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, float("nan"), 0.0, 2, None)
     assert rc == -1 and b"softcap" in lib.ak_last_error()
+    for ls in (-0.1, 1.5, float("nan")):
+        rc = lib.ak_lmhead_ce_fwd(*([None] * 8), 0, 8, 16, 64, 64, 64, -100, 0.0, ls, 2, None)
+        assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
+        rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, 0.0, ls, 2, None)
+        assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
     rc = _lib.load().ak_selective_scan_fwd(*([None] * 12), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     # zero-size work is a no-op success

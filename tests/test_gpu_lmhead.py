@@ -19,10 +19,10 @@ pytestmark = gpu
 DEV = "cuda"
 
 
-def _run(h, W, t, ignore_index=-100, softcap=0.0):
+def _run(h, W, t, ignore_index=-100, softcap=0.0, ls=0.0):
     from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_forward
     return lmhead_ce_forward(h.to(DEV), W.to(DEV), t.to(DEV), ignore_index, return_losses=True,
-                             softcap=softcap)
+                             softcap=softcap, label_smoothing=ls)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -75,6 +75,30 @@ def test_lmhead_ce_softcap_matches_oracle(dtype, cap, n, vocab, d):
     assert bool((losses.cpu()[t == -100] == 0).all())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cap,ls", [(0.0, 0.1), (30.0, 0.1), (0.0, 1.0), (4.0, 0.3)])
+@pytest.mark.parametrize("n,vocab,d", [(5, 300, 64), (257, 4097, 768), (300, 1152, 128), (700, 640, 64),
+                                       (512, 50304, 768)])
+def test_lmhead_ce_label_smoothing_matches_oracle(dtype, cap, ls, n, vocab, d):
+    """Label smoothing in the fused forward (every tile-kernel variant, with
+    and without a softcap) against the streamed fp32 oracle: lse to 1e-4,
+    per-row losses and the mean to 1e-3 (the per-tile logit sums are fp32)."""
+    need_gpu()
+    g = torch.Generator().manual_seed(n * 11 + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = ((0.3 if 0 < cap < 10 else 0.05) * torch.randn(vocab, d, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[: max(0, n // 10)] = -100
+    say("lmhead_ce label smoothing", dtype, cap, ls, n, vocab, d)
+    loss, lse, nv, losses = _run(h, W, t, softcap=cap, ls=ls)
+    rloss, rlse, rlosses = ops.lmhead_ce_ref(h, W, t, softcap=cap, label_smoothing=ls)
+    assert int(nv) == int((t != -100).sum())
+    assert torch.allclose(lse.double().cpu(), rlse.double(), rtol=1e-4, atol=1e-4)
+    assert torch.allclose(losses.double().cpu(), rlosses.double(), rtol=1e-3, atol=1e-3)
+    assert abs(float(loss) - float(rloss)) <= 1e-3 * abs(float(rloss)) + 1e-6
+    assert bool((losses.cpu()[t == -100] == 0).all())
+
+
 def test_lmhead_all_ignored_and_bad_targets():
     need_gpu()
     g = torch.Generator().manual_seed(1)
@@ -118,8 +142,9 @@ def test_c4_full_size():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("softcap,zw", [(0.0, 0.0), (0.0, 1e-4), (20.0, 0.0), (30.0, 1e-4)])
-def test_chunked_linear_ce_fwd_bwd(dtype, softcap, zw):
+@pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (0.0, 0.0, 1e-4), (20.0, 0.0, 0.0),
+                                           (30.0, 0.0, 1e-4), (0.0, 0.1, 0.0), (30.0, 0.1, 1e-4)])
+def test_chunked_linear_ce_fwd_bwd(dtype, softcap, ls, zw):
     need_gpu()
     from kernels.hip.chunked_linear_cross_entropy import ChunkedLinearCrossEntropyLoss
     g = torch.Generator().manual_seed(3)
@@ -130,15 +155,16 @@ def test_chunked_linear_ce_fwd_bwd(dtype, softcap, zw):
     t[0, :10] = -100
     h = h0.to(dtype).to(DEV).requires_grad_()
     W = W0.to(dtype).to(DEV).requires_grad_()
-    say("chunked linear ce", dtype, softcap, zw)
-    loss = ChunkedLinearCrossEntropyLoss(chunk_size=100, softcap=softcap, z_loss_weight=zw)(h, W, t.to(DEV))
+    say("chunked linear ce", dtype, softcap, ls, zw)
+    loss = ChunkedLinearCrossEntropyLoss(chunk_size=100, softcap=softcap, label_smoothing=ls,
+                                         z_loss_weight=zw)(h, W, t.to(DEV))
     loss.backward()
     hr = h0.to(dtype).double().requires_grad_()
     Wr = W0.to(dtype).double().requires_grad_()
     logits = hr.reshape(-1, D) @ Wr.t()
     if softcap > 0:
         logits = softcap * torch.tanh(logits / softcap)
-    ref = F.cross_entropy(logits, t.reshape(-1))
+    ref = F.cross_entropy(logits, t.reshape(-1), label_smoothing=ls)
     ref.backward()
     if zw > 0:
         valid = (t.reshape(-1) != -100).double()
@@ -153,17 +179,18 @@ def test_chunked_linear_ce_fwd_bwd(dtype, softcap, zw):
 # Fused backward: dL/dlogits from the matrix cores, then two GEMMs
 # ---------------------------------------------------------------------------
 
-def _dz_ref(h, W, t, lse, scale, ignore_index=-100, softcap=0.0):
+def _dz_ref(h, W, t, lse, scale, ignore_index=-100, softcap=0.0, ls=0.0):
     """float64 softmax(h W^T) - onehot, times scale, from the GPU forward's lse
-    (through the softcap z' = c tanh(z / c), times 1 - tanh^2, when c > 0)."""
+    (through the softcap z' = c tanh(z / c), times 1 - tanh^2, when c > 0;
+    label smoothing a: softmax - (1 - a) onehot - a / V)."""
     z = h.double() @ W.double().t()
     dcap = 1.0
     if softcap > 0:
         th = torch.tanh(z / softcap)
         z, dcap = softcap * th, 1 - th * th
-    p = torch.exp(z - lse.double()[:, None])
+    p = torch.exp(z - lse.double()[:, None]) - ls / W.shape[0]
     tc = t.clamp(min=0)
-    p[torch.arange(len(t)), tc] -= 1.0
+    p[torch.arange(len(t)), tc] -= 1.0 - ls
     p = p * scale * dcap
     p[t == ignore_index] = 0.0
     return p
@@ -225,6 +252,35 @@ def test_lmhead_ce_grad_logits_softcap(dtype, n, vocab, d):
     _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, gl, denom, dz, -100, cap)
     scale = 0.75 / float(denom)
     ref = _dz_ref(h, W, t, lse.cpu(), scale, softcap=cap)
+    got = dz.double().cpu()
+    err = (got - ref).abs()
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    floor = 2e-6 * scale + (2.0 ** -25 if dtype == torch.float16 else 0.0)
+    assert bool((err <= eps * ref.abs() + floor).all()), float((err / (eps * ref.abs() + floor)).max())
+    assert bool((got[t == -100] == 0).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cap,ls", [(0.0, 0.1), (3.0, 0.2)])
+@pytest.mark.parametrize("n,vocab,d", [(5, 300, 64), (257, 4097, 768), (300, 1152, 128), (512, 50304, 768)])
+def test_lmhead_ce_grad_logits_label_smoothing(dtype, cap, ls, n, vocab, d):
+    """dL/dlogits with label smoothing (and a softcap) against float64, to one
+    rounding of the element type plus 2e-6 of the scale."""
+    need_gpu()
+    from kernels.hip import _lib
+    g = torch.Generator().manual_seed(n * 13 + vocab)
+    h = torch.randn(n, d, generator=g).to(dtype)
+    W = ((0.3 / math.sqrt(d / 64) if cap else 0.05) * torch.randn(vocab, d, generator=g)).to(dtype)
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[: max(0, n // 10)] = -100
+    say("lmhead_ce grad logits label smoothing", dtype, cap, ls, n, vocab, d)
+    loss, lse, nv, _ = _run(h, W, t, softcap=cap, ls=ls)
+    denom = nv.to(torch.float32).clamp(min=1.0).reshape(1)
+    gl = torch.tensor([0.75], device=DEV)
+    dz = torch.empty((n, vocab), dtype=dtype, device=DEV)
+    _lib.lmhead_ce_bwd(h.to(DEV), W.to(DEV), t.to(DEV), lse, gl, denom, dz, -100, cap, ls)
+    scale = 0.75 / float(denom)
+    ref = _dz_ref(h, W, t, lse.cpu(), scale, softcap=cap, ls=ls)
     got = dz.double().cpu()
     err = (got - ref).abs()
     eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
@@ -365,10 +421,12 @@ def test_c4_full_size_backward():
     assert rel < 5e-3, rel
 
 
-def test_fused_and_row_chunked_softcap_paths_agree():
-    """The same softcapped loss and gradients from the fused matrix-core path
-    (bf16) and from the row-chunked GEMM + CE-kernel path (forced with fp32
-    inputs holding the same values): two independent implementations."""
+@pytest.mark.parametrize("ls", [0.0, 0.1])
+def test_fused_and_row_chunked_softcap_paths_agree(ls):
+    """The same softcapped (and label-smoothed) loss and gradients from the
+    fused matrix-core path (bf16) and from the row-chunked GEMM + CE-kernel
+    path (forced with fp32 inputs holding the same values): two independent
+    implementations."""
     need_gpu()
     from kernels.hip.chunked_linear_cross_entropy import ChunkedLinearCrossEntropyLoss
     g = torch.Generator().manual_seed(12)
@@ -376,12 +434,13 @@ def test_fused_and_row_chunked_softcap_paths_agree():
     W0 = (0.05 * torch.randn(5000, 256, generator=g)).bfloat16()
     t = torch.randint(0, 5000, (600,), generator=g).to(DEV)
     t[:20] = -100
-    say("fused vs row-chunked softcap paths")
+    say("fused vs row-chunked softcap paths", ls)
     outs = []
     for dt in (torch.bfloat16, torch.float32):
         h = h0.to(dt).to(DEV).requires_grad_()
         W = W0.to(dt).to(DEV).requires_grad_()
-        loss = ChunkedLinearCrossEntropyLoss(chunk_size=256, softcap=30.0, z_loss_weight=1e-4)(h, W, t)
+        loss = ChunkedLinearCrossEntropyLoss(chunk_size=256, softcap=30.0, label_smoothing=ls,
+                                             z_loss_weight=1e-4)(h, W, t)
         loss.backward()
         outs.append((float(loss), h.grad.double().cpu(), W.grad.double().cpu()))
     (l1, gh1, gw1), (l2, gh2, gw2) = outs

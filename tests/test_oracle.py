@@ -468,3 +468,29 @@ def test_lmhead_ce_ref_softcap_matches_materialised_ce():
     capped = 5.0 * torch.tanh(logits / 5.0)
     ref = F.cross_entropy(capped, t, ignore_index=-100)
     assert torch.allclose(ops.lmhead_ce_ref(h, W, t, softcap=5.0)[0], ref, rtol=1e-5)
+
+
+def test_lmhead_ce_ref_label_smoothing_matches_torch():
+    """Label smoothing in the streamed lm-head oracle equals PyTorch's own
+    F.cross_entropy(label_smoothing=a) (whose smoothing term is a times the
+    mean of -log_softmax, i.e. a (lse - mean z)), with and without a softcap,
+    for every vocab chunking; a = 1 leaves only the uniform term."""
+    g = torch.Generator().manual_seed(23)
+    h = torch.randn(48, 32, generator=g, dtype=torch.float64).float()
+    W = 1.5 * torch.randn(500, 32, generator=g)
+    t = torch.randint(0, 500, (48,), generator=g)
+    t[[2, 30]] = -100
+    logits = h.double() @ W.double().t()
+    for cap in (0.0, 4.0):
+        z = cap * torch.tanh(logits / cap) if cap else logits
+        for a in (0.1, 0.35, 1.0):
+            ref = F.cross_entropy(z, t, ignore_index=-100, label_smoothing=a)
+            per_ref = F.cross_entropy(z, t, ignore_index=-100, label_smoothing=a, reduction="none")
+            for chunk in (64, 500, 4096):
+                loss, _, per = ops.lmhead_ce_ref(h, W, t, vocab_chunk=chunk, softcap=cap,
+                                                 label_smoothing=a)
+                assert torch.allclose(loss.double(), ref, rtol=1e-5), (cap, a, chunk)
+                assert torch.allclose(per.double(), per_ref, rtol=1e-5, atol=1e-5)
+            # the CE row oracle agrees on the same materialised logits
+            per_rows = ops.ce_rows_ref(logits.float(), t, softcap=cap, label_smoothing=a)[0]
+            assert torch.allclose(per_rows.double(), per_ref, rtol=1e-5, atol=1e-5)
