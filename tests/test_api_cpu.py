@@ -348,3 +348,36 @@ def test_optimize_include_exclude(fake_backend):
     assert list(autokernel.report(m)["patterns"]) == ["rmsnorm"]
     m = autokernel.optimize(Tiny(), training=True, exclude=["rmsnorm", "fused_residual_rmsnorm"])
     assert autokernel.report(m)["patterns"] == {}
+
+
+def test_replacements_route_through_custom_ops(fake_backend):
+    """Static audit of the module swaps (as the reference's
+    scripts/audit_autokernel_replacements.py does with ast): every call in a
+    replacement's forward goes through a registered torch.ops.autokernel op
+    (autograd-safe) or ordinary module / tensor methods, never through a raw
+    kernel entry (kernel_fn / kernel_fn_dual / the ctypes library), which
+    would sever autograd. The op attributes are checked to be those ops."""
+    import ast
+    import inspect
+
+    import autokernel
+    from autokernel import _patterns
+
+    tree = ast.parse(inspect.getsource(_patterns))
+    classes = [n for n in tree.body if isinstance(n, ast.ClassDef) and n.name.endswith("Replacement")]
+    assert len(classes) == 2
+    unsafe = ("self.kernel_fn", "self.kernel_fn_dual", "_lib.", "_get_fwd_module", "_get_bwd_module")
+    for cls in classes:
+        fwd = next(f for f in cls.body if isinstance(f, ast.FunctionDef) and f.name == "forward")
+        calls = [ast.unparse(c.func) for c in ast.walk(fwd) if isinstance(c, ast.Call)]
+        assert not [c for c in calls if any(c.startswith(u) or u in c for u in unsafe)], (cls.name, calls)
+        assert any(c.startswith("self._autograd_") for c in calls), (cls.name, calls)
+    model = autokernel.optimize(Tiny(), training=True)
+    ops_seen = set()
+    for m in model.modules():
+        for attr in ("_autograd_op", "_autograd_dual"):
+            op = getattr(m, attr, None)
+            if op is not None:
+                assert isinstance(op, torch._ops.OpOverloadPacket), (type(m).__name__, attr)
+                ops_seen.add(str(op))
+    assert ops_seen == {"autokernel.rmsnorm", "autokernel.fused_res_rmsnorm"}, ops_seen
