@@ -173,11 +173,14 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 def _rows_view(t: torch.Tensor, name: str) -> int:
     """Row pitch (elements) of a 2-D view whose last dim is contiguous."""
-    if t.dim() != 2:
-        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
-    if t.stride(1) != 1 and t.size(1) > 1:
+    shape = t.shape
+    if len(shape) != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(shape)}")
+    s0, s1 = t.stride()
+    n0, n1 = shape
+    if s1 != 1 and n1 > 1:
         raise ValueError(f"{name} must have a contiguous last dimension")
-    return max(t.stride(0), t.size(1)) if t.size(0) > 1 else t.size(1)
+    return max(s0, n1) if n0 > 1 else n1
 
 
 # ---------------------------------------------------------------------------
