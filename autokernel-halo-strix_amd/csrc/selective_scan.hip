@@ -63,6 +63,7 @@ struct ScanParams {
   void* du;                    // [batch, dim, seqlen], strides of out
   void* ddelta;                // [batch, dim, seqlen] in delta's type, strides of out
   float* ck;                   // [batch, nchunks, dim, dstate] states before each 16-step block
+                               // (the forward writes them when non-null)
   float* dB_part;              // [tiles, batch, ngroups, dstate, seqlen]
   float* dC_part;              // [tiles, batch, ngroups, dstate, seqlen]
   float* dA_part;              // [batch, dim, dstate]
@@ -247,8 +248,9 @@ mamba_scan_fwd_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
-      if constexpr (kPrep) {
-        // state before the block: the reverse pass restarts from it
+      if (kPrep || p.ck) {
+        // state before the block: the reverse pass restarts from it (the
+        // forward writes it too when given a checkpoint buffer)
         const int lb = l0 + 16 * blk;
         if (ch_ok && n_ok && lb < p.seqlen)
           p.ck[(((int64_t)b * p.nchunks + lb / kCk) * p.dim + d) * p.dstate + n] = h;
@@ -551,7 +553,7 @@ mamba_scan_fast_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
-      if constexpr (kPrep) {
+      if (kPrep || p.ck) {
         if (n_ok)
           p.ck[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
       }
@@ -1232,11 +1234,46 @@ inline ScanBwdWs scan_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t
   return w;
 }
 
+// dz of the gated output from the forward's pre-gate output y, as the
+// reference's backward computes it from its saved `out`:
+//   dz = dout * y * s * (1 + z (1 - s)),  s = sigmoid(z).
+// dout and z with their strides, y and dz contiguous [batch, dim, seqlen].
+// A workgroup walks rows (batch, channel) with a grid stride; its threads
+// cover a row's steps, so every access is a coalesced row segment.
+template <typename TU>
+__global__ void __launch_bounds__(256)
+scan_dz_kernel(const TU* __restrict__ dout, const TU* __restrict__ z, const TU* __restrict__ y,
+               TU* __restrict__ dz, int64_t rows, int dim, int seqlen, int64_t go_bs,
+               int64_t go_ds, int64_t z_bs, int64_t z_ds) {
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t b = row / dim;
+    const int64_t d = row - b * dim;
+    const TU* gp = dout + b * go_bs + d * go_ds;
+    const TU* zp = z + b * z_bs + d * z_ds;
+    const int64_t o = row * seqlen;
+    for (int l = threadIdx.x; l < seqlen; l += blockDim.x) {
+      const float zv = to_f32(zp[l]);
+      const float sg = sigmoid_f32(zv);
+      dz[o + l] = from_f32<TU>(to_f32(gp[l]) * to_f32(y[o + l]) * sg * fmaf(zv, 1.0f - sg, 1.0f));
+    }
+  }
+}
+
+// With `out_prez` (the forward's pre-gate output, given together with the
+// forward's checkpoints in p.ck) the preparation pass is skipped: the reverse
+// pass restarts from the saved states and dz comes from scan_dz_kernel.
 template <typename TU, typename TD, typename TBC>
 void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* dD, float* dbias,
-                     hipStream_t s) {
+                     bool saved_states, const void* out_prez, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
-  if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
+  if (saved_states) {
+    if (p.z) {
+      const int64_t rows = (int64_t)p.batch * p.dim;
+      scan_dz_kernel<TU><<<dim3((unsigned)std::min<int64_t>(rows, 1 << 20)), dim3(256), 0, s>>>(
+          static_cast<const TU*>(p.dout), static_cast<const TU*>(p.z), static_cast<const TU*>(out_prez),
+          static_cast<TU*>(p.dz), rows, p.dim, p.seqlen, p.go_bs, p.go_ds, p.z_bs, p.z_ds);
+    }
+  } else if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
     mamba_scan_fast_kernel<TU, TD, TBC, true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p, true))
     mamba_scan_fast_kernel<TU, TD, TBC, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
@@ -1265,15 +1302,16 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
 
 template <typename TU>
 int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, void* dB,
-                      void* dC, float* dA, float* dD, float* dbias, hipStream_t s) {
+                      void* dC, float* dA, float* dD, float* dbias, bool saved_states,
+                      const void* out_prez, hipStream_t s) {
   const bool d32 = delta_dtype == AK_DTYPE_F32;
   const bool bc32 = bc_dtype == AK_DTYPE_F32;
   if (!d32 && delta_dtype != u_dtype) return -1;
   if (!bc32 && bc_dtype != u_dtype) return -1;
-  if (d32 && bc32) launch_scan_bwd<TU, float, float>(p, dB, dC, dA, dD, dbias, s);
-  else if (d32) launch_scan_bwd<TU, float, TU>(p, dB, dC, dA, dD, dbias, s);
-  else if (bc32) launch_scan_bwd<TU, TU, float>(p, dB, dC, dA, dD, dbias, s);
-  else launch_scan_bwd<TU, TU, TU>(p, dB, dC, dA, dD, dbias, s);
+  if (d32 && bc32) launch_scan_bwd<TU, float, float>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
+  else if (d32) launch_scan_bwd<TU, float, TU>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
+  else if (bc32) launch_scan_bwd<TU, TU, float>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
+  else launch_scan_bwd<TU, TU, TU>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
   return 0;
 }
 
@@ -1283,7 +1321,8 @@ int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_
 extern "C" int ak_selective_scan_fwd(
     const void* u, const void* delta, const float* A, const void* B, const void* C,
     const float* D, const void* z, const float* delta_bias, void* out, float* last_state,
-    void* out_prez, float* chunk_states, int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate, int64_t ngroups,
+    void* out_prez, float* chunk_states, float* checkpoints, int64_t batch, int64_t dim,
+    int64_t seqlen, int64_t dstate, int64_t ngroups,
     int64_t u_batch_stride, int64_t u_dim_stride, int64_t delta_batch_stride,
     int64_t delta_dim_stride, int64_t A_dim_stride, int64_t B_batch_stride,
     int64_t B_group_stride, int64_t B_state_stride, int64_t C_batch_stride,
@@ -1301,10 +1340,12 @@ extern "C" int ak_selective_scan_fwd(
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
   if (batch == 0 || seqlen == 0) return AK_OK;
   if (!u || !delta || !A || !B || !C || !out) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
-  ak::ScanParams p;
+  ak::ScanParams p{};
   p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
   p.delta_bias = delta_bias; p.out = out; p.last_state = last_state;
   p.out_prez = out_prez; p.chunk_states = chunk_states;
+  p.ck = checkpoints;
+  p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
   p.xchunks = (int)((seqlen + ak::kXChunk - 1) / ak::kXChunk);
   p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
   p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
@@ -1389,6 +1430,7 @@ extern "C" int ak_selective_scan_bwd(
     const void* u, const void* delta, const float* A, const void* B, const void* C,
     const float* D, const void* z, const float* delta_bias, const void* dout, void* du,
     void* ddelta, float* dA, void* dB, void* dC, float* dD, void* dz, float* ddelta_bias,
+    const float* checkpoints, const void* out_prez,
     void* workspace, size_t workspace_bytes, int64_t batch, int64_t dim, int64_t seqlen,
     int64_t dstate, int64_t ngroups, int64_t u_batch_stride, int64_t u_dim_stride,
     int64_t delta_batch_stride, int64_t delta_dim_stride, int64_t A_dim_stride,
@@ -1430,6 +1472,8 @@ extern "C" int ak_selective_scan_bwd(
   }
   if (!u || !delta || !A || !B || !C || !dout || !du || !ddelta || !dB || !dC || (z && !dz))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  if (checkpoints && z && !out_prez)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: checkpoints with a gate z need out_prez", name);
   const ak::ScanBwdWs ws = ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups);
   if (!workspace || workspace_bytes < ws.total)
     return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
@@ -1458,11 +1502,14 @@ extern "C" int ak_selective_scan_bwd(
   p.dD_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA);
   p.dbias_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA + ws.dD);
   p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
+  // saved forward states: the reverse pass reads them in place (it never writes p.ck)
+  if (checkpoints) p.ck = const_cast<float*>(checkpoints);
+  const bool saved = checkpoints != nullptr;
   int rc;
   switch (u_dtype) {
-    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
-    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
-    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, s); break;
+    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
+    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
+    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
   }
   if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and B/C must be fp32 or the dtype of u", name);
   return ak_check_launch(name);

@@ -62,12 +62,12 @@ _SIGNATURES = {
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
                          _int, _c_void_p],
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _f32, _int, _c_void_p],
-    "ak_selective_scan_fwd": [_c_void_p] * 12 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
+    "ak_selective_scan_fwd": [_c_void_p] * 13 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
     "ak_diag_scan_bwd": [_c_void_p] * 12 + [ctypes.c_size_t] + [_i64] * 3 + [_c_void_p],
     "ak_selective_scan_bwd_workspace_bytes": [_i64] * 5,
-    "ak_selective_scan_bwd": [_c_void_p] * 18 + [ctypes.c_size_t] + [_i64] * 5 + [_i64] * 15
+    "ak_selective_scan_bwd": [_c_void_p] * 20 + [ctypes.c_size_t] + [_i64] * 5 + [_i64] * 15
     + [_int] * 4 + [_c_void_p],
 }
 _RESTYPES = {
@@ -326,10 +326,12 @@ def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
 
 
 def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool,
-                   out_prez=None, chunk_states=None) -> None:
+                   out_prez=None, chunk_states=None, checkpoints=None) -> None:
     """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l]; A [d, n]; optional
-    out_prez (pre-gate output, strides of out) and chunk_states [b, d, ceil(l/2048), n, 2]."""
-    require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state, out_prez, chunk_states)
+    out_prez (pre-gate output, strides of out), chunk_states [b, d, ceil(l/2048), n, 2]
+    and checkpoints [b, ceil(l/16), d, n] (the states the backward restarts from)."""
+    require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state, out_prez, chunk_states,
+                   checkpoints)
     if out_prez is not None and out_prez.stride() != out.stride():
         raise ValueError("out_prez must have out's strides")
     batch, dim, seqlen = u.shape
@@ -339,7 +341,7 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
     with _on_device(u):
         rc = load().ak_selective_scan_fwd(
             _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(delta_bias),
-            _ptr(out), _ptr(last_state), _ptr(out_prez), _ptr(chunk_states),
+            _ptr(out), _ptr(last_state), _ptr(out_prez), _ptr(chunk_states), _ptr(checkpoints),
             batch, dim, seqlen, dstate, ngroups,
             u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
             B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),
@@ -350,12 +352,16 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
 
 
 def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
-                       ddelta_bias, delta_softplus: bool) -> None:
+                       ddelta_bias, delta_softplus: bool, checkpoints=None, out_prez=None) -> None:
     """Mamba-1 backward. u/delta/z/dout [b, d, l] (last dim contiguous); B/C [b, g, n, l];
     A [d, n]; outputs du/ddelta/dz contiguous [b, d, l], dB/dC contiguous [b, g, n, l] in
-    B's dtype, dA [d, n] / dD [d] / ddelta_bias [d] fp32."""
+    B's dtype, dA [d, n] / dD [d] / ddelta_bias [d] fp32. With the forward's
+    ``checkpoints`` (and, with z, its contiguous ``out_prez``) the states are not
+    recomputed."""
     require_device(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
-                   ddelta_bias)
+                   ddelta_bias, checkpoints, out_prez)
+    if out_prez is not None and not out_prez.is_contiguous():
+        raise ValueError("out_prez must be contiguous")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     ngroups = B.shape[1]
@@ -367,7 +373,7 @@ def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA
         rc = lib.ak_selective_scan_bwd(
             _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(z), _ptr(delta_bias),
             _ptr(dout), _ptr(du), _ptr(ddelta), _ptr(dA), _ptr(dB), _ptr(dC), _ptr(dD), _ptr(dz),
-            _ptr(ddelta_bias), _ptr(ws), ws.numel(),
+            _ptr(ddelta_bias), _ptr(checkpoints), _ptr(out_prez), _ptr(ws), ws.numel(),
             batch, dim, seqlen, dstate, ngroups,
             u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
             B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),

@@ -42,6 +42,12 @@ HIP_SRC = os.path.join(_lib.CSRC_DIR, "selective_scan.hip")
 # steps per entry of the chunk-state output (the reference binding's chunk,
 # external/mamba/csrc/selective_scan/selective_scan.cpp:307)
 CHUNK = 2048
+# Steps between the states the forward keeps for the backward (the kernels' block).
+CHECKPOINT_STEPS = 16
+# Training keeps those states (fp32, batch x ceil(seqlen / 16) x dim x dstate: at
+# dstate 16 about twice the bytes of a bf16 u) so that the backward does not re-run
+# the forward; AUTOKERNEL_SCAN_RECOMPUTE=1 (or setting this to False) recomputes.
+SAVE_STATES = os.environ.get("AUTOKERNEL_SCAN_RECOMPUTE", "0") != "1"
 
 
 def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Tensor,
@@ -120,28 +126,38 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
 
 
 def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last_state,
-                  want_prez=False, want_chunk_states=False):
+                  want_prez=False, want_chunk_states=False, want_checkpoints=False):
+    """With ``want_checkpoints`` the states before every 16-step block are kept
+    (fp32 ``[batch, ceil(seqlen / 16), dim, dstate]``) together with the
+    pre-gate output when there is a gate, for ``_scan_backward`` to restart
+    from; they are returned after ``saved`` as ``(checkpoints, out_prez)``."""
     u, delta, A, B, C, D, z, delta_bias = _normalise(u, delta, A, B, C, D, z, delta_bias)
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     out = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=u.device)
     last_state = (torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device)
                   if want_last_state else None)
-    prez = torch.empty_like(out) if want_prez else None
+    prez = torch.empty_like(out) if want_prez or (want_checkpoints and z is not None) else None
     chunks = (torch.empty((batch, dim, (seqlen + CHUNK - 1) // CHUNK, dstate, 2), dtype=torch.float32,
                           device=u.device) if want_chunk_states else None)
+    ckpt = (torch.empty((batch, (seqlen + CHECKPOINT_STEPS - 1) // CHECKPOINT_STEPS, dim, dstate),
+                        dtype=torch.float32, device=u.device) if want_checkpoints else None)
     _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus,
-                        out_prez=prez, chunk_states=chunks)
+                        out_prez=prez, chunk_states=chunks, checkpoints=ckpt)
     saved = (u, delta, A, B, C, D, z, delta_bias)
+    if want_checkpoints:
+        return out, last_state, saved, (ckpt, prez)
     if want_prez or want_chunk_states:
         return out, last_state, saved, prez, chunks
     return out, last_state, saved
 
 
-def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus):
+def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus, checkpoints=None,
+                   out_prez=None):
     """Gradients of the Mamba-1 scan for the layouts ``_scan_forward`` produced
     (``ak_selective_scan_bwd``; the reference's ``selective_scan_cuda.bwd``,
-    external/mamba/csrc/selective_scan/selective_scan.cpp:339-490)."""
+    external/mamba/csrc/selective_scan/selective_scan.cpp:339-490). Given the
+    forward's checkpoints (and pre-gate output), the states are not recomputed."""
     if dout.dtype != u.dtype:
         dout = dout.to(u.dtype)
     if dout.stride(-1) != 1:
@@ -157,27 +173,34 @@ def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus):
     dz = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=dev) if z is not None else None
     dbias = torch.empty(dim, dtype=torch.float32, device=dev) if delta_bias is not None else None
     _lib.selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD,
-                            dz, dbias, delta_softplus)
+                            dz, dbias, delta_softplus, checkpoints=checkpoints, out_prez=out_prez)
     return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 
 class SelectiveScanFn(torch.autograd.Function):
     """Forward and backward on gfx950 (mirrors the reference's
-    ``SelectiveScanFn``, external/mamba/mamba_ssm/ops/selective_scan_interface.py:20-83:
-    the backward recomputes the states from the saved inputs)."""
+    ``SelectiveScanFn``, external/mamba/mamba_ssm/ops/selective_scan_interface.py:20-83).
+    When a gradient is needed the forward keeps its states every 16 steps
+    (``SAVE_STATES``), so the backward does not re-run the forward; otherwise
+    the backward recomputes them from the saved inputs, as the reference does."""
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                 return_last_state=False):
-        out, last_state, saved = _scan_forward(u, delta, A, B, C, D, z, delta_bias,
-                                               delta_softplus, return_last_state)
+        keep = SAVE_STATES and any(ctx.needs_input_grad[:8])
+        res = _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
+                            want_checkpoints=keep)
+        out, last_state, saved = res[:3]
+        ckpt, prez = res[3] if keep else (None, None)
+        ctx.has_ckpt = ckpt is not None
+        ctx.has_prez = prez is not None
         ctx.delta_softplus = bool(delta_softplus)
         ctx.squeeze_B = B.dim() == 3
         ctx.squeeze_C = C.dim() == 3
         ctx.has_D = D is not None
         ctx.has_z = z is not None
         ctx.has_bias = delta_bias is not None
-        ctx.save_for_backward(*(t for t in saved if t is not None))
+        ctx.save_for_backward(*(t for t in saved + (ckpt, prez) if t is not None))
         if return_last_state:
             ctx.mark_non_differentiable(last_state)
             return out, last_state
@@ -190,8 +213,10 @@ class SelectiveScanFn(torch.autograd.Function):
         D = next(it) if ctx.has_D else None
         z = next(it) if ctx.has_z else None
         delta_bias = next(it) if ctx.has_bias else None
+        ckpt = next(it) if ctx.has_ckpt else None
+        prez = next(it) if ctx.has_prez else None
         du, ddelta, dA, dB, dC, dD, dz, dbias = _scan_backward(
-            dout, u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus)
+            dout, u, delta, A, B, C, D, z, delta_bias, ctx.delta_softplus, ckpt, prez)
         if ctx.squeeze_B:
             dB = dB.squeeze(1)
         if ctx.squeeze_C:

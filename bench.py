@@ -265,6 +265,31 @@ def make_case(name):
         return Case(name, "C5-shape Mamba-1 selective scan backward B4 L4096 D2048 N16", "hbm",
                     C5B_BYTES, 4 * 4096, launch, sets,
                     "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
+    if name == "c5t":
+        # one training step of the scan: the forward keeps its states every 16
+        # steps and its pre-gate output, the backward restarts from them
+        cpu = gen_c5()
+        cpu["dout"] = torch.randn(cpu["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+        sets = _replicate(cpu, 2)
+        for s in sets:
+            for k in ("out", "prez", "du", "dz"):
+                s[k] = torch.empty_like(s["u"])
+            s["ck"] = torch.empty((4, 4096 // 16, 2048, 16), dtype=torch.float32, device="cuda")
+            s["ddelta"] = torch.empty_like(s["delta"])
+            s["dA"] = torch.empty_like(s["A"])
+            s["dB"] = torch.empty_like(s["B"])
+            s["dC"] = torch.empty_like(s["C"])
+            s["dD"] = torch.empty_like(s["D"])
+
+        def launch(s):
+            _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"], s["z"], None,
+                                s["out"], None, False, out_prez=s["prez"], checkpoints=s["ck"])
+            _lib.selective_scan_bwd(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"], s["z"], None,
+                                    s["dout"], s["du"], s["ddelta"], s["dA"], s["dB"], s["dC"], s["dD"],
+                                    s["dz"], None, False, checkpoints=s["ck"], out_prez=s["prez"])
+        return Case(name, "C5-shape Mamba-1 training step (forward keeping its states + backward from them)",
+                    "hbm", C5_BYTES + C5B_BYTES, 4 * 4096, launch, sets,
+                    "mamba_scan_fast_kernel + scan_dz_kernel + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
     raise ValueError(name)
 
 
@@ -380,6 +405,14 @@ def cpu_baseline(name, budget_s=4.0):
         t = timed(lambda: ops.selective_scan_bwd_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], dout,
                                                      c["D"], c["z"]), 2)
         return (32 * 4096) / t / 2048 / 1e6, "Mtok/s", "batch 1, 32 of 2048 channels, full L=4096 (float64 oracle)"
+    if name == "c5t":
+        c = gen_c5(b=1, d=32)
+        dout = torch.randn(c["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
+        t = timed(lambda: (ops.selective_scan_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"]),
+                           ops.selective_scan_bwd_ref(c["u"], c["delta"], c["A"], c["B"], c["C"], dout,
+                                                      c["D"], c["z"])), 2)
+        return ((32 * 4096) / t / 2048 / 1e6, "Mtok/s",
+                "batch 1, 32 of 2048 channels, full L=4096 (forward oracle + float64 backward oracle)")
     raise ValueError(name)
 
 
@@ -390,7 +423,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b,c5t")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "
@@ -438,7 +471,7 @@ def main(argv=None):
             "input_sets": len(case.sets),
             "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
         }
-        if name in ("c5", "c5b"):
+        if name in ("c5", "c5b", "c5t"):
             rec["Mtok_per_s"] = round(case.tokens / (mean_ms * 1e-3) / 1e6, 2)
         if not args.no_cpu:
             rate, cunit, sample = cpu_baseline(name)

@@ -223,12 +223,17 @@ int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targ
  *               per 2048-step chunk, the scan's running prefix from step 0 to
  *               the chunk's last step, (prod exp(delta' A), h) per state (the
  *               reference binding's `x`, selective_scan.cpp:307-313)
+ *   checkpoints: [batch, ceil(seqlen / 16), dim, dstate] fp32 or NULL: the
+ *               state before every 16-step block, for ak_selective_scan_bwd
+ *               to restart from instead of re-running the forward (training
+ *               keeps them; the reference's backward recomputes from `x`)
  * Strides are in elements. dim must be a multiple of ngroups; dstate <= 16.
  */
 int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           const void* B, const void* C, const float* D,
                           const void* z, const float* delta_bias,
                           void* out, float* last_state, void* out_prez, float* chunk_states,
+                          float* checkpoints,
                           int64_t batch, int64_t dim, int64_t seqlen,
                           int64_t dstate, int64_t ngroups,
                           int64_t u_batch_stride, int64_t u_dim_stride,
@@ -247,13 +252,20 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  * external/mamba/csrc/selective_scan/selective_scan.cpp:339-490, as called by
  * external/mamba/mamba_ssm/ops/selective_scan_interface.py:59-83 (its
  * recompute_out_z option and the saved chunk states x are not needed: the
- * states are recomputed here).
+ * states are recomputed here, or taken from the forward's checkpoints).
  *   inputs as for ak_selective_scan_fwd; dout [batch, dim, seqlen] in u_dtype
  *   du, dz    : contiguous [batch, dim, seqlen], u_dtype (dz only with z)
  *   ddelta    : contiguous [batch, dim, seqlen], delta_dtype
  *   dA        : contiguous [dim, dstate] fp32
  *   dB, dC    : contiguous [batch, ngroups, dstate, seqlen], bc_dtype
  *   dD, ddelta_bias : [dim] fp32, required when D / delta_bias are given
+ *   checkpoints, out_prez : NULL, or the forward's `checkpoints` and (with z)
+ *               its `out_prez` as a contiguous [batch, dim, seqlen] tensor.
+ *               Given, the backward skips its re-run of the forward: it
+ *               restarts from the saved states, which it only reads, and
+ *               computes dz from out_prez. Every gradient but dz is then
+ *               bitwise the same; dz uses the stored (rounded) pre-gate
+ *               output, as the reference's backward does with its `out`.
  * workspace: ak_selective_scan_bwd_workspace_bytes(...) bytes (saved states
  * every 16 steps and the partial sums of dB / dC / dA / dD / ddelta_bias,
  * reduced in a fixed order: results are bitwise reproducible).
@@ -265,6 +277,7 @@ int ak_selective_scan_bwd(const void* u, const void* delta, const float* A,
                           const void* z, const float* delta_bias, const void* dout,
                           void* du, void* ddelta, float* dA, void* dB, void* dC,
                           float* dD, void* dz, float* ddelta_bias,
+                          const float* checkpoints, const void* out_prez,
                           void* workspace, size_t workspace_bytes,
                           int64_t batch, int64_t dim, int64_t seqlen,
                           int64_t dstate, int64_t ngroups,

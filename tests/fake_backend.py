@@ -121,7 +121,7 @@ def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ign
 
 
 def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, out_prez=None,
-          chunk_states=None):
+          chunk_states=None, checkpoints=None):
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
                                      return_last_state=True)
     out.copy_(o)
@@ -131,10 +131,12 @@ def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, 
         out_prez.copy_(ops.selective_scan_ref(u, delta, A, B, C, D, None, delta_bias, delta_softplus))
     if chunk_states is not None:
         chunk_states.copy_(ops.selective_scan_chunk_states_ref(u, delta, A, B, delta_bias, delta_softplus))
+    if checkpoints is not None:  # the fake backward recomputes; mark the buffer as written
+        checkpoints.zero_()
 
 
 def _scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz, dbias,
-              delta_softplus):
+              delta_softplus, checkpoints=None, out_prez=None):
     outs = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, delta_bias, delta_softplus)
     for dst, src in zip((du, ddelta, dA, dB, dC, dD, dz, dbias), outs):
         if dst is not None:

@@ -70,7 +70,7 @@ def test_argument_errors_return_codes(lib):
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
         rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, 0.0, ls, 2, None)
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
-    rc = _lib.load().ak_selective_scan_fwd(*([None] * 12), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
+    rc = _lib.load().ak_selective_scan_fwd(*([None] * 13), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     # zero-size work is a no-op success
     assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0
@@ -91,16 +91,18 @@ def test_selective_scan_bwd_workspace_and_argument_errors(lib):
     assert lib.ak_selective_scan_bwd_workspace_bytes(b, 41, l, n, g) == 0  # dim % ngroups
     fn = _lib.load().ak_selective_scan_bwd
     strides = [0] * 15
-    rc = fn(*([None] * 17), None, 0, 2, 4, 16, 32, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*([None] * 19), None, 0, 2, 4, 16, 32, 1, *strides, 0, 2, 0, 2, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     fake = 4096  # never dereferenced: every check below fails first
-    ptrs = [fake] * 17
+    ptrs = [fake] * 17 + [None, None]  # no saved checkpoints / out_prez
     ptrs[14] = None  # dD missing while D is given
     rc = fn(*ptrs, None, 0, 2, 4, 16, 8, 1, *strides, 0, 2, 0, 2, None)
     assert rc == -1 and b"dD" in lib.ak_last_error()
-    rc = fn(*([fake] * 17), fake, 1024, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*([fake] * 17), fake, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
+    assert rc == -1 and b"out_prez" in lib.ak_last_error()  # checkpoints and z without out_prez
+    rc = fn(*([fake] * 17), None, None, fake, 1024, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
     assert rc < 0 and b"workspace" in lib.ak_last_error()
-    rc = fn(*([fake] * 17), fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 3, 2, None)
+    rc = fn(*([fake] * 17), None, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 3, 2, None)
     assert rc == -2 and b"dtype" in lib.ak_last_error()  # delta neither fp32 nor u's type
 
 

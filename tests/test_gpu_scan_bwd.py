@@ -221,12 +221,14 @@ def test_binding_fwd_chunk_states_and_prez(seqlen, fast):
     assert torch.allclose(out_z.cpu(), ref_z, rtol=rt, atol=at)
 
 
-def test_binding_bwd_matches_autograd():
+def test_binding_bwd_matches_autograd(monkeypatch):
     """selective_scan_cuda.bwd (the reference binding's return list) gives the
-    gradients selective_scan_fn's autograd gives, bit for bit (same kernels),
-    and writes dz into a caller buffer."""
+    gradients selective_scan_fn's autograd gives when the latter recomputes
+    the states too, bit for bit (same kernels), and writes dz into a caller
+    buffer."""
     need_gpu()
-    from kernels.hip import selective_scan_cuda
+    from kernels.hip import selective_scan, selective_scan_cuda
+    monkeypatch.setattr(selective_scan, "SAVE_STATES", False)
     u, delta, A, B, C, D, z, bias, dout = _inputs(2, 32, 16, 512, 1, torch.bfloat16, 22)
     B3, C3 = B[:, 0], C[:, 0]
     say("binding bwd vs autograd")
@@ -269,3 +271,54 @@ def test_backward_strided_views():
     for t in (uw, dw, zw):
         assert float(t.grad[:, 48:].abs().max()) == 0.0
     assert float(Bw.grad[:, :, 16:].abs().max()) == 0.0 and float(Cw.grad[:, :, 16:].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("itype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("batch,dim,seqlen,groups", [(2, 32, 512, 1), (1, 20, 300, 2), (2, 48, 1000, 1)])
+def test_saved_states_backward_matches_recompute(monkeypatch, itype, batch, dim, seqlen, groups):
+    """The training path (the forward keeps its states every 16 steps and its
+    pre-gate output; the backward restarts from them) against the recompute
+    path (the backward re-runs the forward): every gradient but dz bitwise
+    equal, on the fast kernel's shapes and on ragged ones (generic kernel,
+    2 groups); dz bitwise for fp32 and within one rounding of the stored
+    pre-gate output for bf16. Both paths go through selective_scan_fn."""
+    need_gpu()
+    from kernels.hip import selective_scan
+    args = _inputs(batch, dim, 16, seqlen, groups, itype, 31, delta_dtype=torch.float32)
+    say("mamba bwd saved states vs recompute", itype, batch, dim, seqlen, groups)
+    monkeypatch.setattr(selective_scan, "SAVE_STATES", True)
+    saved = _gpu_grads(*args, softplus=True)
+    monkeypatch.setattr(selective_scan, "SAVE_STATES", False)
+    recomputed = _gpu_grads(*args, softplus=True)
+    for name, a, b in zip(NAMES, saved, recomputed):
+        if name == "dz" and itype != torch.float32:
+            bound = 2.0 ** -7 * b.float().abs() + 1e-6 * float(b.float().abs().max())
+            assert bool(((a.float() - b.float()).abs() <= bound).all()), name
+        else:
+            assert torch.equal(a, b), name
+
+
+def test_saved_states_c_abi():
+    """ak_selective_scan_fwd with a checkpoint buffer, then
+    ak_selective_scan_bwd with and without it (no gate, so no out_prez is
+    needed): identical gradients at the C5 channel / state layout."""
+    need_gpu()
+    from kernels.hip import _lib
+    u, delta, A, B, C, D, z, bias, dout = (None if t is None else t.to(DEV) for t in
+                                           _inputs(2, 64, 16, 1024, 1, torch.bfloat16, 33,
+                                                   delta_dtype=torch.float32))
+    say("mamba C-ABI checkpoints")
+    out = torch.empty_like(u)
+    ck = torch.full((2, 1024 // 16, 64, 16), float("nan"), device=DEV)
+    _lib.selective_scan(u, delta, A, B, C, D, None, bias, out, None, True, checkpoints=ck)
+    assert bool(torch.isfinite(ck).all())  # every block's state written
+    assert bool((ck[:, 0] == 0).all())     # the state before step 0
+    grads = []
+    for use in (False, True):
+        g = [torch.empty_like(u), torch.empty_like(delta), torch.empty_like(A), torch.empty_like(B),
+             torch.empty_like(C), torch.empty_like(D), None, torch.empty_like(bias)]
+        _lib.selective_scan_bwd(u, delta, A, B, C, D, None, bias, dout, *g[:6], g[6], g[7], True,
+                                checkpoints=ck if use else None)
+        grads.append(g)
+    for name, a, b in zip(NAMES, *grads):
+        assert (a is None and b is None) or torch.equal(a, b), name
