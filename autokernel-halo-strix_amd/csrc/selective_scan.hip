@@ -890,11 +890,14 @@ mamba_scan_bwd_kernel(ScanParams p) {
     TD dv[4];                            // broadcast sources: steps 4n .. 4n + 3
     TU uv[4], gv[4], zv[4];
     TD dr[4];                            // reducer role: steps 16 blk + n
-    TU ur[4], gr[4], zr[4];
+    TU ur[4], gr[4], zr[4], yr[4];       // yr: the forward's pre-gate output (saved-states path)
     float ck[4];                         // states before the tile's four blocks
   };
   const TU* const zsrc = static_cast<const TU*>(p.z ? p.z : p.u);  // without z: unused u loads
   const int64_t zrow = p.z ? z_row : u_row;
+  // the forward's pre-gate output (contiguous, as du), given on the saved-states path
+  const TU* const ysrc = static_cast<const TU*>(p.out_prez ? p.out_prez : p.u);
+  const int64_t yrow = p.out_prez ? o_row : u_row;
   const int64_t ck_row = (int64_t)d * p.dstate + n_c;
   auto load_tile = [&](int l0, TileRegs& r) {
 #pragma unroll
@@ -918,6 +921,7 @@ mamba_scan_bwd_kernel(ScanParams p) {
       r.ur[blk] = static_cast<const TU*>(p.u)[u_row + lc];
       r.gr[blk] = static_cast<const TU*>(p.dout)[go_row + lc];
       r.zr[blk] = zsrc[zrow + lc];
+      r.yr[blk] = ysrc[yrow + lc];
       const int chunk = min((l0 + 16 * blk) / kCk, p.nchunks - 1);
       r.ck[blk] = p.ck[((int64_t)b * p.nchunks + chunk) * p.dim * p.dstate + ck_row];
     }
@@ -1027,7 +1031,18 @@ mamba_scan_bwd_kernel(ScanParams p) {
       __builtin_amdgcn_wave_barrier();
       const int l = lb + n;
       if (ch_ok && l < p.seqlen) {
-        const float dyv = gated(to_f32(cur.gr[BLK]), to_f32(cur.zr[BLK]));
+        const float go = to_f32(cur.gr[BLK]);
+        float dyv = go;  // dout * silu(z), or dout without a gate
+        if (p.z) {
+          const float zv = to_f32(cur.zr[BLK]);
+          const float sg = sigmoid_f32(zv);
+          dyv = go * zv * sg;
+          // saved-states path: dz = dout * y * s * (1 + z (1 - s)) from the
+          // forward's pre-gate output y, s = sigmoid(z)
+          if (p.out_prez)
+            static_cast<TU*>(p.dz)[o_row + l] =
+                from_f32<TU>(go * to_f32(cur.yr[BLK]) * sg * fmaf(zv, 1.0f - sg, 1.0f));
+        }
         const float uv = to_f32(cur.ur[BLK]);
         const float x = to_f32(cur.dr[BLK]) + dbias;
         float dlt = x, ddl = fmaf(uv, sgb, saw);
@@ -1234,51 +1249,21 @@ inline ScanBwdWs scan_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t
   return w;
 }
 
-// dz of the gated output from the forward's pre-gate output y, as the
-// reference's backward computes it from its saved `out`:
-//   dz = dout * y * s * (1 + z (1 - s)),  s = sigmoid(z).
-// dout and z with their strides, y and dz contiguous [batch, dim, seqlen].
-// A workgroup walks rows (batch, channel) with a grid stride; its threads
-// cover a row's steps, so every access is a coalesced row segment.
-template <typename TU>
-__global__ void __launch_bounds__(256)
-scan_dz_kernel(const TU* __restrict__ dout, const TU* __restrict__ z, const TU* __restrict__ y,
-               TU* __restrict__ dz, int64_t rows, int dim, int seqlen, int64_t go_bs,
-               int64_t go_ds, int64_t z_bs, int64_t z_ds) {
-  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
-    const int64_t b = row / dim;
-    const int64_t d = row - b * dim;
-    const TU* gp = dout + b * go_bs + d * go_ds;
-    const TU* zp = z + b * z_bs + d * z_ds;
-    const int64_t o = row * seqlen;
-    for (int l = threadIdx.x; l < seqlen; l += blockDim.x) {
-      const float zv = to_f32(zp[l]);
-      const float sg = sigmoid_f32(zv);
-      dz[o + l] = from_f32<TU>(to_f32(gp[l]) * to_f32(y[o + l]) * sg * fmaf(zv, 1.0f - sg, 1.0f));
-    }
-  }
-}
-
-// With `out_prez` (the forward's pre-gate output, given together with the
-// forward's checkpoints in p.ck) the preparation pass is skipped: the reverse
-// pass restarts from the saved states and dz comes from scan_dz_kernel.
+// With the forward's states (p.ck) and pre-gate output (p.out_prez) saved,
+// the preparation pass is skipped: the reverse pass restarts from the saved
+// states and computes dz itself.
 template <typename TU, typename TD, typename TBC>
 void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* dD, float* dbias,
-                     bool saved_states, const void* out_prez, hipStream_t s) {
+                     bool saved_states, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
-  if (saved_states) {
-    if (p.z) {
-      const int64_t rows = (int64_t)p.batch * p.dim;
-      scan_dz_kernel<TU><<<dim3((unsigned)std::min<int64_t>(rows, 1 << 20)), dim3(256), 0, s>>>(
-          static_cast<const TU*>(p.dout), static_cast<const TU*>(p.z), static_cast<const TU*>(out_prez),
-          static_cast<TU*>(p.dz), rows, p.dim, p.seqlen, p.go_bs, p.go_ds, p.z_bs, p.z_ds);
-    }
-  } else if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
-    mamba_scan_fast_kernel<TU, TD, TBC, true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
-  else if (scan_fast_ok<TU, TD, TBC>(p, true))
-    mamba_scan_fast_kernel<TU, TD, TBC, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
-  else
-    mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  if (!saved_states) {  // preparation pass: states every 16 steps and dz
+    if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
+      mamba_scan_fast_kernel<TU, TD, TBC, true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    else if (scan_fast_ok<TU, TD, TBC>(p, true))
+      mamba_scan_fast_kernel<TU, TD, TBC, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    else
+      mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  }
   if (p.softplus)
     mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else
@@ -1302,16 +1287,15 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
 
 template <typename TU>
 int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, void* dB,
-                      void* dC, float* dA, float* dD, float* dbias, bool saved_states,
-                      const void* out_prez, hipStream_t s) {
+                      void* dC, float* dA, float* dD, float* dbias, bool saved_states, hipStream_t s) {
   const bool d32 = delta_dtype == AK_DTYPE_F32;
   const bool bc32 = bc_dtype == AK_DTYPE_F32;
   if (!d32 && delta_dtype != u_dtype) return -1;
   if (!bc32 && bc_dtype != u_dtype) return -1;
-  if (d32 && bc32) launch_scan_bwd<TU, float, float>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
-  else if (d32) launch_scan_bwd<TU, float, TU>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
-  else if (bc32) launch_scan_bwd<TU, TU, float>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
-  else launch_scan_bwd<TU, TU, TU>(p, dB, dC, dA, dD, dbias, saved_states, out_prez, s);
+  if (d32 && bc32) launch_scan_bwd<TU, float, float>(p, dB, dC, dA, dD, dbias, saved_states, s);
+  else if (d32) launch_scan_bwd<TU, float, TU>(p, dB, dC, dA, dD, dbias, saved_states, s);
+  else if (bc32) launch_scan_bwd<TU, TU, float>(p, dB, dC, dA, dD, dbias, saved_states, s);
+  else launch_scan_bwd<TU, TU, TU>(p, dB, dC, dA, dD, dbias, saved_states, s);
   return 0;
 }
 
@@ -1502,14 +1486,17 @@ extern "C" int ak_selective_scan_bwd(
   p.dD_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA);
   p.dbias_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA + ws.dD);
   p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
-  // saved forward states: the reverse pass reads them in place (it never writes p.ck)
-  if (checkpoints) p.ck = const_cast<float*>(checkpoints);
+  // saved forward states: the reverse pass reads them (and out_prez) in place
+  if (checkpoints) {
+    p.ck = const_cast<float*>(checkpoints);
+    p.out_prez = const_cast<void*>(out_prez);
+  }
   const bool saved = checkpoints != nullptr;
   int rc;
   switch (u_dtype) {
-    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
-    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
-    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, out_prez, s); break;
+    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
   }
   if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and B/C must be fp32 or the dtype of u", name);
   return ak_check_launch(name);

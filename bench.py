@@ -289,7 +289,7 @@ def make_case(name):
                                     s["dz"], None, False, checkpoints=s["ck"], out_prez=s["prez"])
         return Case(name, "C5-shape Mamba-1 training step (forward keeping its states + backward from them)",
                     "hbm", C5_BYTES + C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel + scan_dz_kernel + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
+                    "mamba_scan_fast_kernel + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
     raise ValueError(name)
 
 
