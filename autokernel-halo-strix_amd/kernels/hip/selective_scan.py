@@ -186,8 +186,11 @@ class SelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                return_last_state=False):
-        keep = SAVE_STATES and any(ctx.needs_input_grad[:8])
+                return_last_state=False, grad_mode=None):
+        # grad_mode: whether autograd was recording at the call (forward itself
+        # runs without it); needs_input_grad alone is also true under no_grad
+        # for inputs that require grad, e.g. parameters during inference
+        keep = SAVE_STATES and any(ctx.needs_input_grad[:8]) and grad_mode is not False
         res = _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
                             want_checkpoints=keep)
         out, last_state, saved = res[:3]
@@ -221,11 +224,11 @@ class SelectiveScanFn(torch.autograd.Function):
             dB = dB.squeeze(1)
         if ctx.squeeze_C:
             dC = dC.squeeze(1)
-        return du, ddelta, dA, dB, dC, dD, dz, dbias, None, None
+        return du, ddelta, dA, dB, dC, dD, dz, dbias, None, None, None
 
 
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                       return_last_state=False):
     """Mamba-1 selective scan. Returns ``out`` or ``(out, last_state)``."""
     return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
-                                 return_last_state)
+                                 return_last_state, torch.is_grad_enabled())

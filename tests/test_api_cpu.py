@@ -381,3 +381,34 @@ def test_replacements_route_through_custom_ops(fake_backend):
                 assert isinstance(op, torch._ops.OpOverloadPacket), (type(m).__name__, attr)
                 ops_seen.add(str(op))
     assert ops_seen == {"autokernel.rmsnorm", "autokernel.fused_res_rmsnorm"}, ops_seen
+
+
+def test_selective_scan_fn_keeps_states_only_when_recording(fake_backend, monkeypatch):
+    """The forward keeps its 16-step states for the backward only when autograd
+    records the call: not under torch.no_grad() (inference with parameters
+    that require grad), nor with AUTOKERNEL_SCAN_RECOMPUTE's switch off."""
+    from kernels.hip import _lib
+    from kernels.hip import selective_scan as ss
+    seen = []
+    fake_scan = _lib.selective_scan
+
+    def spy(*args, **kw):
+        seen.append(kw.get("checkpoints") is not None)
+        return fake_scan(*args, **kw)
+
+    monkeypatch.setattr(_lib, "selective_scan", spy)
+    g = torch.Generator().manual_seed(4)
+    u = torch.randn(1, 4, 32, generator=g)
+    delta = torch.rand(1, 4, 32, generator=g) * 0.5
+    A = torch.nn.Parameter(-torch.rand(4, 8, generator=g) - 0.5)
+    B = torch.randn(1, 8, 32, generator=g)
+    C = torch.randn(1, 8, 32, generator=g)
+    z = torch.randn(1, 4, 32, generator=g)
+    with torch.no_grad():
+        ss.selective_scan_fn(u, delta, A, B, C, z=z)
+    out = ss.selective_scan_fn(u, delta, A, B, C, z=z)
+    out.sum().backward()
+    assert A.grad is not None and torch.isfinite(A.grad).all()
+    monkeypatch.setattr(ss, "SAVE_STATES", False)
+    ss.selective_scan_fn(u, delta, A, B, C, z=z).sum().backward()
+    assert seen == [False, True, False]
