@@ -3,8 +3,8 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1,c2,...] [--no-cpu]
 
 Prints ONE JSON line. The headline (``value``) is the HBM throughput of the
-configuration BASELINE.json's metric is quoted on at one GPU, configs[1]:
-the causal-masked fp16 row softmax [8, 12, 1024, 1024] (C2). A "step" is one
+configuration the benchmark's metric is quoted on at one GPU: the
+causal-masked fp16 row softmax [8, 12, 1024, 1024] (C2). A "step" is one
 launch of that kernel over one batch of synthetic input already resident in
 HBM; ``value`` = algorithmic bytes x K / wall-clock time of the K timed steps.
 ``roofline`` gives the kernel's achieved bandwidth from HIP-event kernel
