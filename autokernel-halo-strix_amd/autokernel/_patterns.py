@@ -81,19 +81,40 @@ def _autokernel_ops():
     return torch.ops.autokernel
 
 
+def _norm_eps(norm: nn.Module) -> float:
+    """The epsilon a norm module was built with: ``eps`` (torch.nn.RMSNorm and
+    the reference's RMSNorm), ``variance_epsilon`` (HF Llama / Mistral / Qwen2 /
+    T5), else the reference's fixed 1e-6. torch.nn.RMSNorm's ``eps=None``
+    means the dtype's machine epsilon."""
+    eps = getattr(norm, "eps", None)
+    if eps is None and hasattr(norm, "variance_epsilon"):
+        eps = norm.variance_epsilon
+    if eps is None:
+        w = getattr(norm, "weight", None)
+        eps = torch.finfo(w.dtype).eps if isinstance(norm, getattr(nn, "RMSNorm", ())) and w is not None \
+            else 1e-6
+    return float(eps)
+
+
 class _RMSNormReplacement(nn.Module):
-    """RMSNorm through ``torch.ops.autokernel.rmsnorm`` with the module's own eps."""
+    """RMSNorm through ``torch.ops.autokernel.rmsnorm`` with the module's own eps.
+
+    HF's GemmaRMSNorm scales by ``1 + weight`` (its weight is stored as an
+    offset from one); the replacement applies the same offset, so the swap
+    keeps that module's output."""
 
     def __init__(self, original: nn.Module, kernel_fn: Callable):
         super().__init__()
         self.weight = original.weight
-        self.eps = getattr(original, "eps", 1e-6)
+        self.eps = _norm_eps(original)
+        self.weight_offset = 1.0 if type(original).__name__ == "GemmaRMSNorm" else 0.0
         self.kernel_fn = kernel_fn
         self._autograd_op = _autokernel_ops().rmsnorm
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
-        out = self._autograd_op(x.reshape(-1, shape[-1]), self.weight, float(self.eps))
+        w = self.weight + self.weight_offset if self.weight_offset else self.weight
+        out = self._autograd_op(x.reshape(-1, shape[-1]), w, float(self.eps))
         return out.view(shape)
 
 
@@ -108,7 +129,7 @@ class _FusedResidualRMSNormBlockReplacement(nn.Module):
         self.feed_forward = getattr(original, ffn_attr)
         ffn_norm = getattr(original, ffn_norm_attr)
         self.ffn_norm_weight = ffn_norm.weight
-        self.eps = float(getattr(ffn_norm, "eps", getattr(ffn_norm, "variance_epsilon", 1e-6)))
+        self.eps = _norm_eps(ffn_norm)
         self.kernel_fn_dual = kernel_fn_dual
         self._autograd_dual = _autokernel_ops().fused_res_rmsnorm
 

@@ -130,6 +130,17 @@ __device__ __forceinline__ float tanh_f32(float a) {
   return copysignf(r, a);
 }
 
+// Grid cap of the row kernels. They walk their rows (or row groups) with a
+// workgroup-uniform grid stride, so any row count runs on a grid of at most
+// this many workgroups: 2^20 workgroups x 1024 threads stays inside HIP's
+// 2^32 work-items per launch dimension and still fills all 256 CUs many
+// times over.
+constexpr int64_t kMaxRowGrid = (int64_t)1 << 20;
+
+inline unsigned row_grid(int64_t units) {
+  return (unsigned)(units < kMaxRowGrid ? units : kMaxRowGrid);
+}
+
 __host__ __device__ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
@@ -143,6 +154,14 @@ int ak_set_error(int code, const char* fmt, ...);
 int ak_check_launch(const char* what);
 
 inline hipStream_t ak_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Whether rows x pitch elements of esz bytes (the last row only `cols` long)
+// stay addressable with signed 64-bit byte offsets.
+inline bool ak_extent_ok(int64_t rows, int64_t pitch, int64_t cols, int esz) {
+  const int64_t lim = INT64_MAX / (esz > 0 ? esz : 1);
+  if (rows <= 1 || pitch <= 0) return cols <= lim;
+  return pitch <= lim && cols <= lim && (rows - 1) <= (lim - cols) / pitch;
+}
 
 inline int ak_dtype_size(int dtype) {
   return dtype == AK_DTYPE_F32 ? 4 : (dtype == AK_DTYPE_F16 || dtype == AK_DTYPE_BF16) ? 2 : 0;

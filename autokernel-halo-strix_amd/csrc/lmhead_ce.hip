@@ -42,6 +42,8 @@
 //   the 16 MFMAs of a 16-wide K slice run over 16 different accumulators
 //   while the fragments of the slice after next are read; one barrier per K
 //   block (after its second slice) publishes the next block's slots.
+#include <atomic>
+
 #include "ak_common.h"
 
 namespace ak {
@@ -786,17 +788,20 @@ WsLayout ws_layout(int64_t n_rows, int64_t vocab) {
   return w;
 }
 
+// Compute units of the current device, queried once per device. The cache
+// entries are atomics: concurrent first calls may both query the attribute,
+// but they store the same value and no caller reads a torn entry.
 int cu_count() {
-  static int cached[64];
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 template <typename T, bool kCap, bool kLs>

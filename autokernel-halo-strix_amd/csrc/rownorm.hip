@@ -106,39 +106,42 @@ rownorm_vec_kernel(const T* __restrict__ x, const T* __restrict__ r,
   }
 }
 
-// Any width / alignment: one 256-thread workgroup per row, scalar accesses,
-// the hidden state recomputed (bit-identically) in the second pass.
+// Any width / alignment: a 256-thread workgroup per row (rows by grid
+// stride), scalar accesses, the hidden state recomputed (bit-identically) in
+// the second pass.
 template <typename T, bool RES>
 __global__ void __launch_bounds__(256)
 rownorm_generic_kernel(const T* __restrict__ x, const T* __restrict__ r,
                        const T* __restrict__ w, T* __restrict__ nr, T* __restrict__ y,
                        int64_t rows, int cols, int64_t ld_x, int64_t ld_r,
                        int64_t ld_nr, int64_t ld_y, float eps) {
-  const int64_t row = blockIdx.x;
-  auto hidden = [&](int c) -> float {
-    if constexpr (RES) {
-      return to_f32(from_f32<T>(to_f32(x[row * ld_x + c]) + to_f32(r[row * ld_r + c])));
-    } else {
-      return to_f32(x[row * ld_x + c]);
-    }
-  };
-  float ss = 0.0f;
-  for (int c = threadIdx.x; c < cols; c += 256) {
-    const float h = hidden(c);
-    ss = fmaf(h, h, ss);
-  }
-  ss = wave_sum(ss);
   __shared__ float part[4];
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = ss;
-  __syncthreads();
-  ss = part[0] + part[1] + part[2] + part[3];
-  const float rms = sqrtf(ss / (float)cols + eps);
-  for (int c = threadIdx.x; c < cols; c += 256) {
-    const float h = hidden(c);
-    if constexpr (RES) {
-      if (nr != nullptr) nr[row * ld_nr + c] = from_f32<T>(h);
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    auto hidden = [&](int c) -> float {
+      if constexpr (RES) {
+        return to_f32(from_f32<T>(to_f32(x[row * ld_x + c]) + to_f32(r[row * ld_r + c])));
+      } else {
+        return to_f32(x[row * ld_x + c]);
+      }
+    };
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      const float h = hidden(c);
+      ss = fmaf(h, h, ss);
     }
-    y[row * ld_y + c] = from_f32<T>((h / rms) * to_f32(w[c]));
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = ss;
+    __syncthreads();
+    ss = part[0] + part[1] + part[2] + part[3];
+    __syncthreads();  // part is rewritten for the next row
+    const float rms = sqrtf(ss / (float)cols + eps);
+    for (int c = threadIdx.x; c < cols; c += 256) {
+      const float h = hidden(c);
+      if constexpr (RES) {
+        if (nr != nullptr) nr[row * ld_nr + c] = from_f32<T>(h);
+      }
+      y[row * ld_y + c] = from_f32<T>((h / rms) * to_f32(w[c]));
+    }
   }
 }
 
@@ -147,8 +150,8 @@ void launch_vec(const T* x, const T* r, const T* w, T* nr, T* y, int64_t rows, i
                 int64_t ld_x, int64_t ld_r, int64_t ld_nr, int64_t ld_y, float eps,
                 hipStream_t s) {
   constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
-  const int64_t grid = (rows + RPW - 1) / RPW;
-  rownorm_vec_kernel<T, RES, VPT, TPR, true><<<dim3((unsigned)grid), dim3(TPR * RPW), 0, s>>>(
+  const unsigned grid = row_grid((rows + RPW - 1) / RPW);
+  rownorm_vec_kernel<T, RES, VPT, TPR, true><<<dim3(grid), dim3(TPR * RPW), 0, s>>>(
       x, r, w, nr, y, rows, cols, ld_x, ld_r, ld_nr, ld_y, eps);
 }
 
@@ -174,7 +177,7 @@ int dispatch(const void* xv, const void* rv, const void* wv, void* nrv, void* yv
   // (fused C3 shape: 1 vector x 512 threads beat 8 vectors x 64 threads by
   // 25% on MI355X).
   if (!vec_ok) {
-    rownorm_generic_kernel<T, RES><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
+    rownorm_generic_kernel<T, RES><<<dim3(row_grid(rows)), dim3(256), 0, s>>>(
         x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps);
   } else if (nvec <= 64) AK_LAUNCH(1, 64);
   else if (nvec <= 128) AK_LAUNCH(1, 128);
@@ -185,7 +188,7 @@ int dispatch(const void* xv, const void* rv, const void* wv, void* nrv, void* yv
   else if (nvec <= 4096) AK_LAUNCH(4, 1024);
   else if (nvec <= 8192) AK_LAUNCH(8, 1024);
   else {
-    rownorm_generic_kernel<T, RES><<<dim3((unsigned)rows), dim3(256), 0, s>>>(
+    rownorm_generic_kernel<T, RES><<<dim3(row_grid(rows)), dim3(256), 0, s>>>(
         x, r, w, nr, y, rows, c, ld_x, ld_r, ld_nr, ld_y, eps);
   }
 #undef AK_LAUNCH
@@ -197,9 +200,10 @@ int check_common(const void* x, const void* w, const void* y, int64_t rows, int6
   if (ak_dtype_size(dtype) == 0) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", name, dtype);
   if (rows < 0 || cols <= 0 || cols > (int64_t)1 << 30)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape rows=%lld cols=%lld", name, (long long)rows, (long long)cols);
-  if (rows > 0xFFFFFFFFll) return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld exceeds 2^32-1", name, (long long)rows);
   if (ld_x < cols || ld_y < cols)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  if (!ak_extent_ok(rows, ld_x, cols, ak_dtype_size(dtype)) || !ak_extent_ok(rows, ld_y, cols, ak_dtype_size(dtype)))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld x pitch exceed 64-bit addressing", name, (long long)rows);
   if (rows > 0 && (!x || !w || !y)) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   return AK_OK;
 }
@@ -232,6 +236,9 @@ extern "C" int ak_fused_add_rmsnorm_fwd(const void* x, const void* residual, con
   if (rows > 0 && !residual) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null residual", name);
   if (ld_r < cols || (new_residual && ld_nr < cols))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  if (!ak_extent_ok(rows, ld_r, cols, ak_dtype_size(dtype)) ||
+      (new_residual && !ak_extent_ok(rows, ld_nr, cols, ak_dtype_size(dtype))))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld x pitch exceed 64-bit addressing", name, (long long)rows);
   if (rows == 0) return AK_OK;
   hipStream_t s = ak_stream(stream);
   switch (dtype) {

@@ -5,8 +5,8 @@
 // and written once, with nontemporal accesses. Rows of up to 128 16-byte
 // vectors are owned by one wave (no barriers), wider rows by up to 1024
 // threads holding one vector each (up to 8 past 1024 vectors). Rows are
-// indexed with 64-bit arithmetic and every row gets its own owner, so there
-// is no grid-size cap on the row count.
+// indexed with 64-bit arithmetic and walked by grid stride on a capped grid,
+// so every row is written whatever the row count.
 //
 // -inf logits give exp2(-inf) = 0 exactly; a row with a single finite entry
 // returns exactly 1.0 there. The file is built without fast-math so those
@@ -113,14 +113,11 @@ __device__ __forceinline__ MaxSum combine(MaxSum a, MaxSum b) {
   return {m, sa + sb};
 }
 
-// Any width / alignment: one 256-thread workgroup per row, two passes over
-// global memory (online max/sum, then normalise).
+// Any width / alignment: a 256-thread workgroup per row (rows by grid
+// stride), two passes over global memory (online max/sum, then normalise).
 template <typename T>
-__global__ void __launch_bounds__(256)
-softmax_generic_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
-                       int64_t ld_x, int64_t ld_y) {
-  const int64_t row = blockIdx.x;
-  const T* xr = x + row * ld_x;
+__device__ void softmax_generic_row(const T* __restrict__ xr, T* __restrict__ yr, int cols,
+                                    MaxSum* part) {
   MaxSum st{-INFINITY, 0.0f};
   for (int c = threadIdx.x; c < cols; c += 256) {
     const float v = to_f32(xr[c]);
@@ -139,17 +136,26 @@ softmax_generic_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
     MaxSum o{__shfl_xor(st.m, off, 64), __shfl_xor(st.s, off, 64)};
     st = (st.m != st.m || o.m != o.m) ? MaxSum{NAN, NAN} : combine(st, o);
   }
-  __shared__ MaxSum part[4];
   if ((threadIdx.x & 63) == 0) part[threadIdx.x / 64] = st;
   __syncthreads();
   st = part[0];
   for (int i = 1; i < 4; ++i) {
     st = (st.m != st.m || part[i].m != part[i].m) ? MaxSum{NAN, NAN} : combine(st, part[i]);
   }
+  __syncthreads();  // part is rewritten for the next row
   const float inv = 1.0f / st.s;
-  T* yr = y + row * ld_y;
   for (int c = threadIdx.x; c < cols; c += 256) {
     yr[c] = from_f32<T>(fast_exp(to_f32(xr[c]) - st.m) * inv);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+softmax_generic_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
+                       int64_t ld_x, int64_t ld_y) {
+  __shared__ MaxSum part[4];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    softmax_generic_row(x + row * ld_x, y + row * ld_y, cols, part);
   }
 }
 
@@ -157,8 +163,8 @@ template <typename T, int VPT, int TPR, bool NT>
 void launch_vec(const T* x, T* y, int64_t rows, int cols, int64_t ld_x, int64_t ld_y,
                 hipStream_t s) {
   constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
-  const int64_t grid = (rows + RPW - 1) / RPW;
-  softmax_vec_kernel<T, VPT, TPR, NT><<<dim3((unsigned)grid), dim3(TPR * RPW), 0, s>>>(
+  const unsigned grid = row_grid((rows + RPW - 1) / RPW);
+  softmax_vec_kernel<T, VPT, TPR, NT><<<dim3(grid), dim3(TPR * RPW), 0, s>>>(
       x, y, rows, cols, ld_x, ld_y);
 }
 
@@ -174,7 +180,7 @@ int dispatch(const void* xv, void* yv, int64_t rows, int64_t cols, int64_t ld_x,
   const int c = (int)cols;
 #define AK_LAUNCH(VPT, TPR) launch_vec<T, VPT, TPR, true>(x, y, rows, c, ld_x, ld_y, s)
   if (!vec_ok || nvec > 8192) {
-    softmax_generic_kernel<T><<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, y, rows, c, ld_x, ld_y);
+    softmax_generic_kernel<T><<<dim3(row_grid(rows)), dim3(256), 0, s>>>(x, y, rows, c, ld_x, ld_y);
   } else if (nvec <= 64) AK_LAUNCH(1, 64);
   else if (nvec <= 128) AK_LAUNCH(2, 64);
   else if (nvec <= 256) AK_LAUNCH(1, 256);
@@ -196,8 +202,9 @@ extern "C" int ak_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols
   if (ak_dtype_size(dtype) == 0) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", name, dtype);
   if (rows < 0 || cols <= 0 || cols > (int64_t)1 << 30)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape rows=%lld cols=%lld", name, (long long)rows, (long long)cols);
-  if (rows > 0xFFFFFFFFll) return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld exceeds 2^32-1", name, (long long)rows);
   if (ld_x < cols || ld_y < cols) return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  if (!ak_extent_ok(rows, ld_x, cols, ak_dtype_size(dtype)) || !ak_extent_ok(rows, ld_y, cols, ak_dtype_size(dtype)))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld x pitch exceed 64-bit addressing", name, (long long)rows);
   if (rows == 0) return AK_OK;
   if (!x || !y) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   hipStream_t s = ak_stream(stream);

@@ -9,16 +9,28 @@ Drop-in for the reference module ``kernels/ce_fused.py``: same public names
 * per row: ``lse = logsumexp(x)``, ``loss = lse - x[t]`` (label smoothing
   ``a``: ``lse - (1-a) x[t] - a mean(x)``; softcap: ``x = c tanh(x / c)``),
   ignored rows give loss 0 and a zero gradient row;
-* scalar loss = sum over non-ignored rows / max(1, #non-ignored);
-* "fused" mode writes the pre-scaled gradient during the forward; "tiny"
-  mode saves row max / sum and recomputes the gradient in the backward;
-  ``z_loss_weight > 0`` forces tiny mode and adds ``w * mean(lse^2)``.
+* scalar loss = sum over non-ignored rows / max(1, #non-ignored), plus
+  ``w * sum(lse^2) / max(1, #non-ignored)`` with a z-loss weight ``w``;
+* "fused" mode writes the gradient during the forward; "tiny" mode saves
+  the row max / sum and recomputes the gradient in the backward.
 
-The kernels are ``ak_ce_fwd`` / ``ak_ce_bwd_tiny`` (``csrc/ce_rows.hip``).
+Everything runs on the device in four small steps, with no host read in the
+forward: ``ak_ce_count_valid`` counts the rows that take part,
+``ak_ce_fwd`` computes the per-row results (and, in fused mode, the gradient
+already scaled by 1 / count read from device memory), ``ak_ce_mean`` reduces
+them in a fixed order, and ``ak_ce_bwd_tiny`` is the tiny-mode backward with
+the upstream gradient taken from device memory. The z-loss gradient
+``2 w lse p / count`` is part of both gradient kernels, so the z-loss works in
+either mode and is taken through the softcap.
+
 Differences from the reference, all deliberate: bf16 and fp32 logits run on
 the GPU kernels in their own dtype (the reference cast bf16 to fp16 and sent
 fp32 to PyTorch); an out-of-range target (neither in ``[0, V)`` nor
-``ignore_index``) yields a NaN loss instead of an out-of-bounds read.
+``ignore_index``) yields a NaN loss instead of an out-of-bounds read; the
+tiny-mode gradient is scaled by 1 / #non-ignored rows (the gradient of the
+returned mean; the reference scaled it by 1 / batch); a z-loss no longer
+switches fused mode to tiny mode, and its gradient includes the softcap's
+``1 - tanh^2`` factor.
 """
 
 import os
@@ -55,6 +67,23 @@ HIP_FWD_SRC = os.path.join(_lib.CSRC_DIR, "ce_rows.hip")
 HIP_BWD_SRC = HIP_FWD_SRC
 
 
+# A target value no int64 row holds: "no ignore_index".
+_NO_IGNORE = -(2 ** 63)
+
+
+def _row_problem(logits: torch.Tensor, targets: torch.Tensor):
+    """Checks and brings logits to a ``[rows, vocab]`` view the row kernels take
+    and targets to contiguous int64."""
+    _lib.require_device(logits, targets)
+    if logits.dim() != 2:
+        raise ValueError("logits must be [batch, vocab]")
+    _lib.dtype_code(logits.dtype)
+    tg = targets.reshape(-1).contiguous().to(torch.int64)
+    if tg.numel() != logits.size(0):
+        raise ValueError(f"{tg.numel()} targets for {logits.size(0)} rows")
+    return _lib.as_rows(logits, logits.size(1)), tg
+
+
 class _FwdModule:
     """Stands where the reference's JIT-built forward module stood."""
 
@@ -62,13 +91,7 @@ class _FwdModule:
     def cross_entropy_fwd_hip(logits, targets, softcap, ignore_index, label_smoothing,
                               write_grad, save_max_sum, scale_grad):
         """Returns ``[losses, lse, row_max, row_sum, grad_logits]`` (None where not requested)."""
-        _lib.require_device(logits, targets)
-        if logits.dim() != 2:
-            raise ValueError("logits must be [batch, vocab]")
-        _lib.dtype_code(logits.dtype)
-        if logits.stride(-1) != 1:
-            logits = logits.contiguous()
-        targets = targets.contiguous().to(torch.int64)
+        logits, targets = _row_problem(logits, targets)
         B = logits.size(0)
         f32 = dict(dtype=torch.float32, device=logits.device)
         losses = torch.empty(B, **f32)
@@ -87,8 +110,7 @@ class _BwdModule:
     def cross_entropy_bwd_tiny_hip(logits, targets, row_maxes, row_sums, softcap, ignore_index,
                                    label_smoothing, scale_grad):
         _lib.require_device(logits, targets, row_maxes, row_sums)
-        if logits.stride(-1) != 1:
-            logits = logits.contiguous()
+        logits = _lib.as_rows(logits, logits.size(-1))
         grad = torch.empty(logits.shape, dtype=logits.dtype, device=logits.device)
         if logits.size(0):
             _lib.ce_bwd_tiny(logits, targets.contiguous().to(torch.int64),
@@ -111,118 +133,79 @@ def _get_bwd_module():
 
 
 class _CrossEntropyHIP(torch.autograd.Function):
-    """CE with fused (gradient written in the forward) or tiny (recompute) backward.
+    """Mean CE over the counted rows, with the gradient either written by the
+    forward (``mode="fused"``) or recomputed from the saved row statistics
+    (``mode="tiny"``).
 
-    Arguments and return values as ``kernels/ce_fused.py:557-698`` of the
-    reference: ``(logits, targets, softcap, ignore_index, label_smoothing,
-    mode, return_z, z_loss_weight)`` -> loss, or ``(loss, lse)`` if return_z.
+    Arguments and return values are those of ``kernels/ce_fused.py:557-578``:
+    ``(logits, targets, softcap, ignore_index, label_smoothing, mode,
+    return_z, z_loss_weight)`` -> ``loss``, or ``(loss, lse)`` with
+    ``return_z``. ``ignore_index=None`` counts every row.
     """
 
     @staticmethod
     def forward(ctx, logits, targets, softcap, ignore_index, label_smoothing, mode, return_z,
                 z_loss_weight=0.0):
-        mod = _get_fwd_module()
-        B = logits.size(0)
-        z_loss_weight = float(z_loss_weight)
-        if z_loss_weight > 0.0 and mode != "tiny":
-            mode = "tiny"
-        write_grad = 1 if mode == "fused" else 0
-        save_max_sum = 1 if mode == "tiny" else 0
-
-        if ignore_index is not None:
-            valid_mask = targets != ignore_index
-            n_valid_t = valid_mask.sum().to(torch.float32).clamp_(min=1.0)
+        rows2d, tg = _row_problem(logits, targets)
+        n = rows2d.size(0)
+        ign = _NO_IGNORE if ignore_index is None else int(ignore_index)
+        params = (float(softcap), ign, float(label_smoothing), float(z_loss_weight))
+        on_dev = dict(dtype=torch.float32, device=rows2d.device)
+        losses, lse = torch.empty(n, **on_dev), torch.empty(n, **on_dev)
+        # [max(1, #counted rows), its reciprocal], never read on the host
+        denom = _lib.ce_count_valid(tg, ign)
+        keep_grad = mode == "fused"
+        if keep_grad:
+            grad, row_max, row_sum = torch.empty(rows2d.shape, dtype=rows2d.dtype,
+                                                 device=rows2d.device), None, None
         else:
-            valid_mask = None
-            n_valid_t = torch.tensor(float(B), device=logits.device, dtype=torch.float32)
+            grad, row_max, row_sum = None, torch.empty(n, **on_dev), torch.empty(n, **on_dev)
+        if n:
+            _lib.ce_fwd(rows2d, tg, losses, lse, row_max, row_sum, grad, params[0], ign, params[2],
+                        1.0, scale_dev=denom[1:], z_loss_weight=params[3])
+        loss = _lib.ce_mean(losses, lse, tg, ign, params[3])
 
-        if write_grad:
-            n_valid_scalar = n_valid_t.item()
-            scale_grad = 1.0 / n_valid_scalar
+        ctx.params = params
+        ctx.keep_grad = keep_grad
+        if keep_grad:
+            ctx.save_for_backward(grad)
         else:
-            n_valid_scalar = float(B)
-            scale_grad = 1.0
-
-        ign = int(ignore_index) if ignore_index is not None else -(2 ** 63)
-        losses, lse, row_max, row_sum, grad_logits = mod.cross_entropy_fwd_hip(
-            logits, targets, float(softcap), ign, float(label_smoothing), int(write_grad),
-            int(save_max_sum), float(scale_grad))
-
-        if valid_mask is not None:
-            loss = (losses * valid_mask.to(torch.float32)).sum() / n_valid_t
-        else:
-            loss = losses.mean()
-
-        if z_loss_weight > 0.0:
-            if valid_mask is not None:
-                lse_valid = lse * valid_mask.to(lse.dtype)
-                z_loss = z_loss_weight * (lse_valid * lse_valid).sum() / n_valid_t
-            else:
-                z_loss = z_loss_weight * lse.pow(2).mean()
-            loss = loss + z_loss
-
-        ctx.mode = mode
-        ctx.softcap = float(softcap)
-        ctx.ignore_index = ign
-        ctx.has_ignore = ignore_index is not None
-        ctx.label_smoothing = float(label_smoothing)
-        ctx.return_z = bool(return_z)
-        ctx.n_valid_item = n_valid_scalar
-        ctx.n_valid_t = n_valid_t
-        ctx.z_loss_weight = z_loss_weight
-        if mode == "fused":
-            ctx.save_for_backward(grad_logits)
-            ctx.has_tiny = False
-        else:
-            ctx.save_for_backward(logits, targets, row_max, row_sum)
-            ctx.has_tiny = True
+            ctx.save_for_backward(rows2d, tg, row_max, row_sum, denom)
         ctx.mark_non_differentiable(lse)
-        if return_z:
-            return loss, lse
-        return loss
+        return (loss, lse) if return_z else loss
 
     @staticmethod
-    def backward(ctx, grad_loss, *rest):
-        nones = (None,) * 7
-        if ctx.has_tiny:
-            logits, targets, row_max, row_sum = ctx.saved_tensors
-            # The loss is a mean over non-ignored rows, so its gradient is
-            # scaled by 1 / n_valid (torch.nn.functional.cross_entropy's
-            # gradient); the reference's tiny mode used 1 / batch here
-            # (kernels/ce_fused.py:607, :661).
-            n_valid = float(ctx.n_valid_t.item())
-            g = float(grad_loss.item()) if grad_loss.dim() == 0 else 1.0
-            grad_logits = _get_bwd_module().cross_entropy_bwd_tiny_hip(
-                logits, targets, row_max, row_sum, ctx.softcap, ctx.ignore_index,
-                ctx.label_smoothing, g / n_valid)
-            if ctx.z_loss_weight > 0.0:
-                # d/dx_ij of w * lse_i^2 / N = (2 w / N) * lse_i * softmax_ij
-                with torch.no_grad():
-                    shifted = logits.float() - row_max.unsqueeze(-1)
-                    softmax = torch.exp(shifted) / row_sum.unsqueeze(-1)
-                    lse_vec = row_max + torch.log(row_sum)
-                    coef = (2.0 * ctx.z_loss_weight / n_valid) * g
-                    z_grad = coef * lse_vec.unsqueeze(-1) * softmax
-                    if ctx.has_ignore:
-                        z_grad = z_grad * (targets != ctx.ignore_index).float().unsqueeze(-1)
-                    grad_logits = grad_logits + z_grad.to(grad_logits.dtype)
-            return (grad_logits,) + nones
-        (saved_grad,) = ctx.saved_tensors
-        if grad_loss.dim() == 0 and grad_loss.item() == 1.0:
-            return (saved_grad,) + nones
-        return (saved_grad * grad_loss.to(saved_grad.dtype),) + nones
+    def backward(ctx, grad_loss, *unused):
+        softcap, ign, ls, zw = ctx.params
+        if ctx.keep_grad:
+            (grad,) = ctx.saved_tensors
+            # The saved gradient already carries 1 / #counted rows. An upstream
+            # gradient of exactly 1 (loss.backward()) needs no further pass.
+            up = float(grad_loss)
+            if up != 1.0:
+                grad = grad * up
+        else:
+            rows2d, tg, row_max, row_sum, denom = ctx.saved_tensors
+            # upstream gradient / #counted rows, kept on the device
+            scale = grad_loss.detach().to(torch.float32).reshape(1) * denom[1:]
+            grad = torch.empty(rows2d.shape, dtype=rows2d.dtype, device=rows2d.device)
+            if rows2d.size(0):
+                _lib.ce_bwd_tiny(rows2d, tg, row_max, row_sum, grad, softcap, ign, ls, 1.0, zw,
+                                 scale_dev=scale)
+        return (grad,) + (None,) * 7
 
 
 def kernel_fn(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
     """Mean cross-entropy; matches ``reference.cross_entropy_ref`` (ignore_index -100)."""
-    _lib.require_device(logits, targets)
-    if not (logits.requires_grad and torch.is_grad_enabled()):
-        losses, _, _, _, _ = _get_fwd_module().cross_entropy_fwd_hip(
-            logits, targets, 0.0, -100, 0.0, 0, 0, 1.0)
-        valid = (targets != -100).to(torch.float32)
-        n_valid = valid.sum().clamp(min=1.0)
-        return (losses * valid).sum() / n_valid
-    return _CrossEntropyHIP.apply(logits, targets, 0.0, -100, 0.0, "fused", False, 0.0)
+    if logits.requires_grad and torch.is_grad_enabled():
+        return _CrossEntropyHIP.apply(logits, targets, 0.0, -100, 0.0, "fused", False, 0.0)
+    rows2d, tg = _row_problem(logits, targets)
+    on_dev = dict(dtype=torch.float32, device=rows2d.device)
+    losses = torch.empty(rows2d.size(0), **on_dev)
+    lse = torch.empty(rows2d.size(0), **on_dev)
+    if rows2d.size(0):
+        _lib.ce_fwd(rows2d, tg, losses, lse, None, None, None, 0.0, -100, 0.0, 1.0)
+    return _lib.ce_mean(losses, None, tg, -100)
 
 
 def ce_full(logits: torch.Tensor, targets: torch.Tensor, *, softcap: float = 0.0,

@@ -54,9 +54,12 @@ _SIGNATURES = {
                                  _f32, _int, _c_void_p],
     "ak_softmax_fwd": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
     "ak_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                  _i64, _i64, _i64, _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
+                  _i64, _i64, _i64, _i64, _f32, _i64, _f32, _f32, _f32, _c_void_p, _int, _c_void_p],
     "ak_ce_bwd_tiny": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
-                       _i64, _f32, _i64, _f32, _f32, _int, _c_void_p],
+                       _i64, _f32, _i64, _f32, _f32, _f32, _c_void_p, _int, _c_void_p],
+    "ak_ce_count_valid": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "ak_ce_mean": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p, _c_void_p,
+                   _c_void_p],
     "ak_lmhead_ce_workspace_bytes": [_i64, _i64],
     "ak_lmhead_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
@@ -172,7 +175,12 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def _rows_view(t: torch.Tensor, name: str) -> int:
-    """Row pitch (elements) of a 2-D view whose last dim is contiguous."""
+    """Row pitch (elements) of a 2-D view whose last dim is contiguous.
+
+    The pitch is passed on as it is, so rows that overlap (``stride(0) <
+    cols``, e.g. an ``expand``-ed tensor with ``stride(0) == 0``) reach the
+    C-ABI's pitch check and are rejected there; :func:`as_rows` copies such
+    views first. A single row has no pitch and reports ``cols``."""
     shape = t.shape
     if len(shape) != 2:
         raise ValueError(f"{name} must be 2-D, got shape {tuple(shape)}")
@@ -180,7 +188,18 @@ def _rows_view(t: torch.Tensor, name: str) -> int:
     n0, n1 = shape
     if s1 != 1 and n1 > 1:
         raise ValueError(f"{name} must have a contiguous last dimension")
-    return max(s0, n1) if n0 > 1 else n1
+    return s0 if n0 > 1 else n1
+
+
+def as_rows(t: torch.Tensor, cols: int) -> torch.Tensor:
+    """``t`` as a ``[rows, cols]`` view the row kernels take: last dimension
+    contiguous and rows that do not overlap (row pitch >= cols). Views that
+    break either (a transposed last dim, an ``expand``-ed batch dim) are
+    copied; everything else is passed through without a copy."""
+    t2 = t.reshape(-1, cols)
+    if (cols > 1 and t2.stride(-1) != 1) or (t2.shape[0] > 1 and t2.stride(0) < cols):
+        t2 = t2.contiguous()
+    return t2
 
 
 # ---------------------------------------------------------------------------
@@ -260,30 +279,63 @@ def softmax(x: torch.Tensor, y: torch.Tensor) -> None:
 def ce_fwd(logits: torch.Tensor, targets: torch.Tensor, losses: torch.Tensor, lse: torch.Tensor,
            row_max: Optional[torch.Tensor], row_sum: Optional[torch.Tensor],
            grad: Optional[torch.Tensor], softcap: float, ignore_index: int,
-           label_smoothing: float, scale_grad: float) -> None:
-    require_device(logits, targets, losses, lse, row_max, row_sum, grad)
+           label_smoothing: float, scale_grad: float,
+           scale_dev: Optional[torch.Tensor] = None, z_loss_weight: float = 0.0) -> None:
+    """Per-row CE over ``logits [rows, vocab]``; the gradient (when ``grad`` is
+    given, including the z-loss term) is scaled by ``scale_grad`` times the
+    device value ``scale_dev[0]``."""
+    require_device(logits, targets, losses, lse, row_max, row_sum, grad, scale_dev)
     rows, vocab = logits.shape
     ld_g = _rows_view(grad, "grad") if grad is not None else vocab
     with _on_device(logits):
         rc = load().ak_ce_fwd(_ptr(logits), _ptr(targets), _ptr(losses), _ptr(lse), _ptr(row_max),
                               _ptr(row_sum), _ptr(grad), rows, vocab, _rows_view(logits, "logits"),
                               ld_g, float(softcap), int(ignore_index), float(label_smoothing),
-                              float(scale_grad), dtype_code(logits.dtype), _stream(logits))
+                              float(scale_grad), float(z_loss_weight), _ptr(scale_dev),
+                              dtype_code(logits.dtype),
+                              _stream(logits))
     _check(rc, "ak_ce_fwd")
 
 
 def ce_bwd_tiny(logits: torch.Tensor, targets: torch.Tensor, row_max: torch.Tensor,
                 row_sum: torch.Tensor, grad: torch.Tensor, softcap: float, ignore_index: int,
-                label_smoothing: float, scale_grad: float) -> None:
-    require_device(logits, targets, row_max, row_sum, grad)
+                label_smoothing: float, scale_grad: float, z_loss_weight: float = 0.0,
+                scale_dev: Optional[torch.Tensor] = None) -> None:
+    require_device(logits, targets, row_max, row_sum, grad, scale_dev)
     rows, vocab = logits.shape
     with _on_device(logits):
         rc = load().ak_ce_bwd_tiny(_ptr(logits), _ptr(targets), _ptr(row_max), _ptr(row_sum),
                                    _ptr(grad), rows, vocab, _rows_view(logits, "logits"),
                                    _rows_view(grad, "grad"), float(softcap), int(ignore_index),
                                    float(label_smoothing), float(scale_grad),
+                                   float(z_loss_weight), _ptr(scale_dev),
                                    dtype_code(logits.dtype), _stream(logits))
     _check(rc, "ak_ce_bwd_tiny")
+
+
+def ce_count_valid(targets: torch.Tensor, ignore_index: int) -> torch.Tensor:
+    """fp32 device tensor ``[max(1, #counted rows), 1 / that]``."""
+    require_device(targets)
+    denom = torch.empty(2, dtype=torch.float32, device=targets.device)
+    with _on_device(targets):
+        rc = load().ak_ce_count_valid(_ptr(targets), targets.numel(), int(ignore_index),
+                                      _ptr(denom), _stream(targets))
+    _check(rc, "ak_ce_count_valid")
+    return denom
+
+
+def ce_mean(losses: torch.Tensor, lse: Optional[torch.Tensor], targets: torch.Tensor,
+            ignore_index: int, z_loss_weight: float = 0.0,
+            n_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """0-d fp32 device tensor: the mean (+ z-loss) over counted rows."""
+    require_device(losses, lse, targets, n_valid)
+    loss = torch.empty((), dtype=torch.float32, device=losses.device)
+    with _on_device(losses):
+        rc = load().ak_ce_mean(_ptr(losses), _ptr(lse), _ptr(targets), targets.numel(),
+                               int(ignore_index), float(z_loss_weight), _ptr(loss),
+                               _ptr(n_valid), _stream(losses))
+    _check(rc, "ak_ce_mean")
+    return loss
 
 
 def lmhead_ce_workspace_bytes(n_rows: int, vocab: int) -> int:

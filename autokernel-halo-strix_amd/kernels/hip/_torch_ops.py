@@ -19,8 +19,8 @@ selects the same gradient as fp32 PyTorch formulas on the GPU instead (the
 gradient of ``rmsnorm_backward.py:166-168`` /
 ``fused_residual_rmsnorm_backward.py:168-170``). The diagonal scan's backward
 runs ``kernels.hip.selective_scan_backward`` (the gradient of the reference's
-sequential formula, ``_torch_ops.py:346-386``, which is also the formula
-path). Importing this module registers the ops.
+sequential formula, ``_torch_ops.py:346-386``); its formula path is torch
+autograd through the recurrence written as torch ops. Importing this module registers the ops.
 
 Autocast: under ``torch.autocast("cuda", dtype=...)`` floating inputs are
 cast to the active autocast dtype (fp16 or bf16) before the kernel runs.
@@ -34,31 +34,29 @@ from typing import Tuple
 
 import torch
 
-# AUTOKERNEL_NO_BWD_HIP=1 selects the fp32 PyTorch formulas for the norm
-# backwards instead of the gfx950 backward kernels (reference
-# _torch_ops.py:20-50).
-_USE_BWD_HIP = os.environ.get("AUTOKERNEL_NO_BWD_HIP", "0") != "1"
+# Environment switch: AUTOKERNEL_NO_BWD_HIP=1 makes the backwards use the
+# fp32 PyTorch formulas below instead of the gfx950 backward kernels (the
+# reference's switch of the same name, _torch_ops.py:20-50).
+_BWD_KERNELS_ENABLED = os.environ.get("AUTOKERNEL_NO_BWD_HIP", "0") != "1"
 
 RMSNORM_EPS = 1e-6
 
+_is_compiling = getattr(getattr(torch, "compiler", None), "is_compiling", None) or (lambda: False)
 
-def _use_hip_backward():
-    """Whether the norm backwards run the gfx950 kernels: not when disabled,
-    and not while torch.compile traces (the formulas are traceable, the
-    library calls are not), as in the reference (_torch_ops.py:24-38)."""
-    if not _USE_BWD_HIP:
-        return False
-    try:
-        if torch.compiler.is_compiling():
-            return False
-    except AttributeError:
-        pass
-    return True
+
+def _bwd_kernels_for(t: torch.Tensor) -> bool:
+    """True when the backward of an op on ``t`` runs the gfx950 kernels.
+
+    The formulas take over when the kernels are switched off and while
+    torch.compile traces the backward (the formulas are traceable torch ops;
+    the library calls go through ctypes and are not)."""
+    return _BWD_KERNELS_ENABLED and t.is_cuda and not _is_compiling()
 
 
 def disable_hip_backward():
-    global _USE_BWD_HIP
-    _USE_BWD_HIP = False
+    """Use the PyTorch formulas for every backward from now on."""
+    global _BWD_KERNELS_ENABLED
+    _BWD_KERNELS_ENABLED = False
 
 
 def _register_autocast(op) -> None:
@@ -100,7 +98,7 @@ def _rmsnorm_setup(ctx, inputs, output):
 def _rmsnorm_backward(ctx, grad_output):
     x, weight = ctx.saved_tensors
     eps = ctx.eps
-    if _use_hip_backward() and x.is_cuda:
+    if _bwd_kernels_for(x):
         from kernels.hip.rmsnorm_backward import kernel_fn as rmsnorm_bwd_fn
         grad_x, grad_weight = rmsnorm_bwd_fn(x, weight, grad_output, eps)
         return grad_x, grad_weight.to(weight.dtype), None
@@ -149,7 +147,7 @@ def _fused_res_rmsnorm_setup(ctx, inputs, output):
 def _fused_res_rmsnorm_backward(ctx, grad_hidden, grad_normed):
     hidden, weight = ctx.saved_tensors
     eps = ctx.eps
-    if _use_hip_backward() and hidden.is_cuda and grad_normed is not None:
+    if _bwd_kernels_for(hidden) and grad_normed is not None:
         from kernels.hip.fused_residual_rmsnorm_backward import kernel_fn as fused_bwd_fn
         grad_x, _, grad_weight = fused_bwd_fn(hidden, weight, grad_hidden, grad_normed, eps)
         return grad_x, grad_x, grad_weight.to(weight.dtype), None
@@ -198,35 +196,31 @@ def _selective_scan_setup(ctx, inputs, output):
     ctx.save_for_backward(dA, dBx, C, D, x, output)
 
 
+def _diag_recurrence(dA, dBx, C, D, x):
+    """The forward recurrence as torch ops over [batch, seq, d_inner] (a
+    traceable stand-in for the kernel; its autograd gives the formula path's
+    gradients)."""
+    state = torch.zeros_like(dA[:, 0])
+    ys = []
+    for t in range(dA.shape[1]):
+        state = torch.addcmul(dBx[:, t], dA[:, t], state)
+        ys.append(C[:, t] * state)
+    return torch.stack(ys, dim=1) + D * x
+
+
 def _selective_scan_backward(ctx, grad_y):
     dA, dBx, C, D, x, _ = ctx.saved_tensors
-    if _use_hip_backward() and dA.is_cuda and dA.dtype == torch.float32:
-        # the gfx950 backward kernel, as the reference's _torch_ops.py:338-350
+    inputs = (dA, dBx, C, D, x)
+    if _bwd_kernels_for(dA):
+        # ak_diag_scan_bwd over fp32 copies (the kernel's state is fp32)
         from kernels.hip.selective_scan_backward import kernel_fn as scan_bwd_fn
-        g_dA, g_dBx, g_C, g_D, g_x = scan_bwd_fn(dA, dBx, C, D, x, grad_y.float())
-        return (g_dA.to(dA.dtype), g_dBx.to(dBx.dtype), g_C.to(C.dtype), g_D.to(D.dtype),
-                g_x.to(x.dtype))
-    gy = grad_y.float()
-    dA_f, dBx_f, C_f, D_f, x_f = dA.float(), dBx.float(), C.float(), D.float(), x.float()
-    batch, seqlen, d_inner = dA.shape
-    states = torch.zeros(batch, seqlen + 1, d_inner, dtype=torch.float32, device=dA.device)
-    for t in range(seqlen):
-        states[:, t + 1] = dA_f[:, t] * states[:, t] + dBx_f[:, t]
-    grad_dA = torch.zeros_like(dA_f)
-    grad_dBx = torch.zeros_like(dBx_f)
-    grad_C = torch.zeros_like(C_f)
-    grad_D = torch.zeros(d_inner, dtype=torch.float32, device=dA.device)
-    grad_state = torch.zeros(batch, d_inner, dtype=torch.float32, device=dA.device)
-    for t in range(seqlen - 1, -1, -1):
-        grad_C[:, t] = gy[:, t] * states[:, t + 1]
-        grad_state = grad_state + gy[:, t] * C_f[:, t]
-        grad_D = grad_D + (gy[:, t] * x_f[:, t]).sum(0)
-        grad_dA[:, t] = grad_state * states[:, t]
-        grad_dBx[:, t] = grad_state
-        grad_state = grad_state * dA_f[:, t]
-    grad_x = gy * D_f
-    return (grad_dA.to(dA.dtype), grad_dBx.to(dBx.dtype), grad_C.to(C.dtype),
-            grad_D.to(D.dtype), grad_x.to(x.dtype))
+        grads = scan_bwd_fn(*(t.float() for t in inputs), grad_y.float())
+    else:
+        with torch.enable_grad():
+            leaves = [t.detach().float().requires_grad_() for t in inputs]
+            y = _diag_recurrence(*leaves)
+            grads = torch.autograd.grad(y, leaves, grad_y.float())
+    return tuple(g.to(t.dtype) for g, t in zip(grads, inputs))
 
 
 selective_scan_op.register_autograd(_selective_scan_backward, setup_context=_selective_scan_setup)

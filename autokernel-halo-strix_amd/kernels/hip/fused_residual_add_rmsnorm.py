@@ -41,12 +41,8 @@ def _prepare(x, residual, weight):
     if weight.dtype != x.dtype:
         weight = weight.to(x.dtype)
     n = x.shape[-1]
-    x2 = x.reshape(-1, n)
-    r2 = residual.reshape(-1, n)
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
-    if r2.stride(-1) != 1:
-        r2 = r2.contiguous()
+    x2 = _lib.as_rows(x, n)
+    r2 = _lib.as_rows(residual, n)
     return x2, r2, weight.contiguous()
 
 

@@ -31,8 +31,7 @@ DEFAULT_EPS = 1e-6
 
 
 def _rows(t: torch.Tensor, d: int) -> torch.Tensor:
-    t2 = t.reshape(-1, d)
-    return t2 if t2.stride(-1) == 1 else t2.contiguous()
+    return _lib.as_rows(t, d)
 
 
 def kernel_fn(hidden: torch.Tensor, weight: torch.Tensor, grad_hidden: Optional[torch.Tensor],

@@ -39,9 +39,7 @@ def kernel_fn(x: torch.Tensor, weight: torch.Tensor, eps: float = DEFAULT_EPS) -
         weight = weight.to(x.dtype)
     weight = weight.contiguous()
     shape = x.shape
-    x2 = x.reshape(-1, shape[-1])
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
+    x2 = _lib.as_rows(x, shape[-1])
     y = torch.empty(shape, dtype=x.dtype, device=x.device)
     if y.numel():
         _lib.rmsnorm(x2, weight, y.view(-1, shape[-1]), eps)

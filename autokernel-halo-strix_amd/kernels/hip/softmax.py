@@ -34,9 +34,7 @@ def kernel_fn(x: torch.Tensor) -> torch.Tensor:
     shape = x.shape
     if x.dim() == 0:
         raise ValueError("softmax needs at least one dimension")
-    x2 = x.reshape(-1, shape[-1]) if x.dim() != 2 else x
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
+    x2 = _lib.as_rows(x, shape[-1])
     y = torch.empty(shape, dtype=x.dtype, device=x.device)
     if y.numel():
         _lib.softmax(x2, y.view(-1, shape[-1]))

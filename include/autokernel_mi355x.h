@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define AK_ABI_VERSION 1
+#define AK_ABI_VERSION 2
 
 #define AK_DTYPE_F32 0
 #define AK_DTYPE_F16 1
@@ -122,27 +122,60 @@ int ak_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols,
  * Replaces kernels/ce_fused.py:333-382 (cross_entropy_fwd_hip).
  * Writes per-row loss and logsumexp; row_max / row_sum when non-NULL
  * (tiny mode); grad_logits (same dtype as logits) when non-NULL (fused mode),
- * pre-multiplied by scale_grad. softcap <= 0 disables the logit softcap,
- * label_smoothing <= 0 disables smoothing. Rows whose target equals
+ * pre-multiplied by scale_grad and, when scale_dev is non-NULL, by the
+ * device value scale_dev[0] (e.g. 1 / #counted rows from ak_ce_count_valid,
+ * so the mean's scale needs no host read); z_loss_weight w >= 0 adds the
+ * gradient of w * lse^2 to it (as in ak_ce_bwd_tiny). softcap <= 0 disables the logit
+ * softcap, label_smoothing <= 0 disables smoothing. Rows whose target equals
  * ignore_index get loss 0 and a zero gradient row; a target outside
- * [0, vocab) that is not ignore_index yields loss NaN.
+ * [0, vocab) that is not ignore_index yields loss NaN. Rows are walked by
+ * grid stride: any row count whose extent fits 64-bit addressing.
  */
 int ak_ce_fwd(const void* logits, const int64_t* targets,
               float* losses, float* lse, float* row_max, float* row_sum,
               void* grad_logits,
               int64_t rows, int64_t vocab, int64_t ld_logits, int64_t ld_grad,
               float softcap, int64_t ignore_index, float label_smoothing,
-              float scale_grad, int dtype, void* stream);
+              float scale_grad, float z_loss_weight, const float* scale_dev,
+              int dtype, void* stream);
 
 /*
- * Cross-entropy backward from saved row max / row sum (tiny mode).
+ * Cross-entropy backward from saved row max / row sum (tiny mode):
+ *   grad[r, i] = (p_ri (1 + 2 w lse_r) - [i == t_r](1 - a) - a / vocab)
+ *                * (softcap > 0 ? 1 - tanh^2(logit / softcap) : 1) * scale
+ * with p and lse over the (capped) logits, w = z_loss_weight (the gradient
+ * of w * lse^2, the z-loss the reference added in PyTorch,
+ * kernels/ce_fused.py:668-684, here taken through the softcap as well) and
+ * scale = scale_grad * (scale_dev ? scale_dev[0] : 1). Ignored rows get a
+ * zero row, out-of-range targets a NaN row.
  * Replaces kernels/ce_fused.py:490-522 (cross_entropy_bwd_tiny_hip).
  */
 int ak_ce_bwd_tiny(const void* logits, const int64_t* targets,
                    const float* row_max, const float* row_sum, void* grad_logits,
                    int64_t rows, int64_t vocab, int64_t ld_logits, int64_t ld_grad,
                    float softcap, int64_t ignore_index, float label_smoothing,
-                   float scale_grad, int dtype, void* stream);
+                   float scale_grad, float z_loss_weight, const float* scale_dev,
+                   int dtype, void* stream);
+
+/*
+ * denom[0] = max(1, #rows with targets[r] != ignore_index), denom[1] =
+ * 1 / denom[0], fp32 on the device. One workgroup, integer count.
+ * Replaces the host-side valid_mask.sum().clamp(min=1) and .item() of
+ * kernels/ce_fused.py:590-605.
+ */
+int ak_ce_count_valid(const int64_t* targets, int64_t rows, int64_t ignore_index,
+                      float* denom, void* stream);
+
+/*
+ * loss[0] = (sum over counted rows of losses[r] + z_loss_weight * lse[r]^2)
+ *           / max(1, #counted rows)
+ * n_valid[0] (nullable, int64) = #counted rows. Summed in a fixed order in
+ * one workgroup (deterministic). lse may be NULL when z_loss_weight is 0.
+ * Replaces the masked mean and z-loss of kernels/ce_fused.py:611-626.
+ */
+int ak_ce_mean(const float* losses, const float* lse, const int64_t* targets,
+               int64_t rows, int64_t ignore_index, float z_loss_weight,
+               float* loss, int64_t* n_valid, void* stream);
 
 /*
  * Fused lm-head + cross-entropy forward: logits = hidden @ weight^T are

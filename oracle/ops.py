@@ -137,15 +137,19 @@ def ce_rows_ref(logits: torch.Tensor, targets: torch.Tensor, softcap: float = 0.
 
 def ce_grad_ref(logits: torch.Tensor, targets: torch.Tensor, softcap: float = 0.0,
                 ignore_index: int = -100, label_smoothing: float = 0.0,
-                scale: float = 1.0) -> torch.Tensor:
+                scale: float = 1.0, z_loss_weight: float = 0.0) -> torch.Tensor:
     """Gradient rows of ``kernels/ce_fused.py:268-328`` (fp32).
 
-    g = softmax(x) - [i == t](1 - a) - a / V, times (1 - tanh^2) under the
-    softcap, times ``scale``; ignored rows are zero.
+    g = softmax(x) - [i == t](1 - a) - a / V, plus 2 w lse softmax(x) for a
+    z-loss weight w (the gradient of w * lse^2, ``ce_fused.py:668-684``),
+    times (1 - tanh^2) under the softcap, times ``scale``; ignored rows are
+    zero.
     """
     x = _capped(logits, softcap)
     V = x.shape[-1]
     p = torch.softmax(x, dim=-1)
+    if z_loss_weight > 0:
+        p = p * (1 + 2 * z_loss_weight * torch.logsumexp(x, dim=-1, keepdim=True))
     t = targets.long()
     ignored = t == ignore_index
     tc = torch.where(ignored, torch.zeros_like(t), t)
@@ -160,10 +164,16 @@ def ce_grad_ref(logits: torch.Tensor, targets: torch.Tensor, softcap: float = 0.
     return torch.where(ignored[:, None], torch.zeros_like(g), g)
 
 
-def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int = -100) -> torch.Tensor:
-    """Mean over non-ignored rows, denominator clamped to 1 (``ce_fused.py:594-622``)."""
+def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int = -100,
+                lse: torch.Tensor = None, z_loss_weight: float = 0.0) -> torch.Tensor:
+    """Mean over non-ignored rows, denominator clamped to 1 (``ce_fused.py:594-622``),
+    plus ``z_loss_weight * sum(lse^2)`` over the same rows and denominator
+    (``:611-626``)."""
     valid = (targets != ignore_index).float()
-    return (losses * valid).sum() / valid.sum().clamp(min=1.0)
+    total = (losses * valid).sum()
+    if z_loss_weight > 0:
+        total = total + z_loss_weight * (lse.float() ** 2 * valid).sum()
+    return total / valid.sum().clamp(min=1.0)
 
 
 def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,

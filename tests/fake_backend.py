@@ -50,7 +50,8 @@ def _bad_targets(targets, vocab, ignore_index):
     return (t != ignore_index) & ((t < 0) | (t >= vocab))
 
 
-def _ce_fwd(logits, targets, losses, lse, row_max, row_sum, grad, softcap, ignore_index, ls, scale):
+def _ce_fwd(logits, targets, losses, lse, row_max, row_sum, grad, softcap, ignore_index, ls, scale,
+            scale_dev=None, z_loss_weight=0.0):
     bad = _bad_targets(targets, logits.shape[1], ignore_index)
     t = torch.where(bad, torch.full_like(targets, ignore_index), targets)
     l, s, m, sm = ops.ce_rows_ref(logits, t, softcap, ignore_index, ls)
@@ -62,17 +63,23 @@ def _ce_fwd(logits, targets, losses, lse, row_max, row_sum, grad, softcap, ignor
     if row_sum is not None:
         row_sum.copy_(sm)
     if grad is not None:
-        g = ops.ce_grad_ref(logits, t, softcap, ignore_index, ls, scale)
+        sc = scale * (float(scale_dev.reshape(-1)[0]) if scale_dev is not None else 1.0)
+        g = ops.ce_grad_ref(logits, t, softcap, ignore_index, ls, sc, z_loss_weight)
         g[bad] = math.nan
         grad.copy_(g)
 
 
-def _ce_bwd_tiny(logits, targets, row_max, row_sum, grad, softcap, ignore_index, ls, scale):
+def _ce_bwd_tiny(logits, targets, row_max, row_sum, grad, softcap, ignore_index, ls, scale,
+                 z_loss_weight=0.0, scale_dev=None):
+    sc = scale * (float(scale_dev.reshape(-1)[0]) if scale_dev is not None else 1.0)
     x = logits.float()
     if softcap > 0:
         x = softcap * torch.tanh(x / softcap)
     V = x.shape[1]
     p = torch.exp(x - row_max.float()[:, None]) / row_sum.float()[:, None]
+    if z_loss_weight > 0:
+        lse = row_max.float() + torch.log(row_sum.float())
+        p = p * (1 + 2 * z_loss_weight * lse[:, None])
     t = targets.long()
     ignored = t == ignore_index
     tc = torch.where(ignored, torch.zeros_like(t), t)
@@ -82,8 +89,19 @@ def _ce_bwd_tiny(logits, targets, row_max, row_sum, grad, softcap, ignore_index,
     if softcap > 0:
         th = x / softcap
         g = g * (1 - th * th)
-    g = torch.where(ignored[:, None], torch.zeros_like(g), g * scale)
+    g = torch.where(ignored[:, None], torch.zeros_like(g), g * sc)
     grad.copy_(g)
+
+
+def _ce_count_valid(targets, ignore_index):
+    n = max(1, int((targets != ignore_index).sum()))
+    return torch.tensor([float(n), 1.0 / n], dtype=torch.float32)
+
+
+def _ce_mean(losses, lse, targets, ignore_index, z_loss_weight=0.0, n_valid=None):
+    if n_valid is not None:
+        n_valid.copy_((targets != ignore_index).sum().reshape(1))
+    return ops.ce_mean_ref(losses, targets, ignore_index, lse, z_loss_weight)
 
 
 def _lmhead(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap=0.0,
@@ -164,6 +182,8 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "softmax", _softmax)
     monkeypatch.setattr(_lib, "ce_fwd", _ce_fwd)
     monkeypatch.setattr(_lib, "ce_bwd_tiny", _ce_bwd_tiny)
+    monkeypatch.setattr(_lib, "ce_count_valid", _ce_count_valid)
+    monkeypatch.setattr(_lib, "ce_mean", _ce_mean)
     monkeypatch.setattr(_lib, "lmhead_ce", _lmhead)
     monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
     monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)

@@ -97,7 +97,8 @@ def test_ce_fused_module_api(fake_backend):
 
 
 @pytest.mark.parametrize("mode", ["fused", "tiny"])
-@pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (8.0, 0.1, 0.0), (0.0, 0.0, 1e-2)])
+@pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (8.0, 0.1, 0.0), (0.0, 0.0, 1e-2),
+                                           (8.0, 0.1, 1e-2)])
 def test_ce_full_autograd(fake_backend, mode, softcap, ls, zw):
     from kernels.ce_fused import ce_full
     g = torch.Generator().manual_seed(1)
@@ -412,3 +413,51 @@ def test_selective_scan_fn_keeps_states_only_when_recording(fake_backend, monkey
     monkeypatch.setattr(ss, "SAVE_STATES", False)
     ss.selective_scan_fn(u, delta, A, B, C, z=z).sum().backward()
     assert seen == [False, True, False]
+
+
+def test_rows_view_rejects_overlapping_rows_and_as_rows_copies():
+    from kernels.hip import _lib
+    e = torch.randn(768).expand(4, 768)
+    # the pitch is passed on unchanged (0), so the C-ABI's pitch check rejects it
+    assert _lib._rows_view(e, "x") == 0
+    assert _lib._rows_view(torch.randn(1, 768).expand(1, 768), "x") == 768
+    c = _lib.as_rows(e, 768)
+    assert c.stride() == (768, 1) and torch.equal(c, e)
+    big = torch.randn(6, 800)
+    v = _lib.as_rows(big[:, :768], 768)        # pitch 800 >= cols: no copy
+    assert v.data_ptr() == big.data_ptr() and v.stride() == (800, 1)
+    t = _lib.as_rows(torch.randn(768, 6).t(), 768)
+    assert t.is_contiguous()
+
+
+def test_rmsnorm_replacement_takes_the_modules_own_eps(fake_backend):
+    """HF-style norms keep eps in ``variance_epsilon``; the swap must use it
+    (and GemmaRMSNorm's 1 + weight scaling)."""
+    import torch.nn as nn
+    from autokernel._patterns import _RMSNormReplacement, _norm_eps
+    from kernels.hip.rmsnorm import kernel_fn
+
+    class LlamaRMSNorm(nn.Module):
+        def __init__(self, d, eps):
+            super().__init__()
+            self.weight = nn.Parameter(1 + 0.1 * torch.randn(d))
+            self.variance_epsilon = eps
+
+        def forward(self, x):
+            v = x.float().pow(2).mean(-1, keepdim=True)
+            return self.weight * (x.float() * torch.rsqrt(v + self.variance_epsilon))
+
+    class GemmaRMSNorm(LlamaRMSNorm):
+        def forward(self, x):
+            v = x.float().pow(2).mean(-1, keepdim=True)
+            return (1 + self.weight) * (x.float() * torch.rsqrt(v + self.variance_epsilon))
+
+    x = 0.01 * torch.randn(3, 5, 32)   # small rows: eps matters
+    for cls in (LlamaRMSNorm, GemmaRMSNorm):
+        m = cls(32, 1e-2)
+        rep = _RMSNormReplacement(m, kernel_fn)
+        assert rep.eps == 1e-2
+        assert torch.allclose(rep(x), m(x), rtol=1e-5, atol=1e-6)
+    assert _norm_eps(nn.Module()) == 1e-6
+    assert _norm_eps(nn.RMSNorm(8, eps=3e-5)) == 3e-5
+    assert _norm_eps(nn.RMSNorm(8)) == torch.finfo(torch.float32).eps

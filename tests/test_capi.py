@@ -38,7 +38,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_version_and_arch(lib):
-    assert lib.ak_abi_version() == 1
+    assert lib.ak_abi_version() == 2
     assert lib.ak_target_arch() == b"gfx950"
 
 
@@ -111,3 +111,38 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.HipExtensionMissing):
         _lib.load()
+
+
+def test_row_extent_checks(lib):
+    # The row kernels walk rows by grid stride on a capped grid, so the row
+    # count is limited only by 64-bit addressing of the last row.
+    huge = 1 << 61
+    rc = lib.ak_rmsnorm_fwd(None, None, None, huge, 8, 8, 8, 1e-6, 0, None)
+    assert rc == -1 and b"64-bit" in lib.ak_last_error()
+    rc = lib.ak_fused_add_rmsnorm_fwd(None, None, None, None, None, 1 << 40, 8, 1 << 30, 8, 8, 8,
+                                      1e-6, 1, None)
+    assert rc == -1 and b"64-bit" in lib.ak_last_error()
+    rc = lib.ak_softmax_fwd(None, None, huge, 8, 8, 8, 1, None)
+    assert rc == -1 and b"64-bit" in lib.ak_last_error()
+    rc = lib.ak_ce_fwd(None, None, None, None, None, None, None, huge, 8, 8, 8, 0.0, -100, 0.0,
+                       1.0, 0.0, None, 2, None)
+    assert rc == -1 and b"64-bit" in lib.ak_last_error()
+    # 2^32 rows (past the old grid-size limit) pass the shape checks and stop
+    # at the null-pointer check, before any HIP call
+    for rows in (1 << 32, (1 << 32) + 5):
+        rc = lib.ak_rmsnorm_fwd(None, None, None, rows, 8, 8, 8, 1e-6, 0, None)
+        assert rc == -1 and b"null" in lib.ak_last_error()
+        rc = lib.ak_softmax_fwd(None, None, rows, 8, 8, 8, 2, None)
+        assert rc == -1 and b"null" in lib.ak_last_error()
+
+
+def test_ce_reduction_argument_errors(lib):
+    rc = lib.ak_ce_count_valid(None, 4, -100, None, None)
+    assert rc == -1 and b"null" in lib.ak_last_error()
+    rc = lib.ak_ce_mean(None, None, None, -1, -100, 0.0, None, None, None)
+    assert rc == -1 and b"rows" in lib.ak_last_error()
+    rc = lib.ak_ce_mean(None, None, None, 4, -100, -1.0, None, None, None)
+    assert rc == -1 and b"z_loss" in lib.ak_last_error()
+    rc = lib.ak_ce_bwd_tiny(None, None, None, None, None, 0, 8, 8, 8, 0.0, -100, 0.0, 1.0, -0.5,
+                            None, 2, None)
+    assert rc == -1 and b"z_loss" in lib.ak_last_error()

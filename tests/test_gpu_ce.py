@@ -106,3 +106,63 @@ def test_ce_out_of_range_target_is_nan_not_oob():
     lc = losses.cpu()
     assert math.isfinite(float(lc[0])) and math.isnan(float(lc[1])) and math.isnan(float(lc[2]))
     assert float(lc[3]) == 0.0 and bool((grad[3] == 0).all())
+
+
+@pytest.mark.parametrize("mode", ["fused", "tiny"])
+@pytest.mark.parametrize("softcap,ls", [(0.0, 0.0), (12.0, 0.1)])
+def test_ce_zloss_in_kernel_vs_float64_autograd(mode, softcap, ls):
+    """The z-loss gradient 2 w lse p comes from the CE kernels themselves, in
+    either mode and through the softcap; the loss and lse from ak_ce_mean.
+    Bars: loss 1e-3 relative (the CE bar), gradient within 1 bf16 ulp of its
+    magnitude plus 1e-6."""
+    need_gpu()
+    from kernels.ce_fused import ce_full
+    g = torch.Generator().manual_seed(21)
+    base = (4 * torch.randn(96, 5003, generator=g)).bfloat16()
+    t = torch.randint(0, 5003, (96,), generator=g)
+    t[torch.randperm(96, generator=g)[:9]] = -100
+    w = 2e-3
+    say("ce z-loss", mode, softcap, ls)
+    x = base.to(DEV).requires_grad_()
+    loss, lse = ce_full(x, t.to(DEV), softcap=softcap, label_smoothing=ls, mode=mode,
+                        return_z=True, z_loss_weight=w)
+    (3.0 * loss).backward()
+    xr = base.double().requires_grad_()
+    xc = softcap * torch.tanh(xr / softcap) if softcap > 0 else xr
+    valid = (t != -100).double()
+    ref = F.cross_entropy(xc, t, label_smoothing=ls) + w * (
+        (torch.logsumexp(xc, -1) ** 2) * valid).sum() / valid.sum()
+    (3.0 * ref).backward()
+    assert abs(float(loss) - float(ref)) <= 1e-3 * abs(float(ref))
+    assert _close(lse, torch.logsumexp(xc.detach(), -1), rtol=1e-5)
+    ok, worst = _grad_ok(x.grad, xr.grad, torch.bfloat16)
+    assert ok, worst
+    assert bool((x.grad[t.to(DEV) == -100] == 0).all())
+
+
+def test_ce_count_and_mean_many_rows():
+    """ak_ce_count_valid / ak_ce_mean over 300k rows against the oracle; the
+    count is exact, the mean within 1e-5 relative (fp32 sums), deterministic."""
+    need_gpu()
+    from kernels.hip import _lib
+    g = torch.Generator().manual_seed(22)
+    n = 300_001
+    losses = torch.rand(n, generator=g) * 5
+    lse = torch.randn(n, generator=g) * 3
+    t = torch.randint(0, 1000, (n,), generator=g)
+    t[torch.randperm(n, generator=g)[:12345]] = -7
+    say("ce count/mean", n)
+    tg = t.to(DEV)
+    denom = _lib.ce_count_valid(tg, -7).cpu()
+    nv = n - 12345
+    assert float(denom[0]) == float(nv) and float(denom[1]) == float(torch.tensor(1.0 / nv))
+    cnt = torch.empty(1, dtype=torch.int64, device=DEV)
+    m1 = _lib.ce_mean(losses.to(DEV), lse.to(DEV), tg, -7, 0.01, n_valid=cnt)
+    m2 = _lib.ce_mean(losses.to(DEV), lse.to(DEV), tg, -7, 0.01)
+    ref = ops.ce_mean_ref(losses.double(), t, -7, lse.double(), 0.01)
+    assert int(cnt) == nv
+    assert abs(float(m1) - float(ref)) <= 1e-5 * abs(float(ref))
+    assert torch.equal(m1, m2)
+    all_ignored = torch.full((10,), -7, device=DEV)
+    assert float(_lib.ce_count_valid(all_ignored, -7)[0]) == 1.0
+    assert float(_lib.ce_mean(torch.ones(10, device=DEV), None, all_ignored, -7)) == 0.0

@@ -107,3 +107,33 @@ def test_rownorm_deterministic():
     say("rownorm determinism")
     outs = [frn.kernel_fn_dual(x, r, w, eps=1e-5)[1] for _ in range(3)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_rownorm_expanded_views_and_grid_stride():
+    """Overlapping rows (an expand-ed residual, stride(0) == 0) are copied by
+    the wrapper, not read past the buffer; row counts past the 2^20-workgroup
+    grid cap are covered by the grid-stride loops (vector and generic paths)."""
+    need_gpu()
+    from kernels.hip import fused_residual_add_rmsnorm as frn
+    from kernels.hip import rmsnorm
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(4, 6, 768, generator=g).bfloat16()
+    r1 = torch.randn(768, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(768, generator=g)).bfloat16()
+    r = r1.expand(4, 6, 768)
+    say("rownorm expanded residual")
+    h, y = frn.kernel_fn_dual(x.to(DEV), r1.to(DEV).expand(4, 6, 768), w.to(DEV), eps=1e-5)
+    hr, yr = ops.fused_residual_add_rmsnorm_ref(x.reshape(-1, 768), r.reshape(-1, 768), w, 1e-5)
+    assert torch.equal(h.cpu().reshape(-1, 768), hr)
+    assert max_ulp(y.cpu().reshape(-1, 768), yr) <= 1
+    xe = torch.randn(256, generator=g).expand(5, 256)
+    ye = rmsnorm.kernel_fn(xe.to(DEV), torch.ones(256, device=DEV)).cpu()
+    assert torch.equal(ye, ops.rmsnorm_f32_ref(xe.contiguous(), torch.ones(256)))
+    # 4.3M rows of 16 fp32 (the 64-thread vector kernel, 4 rows per workgroup:
+    # > 2^20 workgroups) and 1.1M rows of 7 fp32 (the generic kernel)
+    for rows, cols in ((4_300_000, 16), (1_100_000, 7)):
+        say("rownorm grid stride", rows, cols)
+        xs = torch.randn(rows, cols, generator=g)
+        ws = 1 + 0.1 * torch.randn(cols, generator=g)
+        ys = rmsnorm.kernel_fn(xs.to(DEV), ws.to(DEV)).cpu()
+        assert _rel_ok_f32(ys, ops.rmsnorm_f32_ref(xs, ws))

@@ -164,7 +164,7 @@ def test_custom_op_autograd_uses_kernels(dtype):
     (the gfx950 backward kernels) against float64 autograd of the oracle."""
     need_gpu()
     import kernels.hip._torch_ops as T
-    assert T._use_hip_backward()
+    assert T._bwd_kernels_for(torch.empty(1, device=DEV))
     g = torch.Generator().manual_seed(4)
     x = torch.randn(64, 768, generator=g).to(dtype)
     r = torch.randn(64, 768, generator=g).to(dtype)
@@ -187,3 +187,21 @@ def test_custom_op_autograd_uses_kernels(dtype):
     assert torch.equal(xd.grad, rd_.grad)
     assert torch.allclose(xd.grad.double().cpu(), x64.grad, rtol=tol, atol=tol)
     assert torch.allclose(wd.grad.double().cpu(), w64.grad, rtol=tol, atol=tol * 64)
+
+
+def test_backward_of_broadcast_upstream_gradient():
+    """The gradient of y.sum(0) reaches the backward as an expand-ed tensor
+    (stride(0) == 0); the wrapper copies it instead of reading past it."""
+    need_gpu()
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(32, 512, generator=g)
+    w = 1 + 0.1 * torch.randn(512, generator=g)
+    up = torch.randn(512, generator=g)
+    say("rmsnorm bwd expanded grad")
+    xd, wd = x.to(DEV).requires_grad_(), w.to(DEV).requires_grad_()
+    y = torch.ops.autokernel.rmsnorm(xd, wd, 1e-6)
+    y.sum(0).backward(up.to(DEV))
+    x64, w64 = x.double().requires_grad_(), w.double().requires_grad_()
+    ops.rmsnorm_ref(x64, w64, 1e-6).sum(0).backward(up.double())
+    assert torch.allclose(xd.grad.double().cpu(), x64.grad, rtol=1e-4, atol=1e-5)
+    assert torch.allclose(wd.grad.double().cpu(), w64.grad, rtol=1e-4, atol=1e-4)

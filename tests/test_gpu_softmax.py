@@ -92,3 +92,21 @@ def test_softmax_rank_and_determinism():
     xt = torch.randn(64, 128, generator=g).to(DEV).t()                   # non-contiguous last dim
     yt = softmax.kernel_fn(xt).cpu()
     assert torch.allclose(yt, ops.softmax_ref(xt.cpu()), atol=1e-6)
+
+
+def test_softmax_grid_stride_and_expanded_rows():
+    """Row counts past the 2^20-workgroup grid cap (vector and generic
+    kernels) and an expand-ed input (stride(0) == 0)."""
+    need_gpu()
+    from kernels.hip import softmax
+    g = torch.Generator().manual_seed(13)
+    for rows, cols in ((4_300_000, 16), (1_100_000, 7)):
+        say("softmax grid stride", rows, cols)
+        x = 3 * torch.randn(rows, cols, generator=g)
+        y = softmax.kernel_fn(x.to(DEV)).cpu()
+        ref = ops.softmax_ref(x)
+        assert bool(((y - ref).abs() <= 1e-5 * ref.abs() + 1e-7).all())
+    xe = torch.randn(1024, generator=g).half().expand(3, 1024)
+    say("softmax expanded")
+    ye = softmax.kernel_fn(xe.to(DEV)).cpu()
+    assert max_ulp(ye, ops.softmax_ref(xe.contiguous())) <= 1

@@ -215,6 +215,31 @@ def test_ce_grad_matches_autograd(softcap, ls):
     assert torch.allclose(ops.ce_mean_ref(losses, t).double(), loss.detach(), rtol=1e-5)
 
 
+@pytest.mark.parametrize("softcap,ls", [(0.0, 0.0), (6.0, 0.0), (6.0, 0.15)])
+def test_ce_zloss_grad_and_mean_match_autograd(softcap, ls):
+    # loss = mean over counted rows of (CE + w * lse^2): float64 autograd pins
+    # both the z-loss term of ce_mean_ref and the 2 w lse p term of ce_grad_ref,
+    # including the softcap's chain rule
+    w = 0.03
+    g = torch.Generator().manual_seed(17)
+    logits = (4 * torch.randn(9, 21, generator=g)).double().requires_grad_()
+    t = torch.randint(0, 21, (9,), generator=g)
+    t[[2, 6]] = -100
+    x = softcap * torch.tanh(logits / softcap) if softcap > 0 else logits
+    valid = (t != -100).double()
+    ce = F.cross_entropy(x, t, ignore_index=-100, label_smoothing=ls)
+    loss = ce + w * (torch.logsumexp(x, -1) ** 2 * valid).sum() / valid.sum()
+    loss.backward()
+    grad = ops.ce_grad_ref(logits.detach().float(), t, softcap, -100, ls, 1.0 / 7, w)
+    assert torch.allclose(grad.double(), logits.grad, atol=3e-6, rtol=1e-4)
+    losses, lse, _, _ = ops.ce_rows_ref(logits.detach().float(), t, softcap, -100, ls)
+    mean = ops.ce_mean_ref(losses, t, -100, lse, w)
+    assert torch.allclose(mean.double(), loss.detach(), rtol=1e-5)
+    # the z-loss term really enters: without it the gradient differs
+    plain = ops.ce_grad_ref(logits.detach().float(), t, softcap, -100, ls, 1.0 / 7)
+    assert not torch.allclose(plain.double(), logits.grad, atol=1e-4)
+
+
 def test_ce_closed_forms():
     V = 50
     losses, lse, _, _ = ops.ce_rows_ref(torch.zeros(4, V), torch.tensor([0, 3, 49, 7]))
