@@ -23,6 +23,8 @@
 // slot) into the caller's workspace and a second kernel sums the partial
 // rows per column in a fixed order: dw is deterministic (the reference
 // accumulated it with fp32 atomics).
+#include <atomic>
+
 #include "ak_common.h"
 
 namespace ak {
@@ -249,67 +251,132 @@ size_t bwd_ws_bytes(int64_t rows, int64_t cols) {
   return align256((size_t)parts * (size_t)cols * sizeof(float));
 }
 
-template <typename T, bool ADD_DH, int VPT, int TPR>
-int launch_bwd_vec(const T* x, const T* w, const T* dy, const T* dh, T* dx, float* part,
-                   int64_t rows, int cols, int64_t ld_x, int64_t ld_dy, int64_t ld_dh,
-                   int64_t ld_dx, float eps, hipStream_t s) {
-  constexpr int RPW = TPR >= 256 ? 1 : 256 / TPR;
-  const int64_t blocks = (rows + RPW - 1) / RPW;
-  const int grid = (int)(blocks < kBwdMaxGrid ? blocks : kBwdMaxGrid);
-  rownorm_bwd_vec_kernel<T, ADD_DH, VPT, TPR><<<dim3(grid), dim3(TPR * RPW), 0, s>>>(
-      x, w, dy, dh, dx, part, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, eps);
-  return grid * RPW;
+// Launch plan of the backward's row pass: the kernel (the generic one, or a
+// vector kernel with VPT vectors per thread and TPR threads per row), its
+// grid, and the number of partial weight-gradient rows it writes (one per
+// workgroup row slot), which colsum_kernel then sums.
+struct BwdPlan {
+  bool generic;
+  int vpt, tpr, grid, nparts;
+};
+
+template <typename T>
+BwdPlan plan_bwd(const void* x, const void* w, const void* dy, const void* dh, const void* dx,
+                 int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_dy, int64_t ld_dh,
+                 int64_t ld_dx) {
+  constexpr int VE = Vec16<T>::VE;
+  bool vec_ok = cols % VE == 0 && ld_x % VE == 0 && ld_dy % VE == 0 && ld_dx % VE == 0 &&
+                aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+  if (dh) vec_ok = vec_ok && ld_dh % VE == 0 && aligned16(dh);
+  const int64_t nvec = cols / VE;
+  BwdPlan p{};
+  if (!vec_ok || nvec > 8192) {
+    p.generic = true;
+    p.grid = (int)(rows < kBwdMaxGrid ? rows : kBwdMaxGrid);
+    p.nparts = p.grid;
+    return p;
+  }
+  p.vpt = nvec <= 1024 ? 1 : nvec <= 2048 ? 2 : nvec <= 4096 ? 4 : 8;
+  p.tpr = nvec <= 64 ? 64 : nvec <= 128 ? 128 : nvec <= 256 ? 256 : nvec <= 512 ? 512 : 1024;
+  const int rpw = p.tpr >= 256 ? 1 : 256 / p.tpr;
+  const int64_t blocks = (rows + rpw - 1) / rpw;
+  p.grid = (int)(blocks < kBwdMaxGrid ? blocks : kBwdMaxGrid);
+  p.nparts = p.grid * rpw;
+  return p;
+}
+
+// Bytes of partial weight-gradient rows a plan writes.
+size_t plan_ws_bytes(const BwdPlan& p, int64_t cols) {
+  return align256((size_t)p.nparts * (size_t)cols * sizeof(float));
 }
 
 template <typename T, bool ADD_DH>
-int dispatch_bwd(const void* xv, const void* wv, const void* dyv, const void* dhv, void* dxv,
-                 float* dw, void* ws, int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_dy,
-                 int64_t ld_dh, int64_t ld_dx, float eps, hipStream_t s) {
+void run_bwd(const BwdPlan& plan, const void* xv, const void* wv, const void* dyv,
+             const void* dhv, void* dxv, float* dw, float* part, int64_t rows, int64_t cols,
+             int64_t ld_x, int64_t ld_dy, int64_t ld_dh, int64_t ld_dx, float eps,
+             hipStream_t s) {
   const T* x = static_cast<const T*>(xv);
   const T* w = static_cast<const T*>(wv);
   const T* dy = static_cast<const T*>(dyv);
   const T* dh = static_cast<const T*>(dhv);
   T* dx = static_cast<T*>(dxv);
-  float* part = dw ? static_cast<float*>(ws) : nullptr;
-  constexpr int VE = Vec16<T>::VE;
-  bool vec_ok = cols % VE == 0 && ld_x % VE == 0 && ld_dy % VE == 0 && ld_dx % VE == 0 &&
-                aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
-  if (ADD_DH) vec_ok = vec_ok && ld_dh % VE == 0 && aligned16(dh);
-  const int64_t nvec = cols / VE;
+  if (!dw) part = nullptr;
   const int c = (int)cols;
-  int nparts = 0;
-#define AK_LAUNCH(VPT, TPR) \
-  nparts = launch_bwd_vec<T, ADD_DH, VPT, TPR>(x, w, dy, dh, dx, part, rows, c, ld_x, ld_dy, ld_dh, ld_dx, eps, s)
-  if (!vec_ok || nvec > 8192) {
-    const int grid = (int)(rows < kBwdMaxGrid ? rows : kBwdMaxGrid);
-    rownorm_bwd_generic_kernel<T, ADD_DH><<<dim3(grid), dim3(256), 0, s>>>(
+  const dim3 grid(plan.grid);
+#define AK_VEC(VPT, TPR)                                                                       \
+  rownorm_bwd_vec_kernel<T, ADD_DH, VPT, TPR><<<grid, dim3(TPR >= 256 ? TPR : 256), 0, s>>>( \
+      x, w, dy, dh, dx, part, rows, c, ld_x, ld_dy, ld_dh, ld_dx, eps)
+  if (plan.generic) {
+    rownorm_bwd_generic_kernel<T, ADD_DH><<<grid, dim3(256), 0, s>>>(
         x, w, dy, dh, dx, part, rows, c, ld_x, ld_dy, ld_dh, ld_dx, eps);
-    nparts = grid;
-  } else if (nvec <= 64) AK_LAUNCH(1, 64);
-  else if (nvec <= 128) AK_LAUNCH(1, 128);
-  else if (nvec <= 256) AK_LAUNCH(1, 256);
-  else if (nvec <= 512) AK_LAUNCH(1, 512);
-  else if (nvec <= 1024) AK_LAUNCH(1, 1024);
-  else if (nvec <= 2048) AK_LAUNCH(2, 1024);
-  else if (nvec <= 4096) AK_LAUNCH(4, 1024);
-  else AK_LAUNCH(8, 1024);
-#undef AK_LAUNCH
-  if (dw) colsum_kernel<<<dim3((c + 63) / 64), dim3(64 * kColWaves), 0, s>>>(part, dw, nparts, c);
+  } else if (plan.tpr == 64) AK_VEC(1, 64);
+  else if (plan.tpr == 128) AK_VEC(1, 128);
+  else if (plan.tpr == 256) AK_VEC(1, 256);
+  else if (plan.tpr == 512) AK_VEC(1, 512);
+  else if (plan.vpt == 1) AK_VEC(1, 1024);
+  else if (plan.vpt == 2) AK_VEC(2, 1024);
+  else if (plan.vpt == 4) AK_VEC(4, 1024);
+  else AK_VEC(8, 1024);
+#undef AK_VEC
+  if (dw) colsum_kernel<<<dim3((c + 63) / 64), dim3(64 * kColWaves), 0, s>>>(part, dw, plan.nparts, c);
+}
+
+BwdPlan plan_for(const void* x, const void* w, const void* dy, const void* dh, const void* dx,
+                 int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_dy, int64_t ld_dh,
+                 int64_t ld_dx, int dtype) {
+  switch (dtype) {
+    case AK_DTYPE_F32: return plan_bwd<float>(x, w, dy, dh, dx, rows, cols, ld_x, ld_dy, ld_dh, ld_dx);
+    case AK_DTYPE_F16: return plan_bwd<f16>(x, w, dy, dh, dx, rows, cols, ld_x, ld_dy, ld_dh, ld_dx);
+    default: return plan_bwd<bf16>(x, w, dy, dh, dx, rows, cols, ld_x, ld_dy, ld_dh, ld_dx);
+  }
+}
+
+// Argument checks shared by the entry points (no HIP call).
+int check_bwd_args(const char* name, int64_t rows, int64_t cols, int64_t ld_x, int64_t ld_dy,
+                   int64_t ld_dh, int64_t ld_dx, bool has_dh, int dtype) {
+  if (ak_dtype_size(dtype) == 0)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", name, dtype);
+  if (rows < 0 || cols <= 0 || cols > (int64_t)1 << 30)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape rows=%lld cols=%lld", name,
+                        (long long)rows, (long long)cols);
+  if (ld_x < cols || ld_dy < cols || ld_dx < cols || (has_dh && ld_dh < cols))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  const int esz = ak_dtype_size(dtype);
+  if (!ak_extent_ok(rows, ld_x, cols, esz) || !ak_extent_ok(rows, ld_dy, cols, esz) ||
+      !ak_extent_ok(rows, ld_dx, cols, esz) || (has_dh && !ak_extent_ok(rows, ld_dh, cols, esz)))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld x pitch exceed 64-bit addressing", name,
+                        (long long)rows);
   return AK_OK;
+}
+
+// Enqueues the backward with the partial rows in `part` (checked by the caller).
+int enqueue_bwd(const char* name, const BwdPlan& plan, const void* x, const void* w,
+                const void* dy, const void* dh, void* dx, float* dw, float* part, int64_t rows,
+                int64_t cols, int64_t ld_x, int64_t ld_dy, int64_t ld_dh, int64_t ld_dx,
+                float eps, int dtype, hipStream_t s) {
+  if (rows == 0) {
+    // no rows: dw is all zeros (a fixed-order sum over no partial rows)
+    if (dw) colsum_kernel<<<dim3((unsigned)((cols + 63) / 64)), dim3(64 * kColWaves), 0, s>>>(nullptr, dw, 0, (int)cols);
+    return ak_check_launch(name);
+  }
+#define AK_BWD(TT)                                                                              \
+  (dh ? run_bwd<TT, true>(plan, x, w, dy, dh, dx, dw, part, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, eps, s) \
+      : run_bwd<TT, false>(plan, x, w, dy, dh, dx, dw, part, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, eps, s))
+  switch (dtype) {
+    case AK_DTYPE_F32: AK_BWD(float); break;
+    case AK_DTYPE_F16: AK_BWD(f16); break;
+    default: AK_BWD(bf16); break;
+  }
+#undef AK_BWD
+  return ak_check_launch(name);
 }
 
 int bwd_entry(const char* name, const void* x, const void* w, const void* dy, const void* dh,
               void* dx, float* dw, void* ws, size_t ws_bytes, int64_t rows, int64_t cols,
               int64_t ld_x, int64_t ld_dy, int64_t ld_dh, int64_t ld_dx, float eps, int dtype,
               void* stream) {
-  if (ak_dtype_size(dtype) == 0)
-    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype code %d", name, dtype);
-  if (rows < 0 || cols <= 0 || cols > (int64_t)1 << 30)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape rows=%lld cols=%lld", name,
-                        (long long)rows, (long long)cols);
-  if (rows > 0x7FFFFFFFll) return ak_set_error(AK_ERR_INVALID_ARG, "%s: rows=%lld exceeds 2^31-1", name, (long long)rows);
-  if (ld_x < cols || ld_dy < cols || ld_dx < cols || (dh && ld_dh < cols))
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: row pitch smaller than cols", name);
+  int rc = check_bwd_args(name, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, dh != nullptr, dtype);
+  if (rc) return rc;
   if (rows > 0 && (!x || !w || !dy || !dx))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   if (dw && rows > 0) {
@@ -319,22 +386,46 @@ int bwd_entry(const char* name, const void* x, const void* w, const void* dy, co
       return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
                           ws_bytes, bwd_ws_bytes(rows, cols));
   }
-  hipStream_t s = ak_stream(stream);
-  if (rows == 0) {
-    // no rows: dw is all zeros (a fixed-order sum over no partial rows)
-    if (dw) colsum_kernel<<<dim3((unsigned)((cols + 63) / 64)), dim3(64 * kColWaves), 0, s>>>(nullptr, dw, 0, (int)cols);
-    return ak_check_launch(name);
+  const BwdPlan plan = plan_for(x, w, dy, dh, dx, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, dtype);
+  return enqueue_bwd(name, plan, x, w, dy, dh, dx, dw, static_cast<float*>(ws), rows, cols, ld_x,
+                     ld_dy, ld_dh, ld_dx, eps, dtype, ak_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation entry point: the partial weight-gradient rows
+// live in this file-scope device array (one copy per GPU, held until the
+// process ends) instead of a caller workspace. In host code the array's name
+// is only a stand-in; its device address is queried once per device with
+// hipGetSymbolAddress (with that device current) and kept in
+// g_scratch_addr. Calls on one GPU share the array: concurrent calls on one
+// device race on it.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;  // 16 MiB
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+std::atomic<float*> g_scratch_addr[kMaxDevices];
+
+// Device address of `scratch` on the current device (queried on first use).
+int scratch_addr(const char* name, float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+    return ak_set_error(AK_ERR_LAUNCH, "%s: no current HIP device", name);
+  if (dev >= kMaxDevices)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: device %d >= %d", name, dev, kMaxDevices);
+  float* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !addr)
+      return ak_set_error(AK_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", name,
+                          hipGetErrorString(e));
+    p = static_cast<float*>(addr);
+    g_scratch_addr[dev].store(p, std::memory_order_release);
   }
-#define AK_BWD(TT)                                                                                \
-  (dh ? dispatch_bwd<TT, true>(x, w, dy, dh, dx, dw, ws, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, eps, s) \
-      : dispatch_bwd<TT, false>(x, w, dy, dh, dx, dw, ws, rows, cols, ld_x, ld_dy, ld_dh, ld_dx, eps, s))
-  switch (dtype) {
-    case AK_DTYPE_F32: AK_BWD(float); break;
-    case AK_DTYPE_F16: AK_BWD(f16); break;
-    default: AK_BWD(bf16); break;
-  }
-#undef AK_BWD
-  return ak_check_launch(name);
+  *out = p;
+  return AK_OK;
 }
 
 }  // namespace
@@ -362,4 +453,34 @@ extern "C" int ak_fused_add_rmsnorm_bwd(const void* hidden, const void* weight,
   return ak::bwd_entry("ak_fused_add_rmsnorm_bwd", hidden, weight, grad_normed, grad_hidden,
                        grad_x, grad_weight, workspace, workspace_bytes, rows, cols, ld_h, ld_gn,
                        ld_gh, ld_gx, eps, dtype, stream);
+}
+
+extern "C" int ak_fused_add_rmsnorm_bwd_noalloc(const void* hidden, const void* weight,
+                                                const void* grad_hidden, const void* grad_normed,
+                                                void* grad_x, float* grad_weight, int64_t rows,
+                                                int64_t cols, int64_t ld_h, int64_t ld_gh,
+                                                int64_t ld_gn, int64_t ld_gx, float eps,
+                                                int dtype, void* stream) {
+  const char* name = "ak_fused_add_rmsnorm_bwd_noalloc";
+  int rc = ak::check_bwd_args(name, rows, cols, ld_h, ld_gn, ld_gh, ld_gx, grad_hidden != nullptr,
+                              dtype);
+  if (rc) return rc;
+  const ak::BwdPlan plan = ak::plan_for(hidden, weight, grad_normed, grad_hidden, grad_x,
+                                              rows, cols, ld_h, ld_gn, ld_gh, ld_gx, dtype);
+  const size_t need = grad_weight && rows > 0 ? ak::plan_ws_bytes(plan, cols) : 0;
+  if (need > ak::kNoAllocScratchBytes)
+    return ak_set_error(AK_ERR_WORKSPACE,
+                        "%s: %zu bytes of scratch needed (%d partial rows x %lld cols x 4), "
+                        "the fixed scratch holds %zu; use ak_fused_add_rmsnorm_bwd with a workspace",
+                        name, need, plan.nparts, (long long)cols, ak::kNoAllocScratchBytes);
+  if (rows > 0 && (!hidden || !weight || !grad_normed || !grad_x))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  float* part = nullptr;
+  if (need > 0) {
+    rc = ak::scratch_addr(name, &part);
+    if (rc) return rc;
+  }
+  return ak::enqueue_bwd(name, plan, hidden, weight, grad_normed, grad_hidden, grad_x,
+                         grad_weight, part, rows, cols, ld_h, ld_gn, ld_gh, ld_gx, eps, dtype,
+                         ak_stream(stream));
 }

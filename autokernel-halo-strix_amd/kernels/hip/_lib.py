@@ -52,6 +52,7 @@ _SIGNATURES = {
     "ak_fused_add_rmsnorm_bwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                  _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64,
                                  _f32, _int, _c_void_p],
+    "ak_fused_add_rmsnorm_bwd_noalloc": [_c_void_p] * 6 + [_i64] * 6 + [_f32, _int, _c_void_p],
     "ak_softmax_fwd": [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p],
     "ak_ce_fwd": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                   _i64, _i64, _i64, _i64, _f32, _i64, _f32, _f32, _f32, _c_void_p, _int, _c_void_p],
@@ -265,6 +266,29 @@ def fused_add_rmsnorm_bwd(hidden: torch.Tensor, weight: torch.Tensor,
             _rows_view(hidden, "hidden"), ld_gh, _rows_view(grad_normed, "grad_normed"),
             _rows_view(grad_x, "grad_x"), float(eps), dtype_code(hidden.dtype), _stream(hidden))
     _check(rc, "ak_fused_add_rmsnorm_bwd")
+
+
+# Bytes of the fixed scratch behind ak_fused_add_rmsnorm_bwd_noalloc.
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def fused_add_rmsnorm_bwd_noalloc(hidden: torch.Tensor, weight: torch.Tensor,
+                                  grad_hidden: Optional[torch.Tensor], grad_normed: torch.Tensor,
+                                  grad_x: torch.Tensor, grad_weight: Optional[torch.Tensor],
+                                  eps: float) -> None:
+    """:func:`fused_add_rmsnorm_bwd` through the entry point that allocates
+    nothing (the library's fixed scratch holds the partial weight-gradient
+    rows); shapes beyond that scratch raise."""
+    require_device(hidden, weight, grad_hidden, grad_normed, grad_x, grad_weight)
+    rows, cols = hidden.shape
+    ld_gh = _rows_view(grad_hidden, "grad_hidden") if grad_hidden is not None else cols
+    with _on_device(hidden):
+        rc = load().ak_fused_add_rmsnorm_bwd_noalloc(
+            _ptr(hidden), _ptr(weight), _ptr(grad_hidden), _ptr(grad_normed), _ptr(grad_x),
+            _ptr(grad_weight), rows, cols, _rows_view(hidden, "hidden"), ld_gh,
+            _rows_view(grad_normed, "grad_normed"), _rows_view(grad_x, "grad_x"), float(eps),
+            dtype_code(hidden.dtype), _stream(hidden))
+    _check(rc, "ak_fused_add_rmsnorm_bwd_noalloc")
 
 
 def softmax(x: torch.Tensor, y: torch.Tensor) -> None:

@@ -110,6 +110,29 @@ int ak_fused_add_rmsnorm_bwd(const void* hidden, const void* weight,
                              float eps, int dtype, void* stream);
 
 /*
+ * ak_fused_add_rmsnorm_bwd without a workspace: the same kernels and results
+ * (bitwise), with the partial weight-gradient rows in a fixed 16 MiB device
+ * array inside the library (one per GPU, held until the process ends) instead
+ * of a caller buffer. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * or training loops, harnesses that forbid hipMalloc); it calls no hipMalloc,
+ * hipFree or allocating routine. grad_hidden = NULL gives the plain RMSNorm
+ * backward of ak_rmsnorm_bwd (x passed as hidden). Shapes whose partial rows
+ * (at most 256 workgroup slots, 1024 for rows of <= 512 bf16 / fp16 elements)
+ * times cols x 4 bytes exceed 16 MiB -- cols > 16384 for a full grid -- are
+ * rejected with AK_ERR_WORKSPACE; use ak_fused_add_rmsnorm_bwd for those. The
+ * array is shared by every call on a GPU and keeps the last call's contents:
+ * calls that overlap on one GPU (different streams, or host threads) race.
+ * The first call on each device looks up the array's address on it.
+ */
+int ak_fused_add_rmsnorm_bwd_noalloc(const void* hidden, const void* weight,
+                                     const void* grad_hidden, const void* grad_normed,
+                                     void* grad_x, float* grad_weight,
+                                     int64_t rows, int64_t cols,
+                                     int64_t ld_h, int64_t ld_gh, int64_t ld_gn, int64_t ld_gx,
+                                     float eps, int dtype, void* stream);
+
+/*
  * Row softmax over the last dimension with fp32 accumulation.
  * Replaces kernels/hip/softmax.py:273-326 (softmax_hip); semantics of
  * reference.py:14-17 (softmax_ref). -inf entries give exact zeros.

@@ -146,3 +146,15 @@ def test_ce_reduction_argument_errors(lib):
     rc = lib.ak_ce_bwd_tiny(None, None, None, None, None, 0, 8, 8, 8, 0.0, -100, 0.0, 1.0, -0.5,
                             None, 2, None)
     assert rc == -1 and b"z_loss" in lib.ak_last_error()
+
+
+def test_no_alloc_entry_rejects_beyond_its_scratch(lib):
+    # 256 partial rows x 16392 fp32 columns need more than the fixed 16 MiB;
+    # the size check runs before the pointer checks and any HIP call
+    rc = lib.ak_fused_add_rmsnorm_bwd_noalloc(None, None, None, None, None, ctypes.c_void_p(16),
+                                              512, 16392, 16392, 16392, 16392, 16392, 1e-6, 0, None)
+    assert rc == -4 and b"scratch" in lib.ak_last_error()
+    # exactly 16 MiB (256 x 16384 fp32) passes the size check, then the null check
+    rc = lib.ak_fused_add_rmsnorm_bwd_noalloc(None, None, None, None, None, ctypes.c_void_p(16),
+                                              512, 16384, 16384, 16384, 16384, 16384, 1e-6, 0, None)
+    assert rc == -1 and b"null" in lib.ak_last_error()
