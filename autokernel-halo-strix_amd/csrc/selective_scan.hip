@@ -26,84 +26,10 @@
 // 2048-step chunk, the running prefix (decay product, state) of every state
 // (the reference binding's chunk-state tensor x). The backward's design is
 // described above mamba_scan_bwd_kernel.
-#include "ak_common.h"
+#include "scan_common.h"
 
 namespace ak {
 namespace {
-
-constexpr int kScanT = 64;          // steps per LDS tile
-constexpr int kScanCh = 16;         // channels per workgroup (4 waves x 4)
-constexpr int kBStride = kScanT + 4; // Bs[n][l] row pitch (floats)
-constexpr int kCStride = 20;        // Cs[l][n] row pitch (floats)
-constexpr int kHJ = 20;             // hbuf[c][j][n] step pitch (floats)
-constexpr int kHC = 16 * kHJ + 16;  // hbuf channel pitch: 336 = 16 mod 64
-constexpr int kCk = 16;             // steps between the states saved for the backward
-constexpr int kXChunk = 2048;       // steps per chunk-state entry (the reference's chunk)
-
-struct ScanParams {
-  const void* u;
-  const void* delta;
-  const float* A;
-  const void* B;
-  const void* C;
-  const float* D;
-  const void* z;
-  const float* delta_bias;
-  void* out;
-  float* last_state;
-  void* out_prez;              // optional: y + D u before the gate (strides of out)
-  float* chunk_states;         // optional: [batch, dim, xchunks, dstate, 2] (decay product, state)
-  int xchunks;                 // 2048-step chunks of chunk_states
-  int batch, dim, seqlen, dstate, ngroups, ch_per_group, tiles_per_group;
-  int64_t u_bs, u_ds, d_bs, d_ds, A_ds, B_bs, B_gs, B_ns, C_bs, C_gs, C_ns, z_bs, z_ds, o_bs, o_ds;
-  int softplus;
-  // backward only (the preparation pass and the reverse pass)
-  const void* dout;            // [batch, dim, seqlen], element type of u, strides go_bs / go_ds
-  void* dz;                    // [batch, dim, seqlen], strides of out
-  void* du;                    // [batch, dim, seqlen], strides of out
-  void* ddelta;                // [batch, dim, seqlen] in delta's type, strides of out
-  float* ck;                   // [batch, nchunks, dim, dstate] states before each 16-step block
-                               // (the forward writes them when non-null)
-  float* dB_part;              // [tiles, batch, ngroups, dstate, seqlen]
-  float* dC_part;              // [tiles, batch, ngroups, dstate, seqlen]
-  float* dA_part;              // [batch, dim, dstate]
-  float* dD_part;              // [batch, dim]
-  float* dbias_part;           // [batch, dim]
-  int64_t go_bs, go_ds;
-  int nchunks;
-};
-
-// v * m, with v taken from lane K of each 16-lane row (DPP row_newbcast:K
-// fused into the multiply). The DPP source must not have been written by a
-// VALU instruction in the two preceding cycles; callers write it once per
-// tile and separate that write from the first use with an s_nop 1.
-template <int K>
-__device__ __forceinline__ float mul_bcast(float v, float m) {
-  float r;
-  asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-               : "=v"(r)
-               : "v"(v), "v"(m), "i"(K));
-  return r;
-}
-
-// torch.nn.functional.softplus with beta=1, threshold=20: x above 20, else
-// log1p(e^x). e^x and log2 come from the hardware (about 1 ulp each);
-// log1p(t) = log(1 + t) * t / ((1 + t) - 1) corrects the rounding of 1 + t
-// (D. Goldberg, "What every computer scientist should know about
-// floating-point arithmetic", 1991, Theorem 4), so small results keep their
-// relative accuracy. About 8 instructions instead of a library log1p / exp.
-__device__ __forceinline__ float softplus_f32(float x) {
-  const float t = __builtin_amdgcn_exp2f(fminf(x, 20.0f) * kLog2e);
-  const float u = 1.0f + t;
-  const float lp = u == 1.0f ? t : __builtin_amdgcn_logf(u) * kLn2 * (t * __builtin_amdgcn_rcpf(u - 1.0f));
-  return x > 20.0f ? x : lp;
-}
-
-// silu(z) = z / (1 + exp(-z)) with the hardware exp2 and reciprocal (about
-// 1 ulp each), evaluated once per output element.
-__device__ __forceinline__ float silu_fast(float z) {
-  return z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z * kLog2e));
-}
 
 // kPrep: the preparation pass of the backward. Instead of the output it
 // writes the state before every 64-step tile to p.ck and, with a gate,
@@ -802,44 +728,6 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
 // LDS, and over channel tiles in the final pass (scan_bwd_finalize_kernel)
 // in a fixed order, so every gradient is deterministic.
 // ---------------------------------------------------------------------------
-constexpr int kTJ = 36;             // tbuf[c][j][n] step pitch: float pairs, b128 reads conflict-free
-constexpr int kTC = 16 * kTJ + 32;  // tbuf channel pitch: 608 = 32 mod 64
-constexpr int kWP = 33;             // wbuf[lane][pair] lane pitch
-
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
-// a + b over lanes i and i ^ 32 for x, and the same for y, with x's sums
-// landing in lanes 0..31 and y's in lanes 32..63.
-__device__ __forceinline__ float swap32_sum(float x, float y) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Row pairs (0, 1) and (2, 3): x's sums land in rows 0 and 2, y's in rows 1 and 3.
-__device__ __forceinline__ float swap16_sum(float x, float y) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// acc + v * m, v from lane K of each 16-lane row (DPP as in mul_bcast).
-template <int K>
-__device__ __forceinline__ float fma_bcast(float v, float m, float acc) {
-  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-      : "+v"(acc)
-      : "v"(v), "v"(m), "i"(K));
-  return acc;
-}
-
-__device__ __forceinline__ float sigmoid_f32(float x) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
-}
-
 template <typename TU, typename TD, typename TBC, bool kSoftplus>
 __global__ void __launch_bounds__(256)
 mamba_scan_bwd_kernel(ScanParams p) {
@@ -1104,6 +992,7 @@ scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restri
        i += (int64_t)gridDim.x * blockDim.x) {
     const bool is_c = i >= n4;
     const int64_t e4 = is_c ? i - n4 : i;
+    if (!(is_c ? dC : dB)) continue;
     const float4* part = reinterpret_cast<const float4*>(is_c ? dC_part : dB_part) + e4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     int t = 0;
@@ -1136,38 +1025,47 @@ scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restri
 }
 
 // Fixed-order sums of the reverse pass's partial results:
-//   dB / dC [b, g, n, l] = sum over the channel tiles of the group
-//   dA [d, n], dD [d], dbias [d] = sum over the batch
-// nb = 0 (no steps) writes zeros.
+//   dB / dC [b, g, n, l] = sum over the channel tiles of the group (variable B / C)
+//   dA [d, n], constant dB / dC [d, n], dD [d], dbias [d] = sum over the batch
+// A null destination is skipped; nb = 0 (no steps) writes zeros.
 template <typename TBC>
 __global__ void __launch_bounds__(256)
 scan_bwd_finalize_kernel(const float* __restrict__ dB_part, const float* __restrict__ dC_part,
-                         const float* __restrict__ dA_part, const float* __restrict__ dD_part,
+                         const float* __restrict__ dA_part, const float* __restrict__ dBc_part,
+                         const float* __restrict__ dCc_part, const float* __restrict__ dD_part,
                          const float* __restrict__ dbias_part, TBC* __restrict__ dB,
-                         TBC* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dD,
+                         TBC* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dBc,
+                         float* __restrict__ dCc, float* __restrict__ dD,
                          float* __restrict__ dbias, int64_t nbc, int tiles, int nb, int dim,
                          int dstate) {
   const int64_t nA = (int64_t)dim * dstate;
-  const int64_t total = 2 * nbc + nA + 2 * (int64_t)dim;
+  const int64_t total = 2 * nbc + 3 * nA + 2 * (int64_t)dim;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     if (i < 2 * nbc) {
       const bool is_c = i >= nbc;
       const int64_t e = is_c ? i - nbc : i;
+      TBC* dst = is_c ? dC : dB;
+      if (!dst) continue;
       const float* part = is_c ? dC_part : dB_part;
       float s = 0.0f;
       for (int t = 0; t < tiles; ++t) s += part[(int64_t)t * nbc + e];
-      (is_c ? dC : dB)[e] = from_f32<TBC>(s);
+      dst[e] = from_f32<TBC>(s);
       continue;
     }
     int64_t e = i - 2 * nbc;
-    if (e < nA) {
+    if (e < 3 * nA) {
+      const int k = (int)(e / nA);
+      e -= k * nA;
+      float* dst = k == 0 ? dA : k == 1 ? dBc : dCc;
+      if (!dst) continue;
+      const float* part = k == 0 ? dA_part : k == 1 ? dBc_part : dCc_part;
       float s = 0.0f;
-      for (int bb = 0; bb < nb; ++bb) s += dA_part[(int64_t)bb * nA + e];
-      dA[e] = s;
+      for (int bb = 0; bb < nb; ++bb) s += part[(int64_t)bb * nA + e];
+      dst[e] = s;
       continue;
     }
-    e -= nA;
+    e -= 3 * nA;
     const bool is_bias = e >= dim;
     const int dd = (int)(is_bias ? e - dim : e);
     float* dst = is_bias ? dbias : dD;
@@ -1230,23 +1128,41 @@ int dispatch_scan(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtyp
   return 0;
 }
 
-// Workspace of the Mamba-1 backward, each region 256-byte aligned.
-struct ScanBwdWs {
-  size_t ck, part, dA, dD, total;
-};
+// The backward's finish pass: fixed-order sums of the reverse pass's
+// partials into the gradients. A variable dB / dC comes out in TBC, a
+// constant one ([dim, dstate]) in fp32.
+template <typename TBC>
+void scan_bwd_finish(const ScanParams& p, void* dB, void* dC, float* dA, float* dD, float* dbias,
+                     hipStream_t s) {
+  TBC* dBv = p.b_const ? nullptr : static_cast<TBC*>(dB);
+  TBC* dCv = p.c_const ? nullptr : static_cast<TBC*>(dC);
+  float* dBk = p.b_const ? static_cast<float*>(dB) : nullptr;
+  float* dCk = p.c_const ? static_cast<float*>(dC) : nullptr;
+  int64_t nbc = (dBv || dCv) ? (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen : 0;
+  const size_t out4 = 4 * sizeof(TBC);
+  auto al4 = [&](const void* q) { return !q || reinterpret_cast<uintptr_t>(q) % out4 == 0; };
+  if (nbc > 0 && nbc % 4 == 0 && al4(dBv) && al4(dCv)) {
+    const int64_t n4 = nbc / 4;
+    const unsigned blocks4 = (unsigned)std::min<int64_t>((2 * n4 + 255) / 256, 65535);
+    scan_bwd_bc_sum4_kernel<TBC><<<dim3(blocks4), dim3(256), 0, s>>>(
+        p.dB_part, p.dC_part, dBv, dCv, n4, p.tiles_per_group);
+    nbc = 0;  // the scalar pass below then covers the per-batch sums only
+  }
+  const int64_t total = 2 * nbc + 3 * (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
+  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+  scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(
+      p.dB_part, p.dC_part, p.dA_part, p.dBc_part, p.dCc_part, p.dD_part, p.dbias_part, dBv, dCv,
+      dA, dBk, dCk, dD, dbias, nbc, p.tiles_per_group, p.batch, p.dim, p.dstate);
+}
 
-inline ScanBwdWs scan_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate,
-                             int64_t ngroups) {
-  auto a256 = [](int64_t v) { return (size_t)((v + 255) & ~(int64_t)255); };
-  const int64_t tiles = (dim / ngroups + kScanCh - 1) / kScanCh;
-  const int64_t nck = (seqlen + kCk - 1) / kCk;
-  ScanBwdWs w;
-  w.ck = a256(batch * nck * dim * dstate * 4);
-  w.part = a256(tiles * batch * ngroups * dstate * seqlen * 4);
-  w.dA = a256(batch * dim * dstate * 4);
-  w.dD = a256(batch * dim * 4);
-  w.total = w.ck + 2 * w.part + w.dA + 2 * w.dD;
-  return w;
+int finish_for(int bc_dtype, const ScanParams& p, void* dB, void* dC, float* dA, float* dD,
+               float* dbias, hipStream_t s) {
+  switch (bc_dtype) {
+    case AK_DTYPE_F32: scan_bwd_finish<float>(p, dB, dC, dA, dD, dbias, s); break;
+    case AK_DTYPE_F16: scan_bwd_finish<f16>(p, dB, dC, dA, dD, dbias, s); break;
+    default: scan_bwd_finish<bf16>(p, dB, dC, dA, dD, dbias, s); break;
+  }
+  return 0;
 }
 
 // With the forward's states (p.ck) and pre-gate output (p.out_prez) saved,
@@ -1268,21 +1184,7 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
     mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else
     mamba_scan_bwd_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
-  int64_t nbc = (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen;
-  const size_t out4 = 4 * sizeof(TBC);
-  if (nbc % 4 == 0 && reinterpret_cast<uintptr_t>(dB) % out4 == 0 &&
-      reinterpret_cast<uintptr_t>(dC) % out4 == 0) {
-    const int64_t n4 = nbc / 4;
-    const unsigned blocks4 = (unsigned)std::min<int64_t>((2 * n4 + 255) / 256, 65535);
-    scan_bwd_bc_sum4_kernel<TBC><<<dim3(blocks4), dim3(256), 0, s>>>(
-        p.dB_part, p.dC_part, static_cast<TBC*>(dB), static_cast<TBC*>(dC), n4, p.tiles_per_group);
-    nbc = 0;  // the scalar pass below then covers dA / dD / ddelta_bias only
-  }
-  const int64_t total = 2 * nbc + (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
-  const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-  scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(
-      p.dB_part, p.dC_part, p.dA_part, p.dD_part, p.dbias_part, static_cast<TBC*>(dB),
-      static_cast<TBC*>(dC), dA, dD, dbias, nbc, p.tiles_per_group, p.batch, p.dim, p.dstate);
+  scan_bwd_finish<TBC>(p, dB, dC, dA, dD, dbias, s);
 }
 
 template <typename TU>
@@ -1299,6 +1201,54 @@ int dispatch_scan_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_
   return 0;
 }
 
+// Checks shared by the forward and backward entry points, and the common
+// parameter fields. bc_dtype_eff: the element type of the variable B / C
+// (fp32 when both are constant).
+int scan_common_args(const char* name, ScanParams& p, int64_t batch, int64_t dim, int64_t seqlen,
+                     int64_t dstate, int64_t ngroups, int bc_flags, int u_dtype, int delta_dtype,
+                     int bc_dtype, int a_dtype, int* bc_dtype_eff) {
+  if (batch < 0 || dim <= 0 || seqlen < 0 || dstate <= 0 || ngroups <= 0)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
+  if (a_dtype == AK_DTYPE_C64)
+    return ak_set_error(AK_ERR_UNSUPPORTED,
+                        "%s: complex A (complex64 weights) is not supported; A must be real fp32",
+                        name);
+  if (a_dtype != AK_DTYPE_F32) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: A must be fp32", name);
+  if (dstate > 256)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dstate=%lld > 256 is not supported", name,
+                        (long long)dstate);
+  if (bc_flags & ~(AK_SCAN_B_CONST | AK_SCAN_C_CONST))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: unknown bc_flags %d", name, bc_flags);
+  if (dim % ngroups) return ak_set_error(AK_ERR_INVALID_ARG, "%s: dim %% ngroups != 0", name);
+  const bool both_const = (bc_flags & AK_SCAN_B_CONST) && (bc_flags & AK_SCAN_C_CONST);
+  *bc_dtype_eff = both_const ? AK_DTYPE_F32 : bc_dtype;
+  if (ak_dtype_size(u_dtype) == 0 || ak_dtype_size(delta_dtype) == 0 ||
+      ak_dtype_size(*bc_dtype_eff) == 0)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
+  if (batch > 65535 || dim > (1 << 24) || seqlen > ((int64_t)1 << 31) - kScanT)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
+  p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
+  p.tiles_per_group = (p.ch_per_group + kScanCh - 1) / kScanCh;
+  if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grid too large", name);
+  p.b_const = (bc_flags & AK_SCAN_B_CONST) ? 1 : 0;
+  p.c_const = (bc_flags & AK_SCAN_C_CONST) ? 1 : 0;
+  p.nchunks = (int)((seqlen + kCk - 1) / kCk);
+  p.xchunks = (int)((seqlen + kXChunk - 1) / kXChunk);
+  return AK_OK;
+}
+
+// B / C strides: variable ([batch, ngroups, dstate, seqlen]) or constant
+// ([dim, dstate], group_stride read as the dim stride).
+void scan_bc_strides(ScanParams& p, int64_t B_bs, int64_t B_gs, int64_t B_ns, int64_t C_bs,
+                     int64_t C_gs, int64_t C_ns) {
+  p.B_ns = B_ns;
+  p.C_ns = C_ns;
+  if (p.b_const) { p.B_bs = 0; p.B_gs = 0; p.B_ds = B_gs; } else { p.B_bs = B_bs; p.B_gs = B_gs; }
+  if (p.c_const) { p.C_bs = 0; p.C_gs = 0; p.C_ds = C_gs; } else { p.C_bs = C_bs; p.C_gs = C_gs; }
+}
+
 }  // namespace
 }  // namespace ak
 
@@ -1311,44 +1261,37 @@ extern "C" int ak_selective_scan_fwd(
     int64_t delta_dim_stride, int64_t A_dim_stride, int64_t B_batch_stride,
     int64_t B_group_stride, int64_t B_state_stride, int64_t C_batch_stride,
     int64_t C_group_stride, int64_t C_state_stride, int64_t z_batch_stride, int64_t z_dim_stride,
-    int64_t out_batch_stride, int64_t out_dim_stride, int delta_softplus, int u_dtype,
-    int delta_dtype, int bc_dtype, void* stream) {
+    int64_t out_batch_stride, int64_t out_dim_stride, int delta_softplus, int bc_flags,
+    int u_dtype, int delta_dtype, int bc_dtype, int a_dtype, void* stream) {
   const char* name = "ak_selective_scan_fwd";
-  if (batch < 0 || dim <= 0 || seqlen < 0 || dstate <= 0 || ngroups <= 0)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
-  if (dstate > 16) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dstate=%lld > 16 is not supported", name, (long long)dstate);
-  if (dim % ngroups) return ak_set_error(AK_ERR_INVALID_ARG, "%s: dim %% ngroups != 0", name);
-  if (ak_dtype_size(u_dtype) == 0 || ak_dtype_size(delta_dtype) == 0 || ak_dtype_size(bc_dtype) == 0)
-    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
-  if (batch > 65535 || dim > (1 << 24) || seqlen > ((int64_t)1 << 31) - ak::kScanT)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  ak::ScanParams p{};
+  int bc_eff = 0;
+  int rc = ak::scan_common_args(name, p, batch, dim, seqlen, dstate, ngroups, bc_flags, u_dtype,
+                                delta_dtype, bc_dtype, a_dtype, &bc_eff);
+  if (rc) return rc;
   if (batch == 0 || seqlen == 0) return AK_OK;
   if (!u || !delta || !A || !B || !C || !out) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
-  ak::ScanParams p{};
   p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
   p.delta_bias = delta_bias; p.out = out; p.last_state = last_state;
   p.out_prez = out_prez; p.chunk_states = chunk_states;
   p.ck = checkpoints;
-  p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
-  p.xchunks = (int)((seqlen + ak::kXChunk - 1) / ak::kXChunk);
-  p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
-  p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
-  p.tiles_per_group = (p.ch_per_group + ak::kScanCh - 1) / ak::kScanCh;
-  if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grid too large", name);
   p.u_bs = u_batch_stride; p.u_ds = u_dim_stride; p.d_bs = delta_batch_stride; p.d_ds = delta_dim_stride;
-  p.A_ds = A_dim_stride; p.B_bs = B_batch_stride; p.B_gs = B_group_stride; p.B_ns = B_state_stride;
-  p.C_bs = C_batch_stride; p.C_gs = C_group_stride; p.C_ns = C_state_stride;
+  p.A_ds = A_dim_stride;
+  ak::scan_bc_strides(p, B_batch_stride, B_group_stride, B_state_stride, C_batch_stride,
+                      C_group_stride, C_state_stride);
   p.z_bs = z_batch_stride; p.z_ds = z_dim_stride; p.o_bs = out_batch_stride; p.o_ds = out_dim_stride;
   p.softplus = delta_softplus ? 1 : 0;
   hipStream_t s = ak_stream(stream);
-  int rc;
-  switch (u_dtype) {
-    case AK_DTYPE_F32: rc = ak::dispatch_scan<float>(p, u_dtype, delta_dtype, bc_dtype, s); break;
-    case AK_DTYPE_F16: rc = ak::dispatch_scan<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, s); break;
-    default: rc = ak::dispatch_scan<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, s); break;
+  if (ak::scan_needs_wide(p)) {
+    rc = ak::launch_scan_wide_fwd(p, false, u_dtype, delta_dtype, bc_eff, s);
+  } else {
+    switch (u_dtype) {
+      case AK_DTYPE_F32: rc = ak::dispatch_scan<float>(p, u_dtype, delta_dtype, bc_eff, s); break;
+      case AK_DTYPE_F16: rc = ak::dispatch_scan<ak::f16>(p, u_dtype, delta_dtype, bc_eff, s); break;
+      default: rc = ak::dispatch_scan<ak::bf16>(p, u_dtype, delta_dtype, bc_eff, s); break;
+    }
   }
-  if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and B/C must be fp32 or the dtype of u", name);
+  if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and a variable B/C must be fp32 or the dtype of u", name);
   return ak_check_launch(name);
 }
 
@@ -1405,9 +1348,10 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
 }
 
 extern "C" size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
-                                                       int64_t dstate, int64_t ngroups) {
+                                                       int64_t dstate, int64_t ngroups,
+                                                       int bc_flags) {
   if (batch <= 0 || dim <= 0 || seqlen <= 0 || dstate <= 0 || ngroups <= 0 || dim % ngroups) return 0;
-  return ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups).total;
+  return ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags).total;
 }
 
 extern "C" int ak_selective_scan_bwd(
@@ -1421,83 +1365,76 @@ extern "C" int ak_selective_scan_bwd(
     int64_t B_batch_stride, int64_t B_group_stride, int64_t B_state_stride,
     int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
     int64_t z_batch_stride, int64_t z_dim_stride, int64_t dout_batch_stride,
-    int64_t dout_dim_stride, int delta_softplus, int u_dtype, int delta_dtype, int bc_dtype,
-    void* stream) {
+    int64_t dout_dim_stride, int delta_softplus, int bc_flags, int u_dtype, int delta_dtype,
+    int bc_dtype, int a_dtype, void* stream) {
   const char* name = "ak_selective_scan_bwd";
-  if (batch < 0 || dim <= 0 || seqlen < 0 || dstate <= 0 || ngroups <= 0)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
-  if (dstate > 16) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dstate=%lld > 16 is not supported", name, (long long)dstate);
-  if (dim % ngroups) return ak_set_error(AK_ERR_INVALID_ARG, "%s: dim %% ngroups != 0", name);
-  if (ak_dtype_size(u_dtype) == 0 || ak_dtype_size(delta_dtype) == 0 || ak_dtype_size(bc_dtype) == 0)
-    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
-  if (batch > 65535 || dim > (1 << 24) || seqlen > ((int64_t)1 << 31) - ak::kScanT)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  ak::ScanParams p{};
+  int bc_eff = 0;
+  int rc = ak::scan_common_args(name, p, batch, dim, seqlen, dstate, ngroups, bc_flags, u_dtype,
+                                delta_dtype, bc_dtype, a_dtype, &bc_eff);
+  if (rc) return rc;
   if (!dA) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dA", name);
   if (D && !dD) return ak_set_error(AK_ERR_INVALID_ARG, "%s: D given without dD", name);
   if (delta_bias && !ddelta_bias) return ak_set_error(AK_ERR_INVALID_ARG, "%s: delta_bias given without ddelta_bias", name);
   hipStream_t s = ak_stream(stream);
-  const int bc_size = ak_dtype_size(bc_dtype);
-  if (bc_size == 0) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: unsupported dtype", name);
   if (batch == 0 || seqlen == 0) {
-    // no steps: dA, dD and ddelta_bias are sums over nothing; dB / dC / du / ... are empty
-    switch (bc_dtype) {
-      case AK_DTYPE_F32:
-        ak::scan_bwd_finalize_kernel<float><<<dim3(64), dim3(256), 0, s>>>(
-            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA, dD, ddelta_bias, 0,
-            0, 0, (int)dim, (int)dstate);
-        break;
-      default:
-        ak::scan_bwd_finalize_kernel<ak::bf16><<<dim3(64), dim3(256), 0, s>>>(
-            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA, dD, ddelta_bias, 0,
-            0, 0, (int)dim, (int)dstate);
-        break;
-    }
+    // no steps: dA, dD, ddelta_bias and a constant dB / dC are sums over
+    // nothing; a variable dB / dC, du, ... are empty
+    if (p.b_const && !dB) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dB", name);
+    if (p.c_const && !dC) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dC", name);
+    ak::scan_bwd_finalize_kernel<float><<<dim3(64), dim3(256), 0, s>>>(
+        nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA,
+        p.b_const ? static_cast<float*>(dB) : nullptr, p.c_const ? static_cast<float*>(dC) : nullptr,
+        dD, ddelta_bias, 0, 0, 0, (int)dim, (int)dstate);
     return ak_check_launch(name);
   }
   if (!u || !delta || !A || !B || !C || !dout || !du || !ddelta || !dB || !dC || (z && !dz))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   if (checkpoints && z && !out_prez)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: checkpoints with a gate z need out_prez", name);
-  const ak::ScanBwdWs ws = ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups);
+  const ak::ScanBwdWs ws = ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags);
   if (!workspace || workspace_bytes < ws.total)
     return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
                         workspace_bytes, ws.total);
-  ak::ScanParams p{};
   p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
   p.delta_bias = delta_bias; p.out = nullptr; p.last_state = nullptr;
-  p.batch = (int)batch; p.dim = (int)dim; p.seqlen = (int)seqlen; p.dstate = (int)dstate;
-  p.ngroups = (int)ngroups; p.ch_per_group = (int)(dim / ngroups);
-  p.tiles_per_group = (p.ch_per_group + ak::kScanCh - 1) / ak::kScanCh;
-  if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grid too large", name);
   p.u_bs = u_batch_stride; p.u_ds = u_dim_stride; p.d_bs = delta_batch_stride; p.d_ds = delta_dim_stride;
-  p.A_ds = A_dim_stride; p.B_bs = B_batch_stride; p.B_gs = B_group_stride; p.B_ns = B_state_stride;
-  p.C_bs = C_batch_stride; p.C_gs = C_group_stride; p.C_ns = C_state_stride;
+  p.A_ds = A_dim_stride;
+  ak::scan_bc_strides(p, B_batch_stride, B_group_stride, B_state_stride, C_batch_stride,
+                      C_group_stride, C_state_stride);
   p.z_bs = z_batch_stride; p.z_ds = z_dim_stride;
   p.o_bs = dim * seqlen; p.o_ds = seqlen;  // du, ddelta, dz: contiguous [batch, dim, seqlen]
   p.go_bs = dout_batch_stride; p.go_ds = dout_dim_stride;
   p.softplus = delta_softplus ? 1 : 0;
   p.dout = dout; p.dz = dz; p.du = du; p.ddelta = ddelta;
   char* w = static_cast<char*>(workspace);
-  p.ck = reinterpret_cast<float*>(w);
-  p.dB_part = reinterpret_cast<float*>(w + ws.ck);
-  p.dC_part = reinterpret_cast<float*>(w + ws.ck + ws.part);
-  p.dA_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part);
-  p.dD_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA);
-  p.dbias_part = reinterpret_cast<float*>(w + ws.ck + 2 * ws.part + ws.dA + ws.dD);
-  p.nchunks = (int)((seqlen + ak::kCk - 1) / ak::kCk);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { float* q = bytes ? reinterpret_cast<float*>(w + off) : nullptr; off += bytes; return q; };
+  p.ck = take(ws.ck);
+  p.dB_part = take(ws.partB);
+  p.dC_part = take(ws.partC);
+  p.dA_part = take(ws.dA);
+  p.dD_part = take(ws.dD);
+  p.dbias_part = take(ws.dD);
+  p.dBc_part = take(ws.dBc);
+  p.dCc_part = take(ws.dCc);
   // saved forward states: the reverse pass reads them (and out_prez) in place
   if (checkpoints) {
     p.ck = const_cast<float*>(checkpoints);
     p.out_prez = const_cast<void*>(out_prez);
   }
   const bool saved = checkpoints != nullptr;
-  int rc;
-  switch (u_dtype) {
-    case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
-    case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
-    default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_dtype, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+  if (ak::scan_needs_wide(p)) {
+    if (!saved) rc = ak::launch_scan_wide_fwd(p, true, u_dtype, delta_dtype, bc_eff, s);
+    if (!rc) rc = ak::launch_scan_wide_bwd(p, u_dtype, delta_dtype, bc_eff, s);
+    if (!rc) rc = ak::finish_for(bc_eff, p, dB, dC, dA, dD, ddelta_bias, s);
+  } else {
+    switch (u_dtype) {
+      case AK_DTYPE_F32: rc = ak::dispatch_scan_bwd<float>(p, u_dtype, delta_dtype, bc_eff, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+      case AK_DTYPE_F16: rc = ak::dispatch_scan_bwd<ak::f16>(p, u_dtype, delta_dtype, bc_eff, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+      default: rc = ak::dispatch_scan_bwd<ak::bf16>(p, u_dtype, delta_dtype, bc_eff, dB, dC, dA, dD, ddelta_bias, saved, s); break;
+    }
   }
-  if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and B/C must be fp32 or the dtype of u", name);
+  if (rc) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and a variable B/C must be fp32 or the dtype of u", name);
   return ak_check_launch(name);
 }

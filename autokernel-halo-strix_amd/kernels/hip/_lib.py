@@ -32,6 +32,8 @@ CSRC_DIR = os.path.normpath(os.path.join(os.path.dirname(os.path.abspath(__file_
 
 AK_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 FLOAT_DTYPES = tuple(AK_DTYPE)
+# complex64: named only so that the selective scan's C-ABI can reject a complex A
+AK_DTYPE_C64 = 3
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -66,13 +68,13 @@ _SIGNATURES = {
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
                          _int, _c_void_p],
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _f32, _int, _c_void_p],
-    "ak_selective_scan_fwd": [_c_void_p] * 13 + [_i64] * 5 + [_i64] * 15 + [_int] * 4 + [_c_void_p],
+    "ak_selective_scan_fwd": [_c_void_p] * 13 + [_i64] * 5 + [_i64] * 15 + [_int] * 6 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
     "ak_diag_scan_bwd": [_c_void_p] * 12 + [ctypes.c_size_t] + [_i64] * 3 + [_c_void_p],
-    "ak_selective_scan_bwd_workspace_bytes": [_i64] * 5,
+    "ak_selective_scan_bwd_workspace_bytes": [_i64] * 5 + [_int],
     "ak_selective_scan_bwd": [_c_void_p] * 20 + [ctypes.c_size_t] + [_i64] * 5 + [_i64] * 15
-    + [_int] * 4 + [_c_void_p],
+    + [_int] * 6 + [_c_void_p],
 }
 _RESTYPES = {
     "ak_last_error": ctypes.c_char_p,
@@ -401,18 +403,49 @@ def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
     _check(rc, "ak_lmhead_ce_bwd")
 
 
+# bc_flags of the selective-scan entry points: B / C input-independent ([dim, dstate] fp32)
+SCAN_B_CONST = 1
+SCAN_C_CONST = 2
+
+
+def _scan_bc(B: torch.Tensor, C: torch.Tensor):
+    """(bc_flags, B strides, C strides, ngroups, element-type code of the variable
+    B / C) for B / C that are either variable ``[batch, ngroups, dstate, seqlen]``
+    or input-independent ``[dim, dstate]`` fp32."""
+    flags = 0
+    if B.dim() == 2:
+        flags |= SCAN_B_CONST
+        bs = (0, B.stride(0), B.stride(1))
+    else:
+        bs = (B.stride(0), B.stride(1), B.stride(2))
+    if C.dim() == 2:
+        flags |= SCAN_C_CONST
+        cs = (0, C.stride(0), C.stride(1))
+    else:
+        cs = (C.stride(0), C.stride(1), C.stride(2))
+    var = [t for t in (B, C) if t.dim() == 4]
+    ngroups = var[0].shape[1] if var else 1
+    bc_dtype = dtype_code(var[0].dtype) if var else AK_DTYPE[torch.float32]
+    return flags, bs, cs, ngroups, bc_dtype
+
+
+def _a_code(A: torch.Tensor) -> int:
+    return AK_DTYPE_C64 if A.dtype == torch.complex64 else dtype_code(A.dtype)
+
+
 def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus: bool,
                    out_prez=None, chunk_states=None, checkpoints=None) -> None:
-    """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l]; A [d, n]; optional
-    out_prez (pre-gate output, strides of out), chunk_states [b, d, ceil(l/2048), n, 2]
-    and checkpoints [b, ceil(l/16), d, n] (the states the backward restarts from)."""
+    """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l] or input-independent
+    [d, n] fp32; A [d, n] fp32; optional out_prez (pre-gate output, strides of out),
+    chunk_states [b, d, ceil(l/2048), n, 2] and checkpoints [b, ceil(l/16), d, n]
+    (the states the backward restarts from)."""
     require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state, out_prez, chunk_states,
                    checkpoints)
     if out_prez is not None and out_prez.stride() != out.stride():
         raise ValueError("out_prez must have out's strides")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
-    ngroups = B.shape[1]
+    flags, bs, cs, ngroups, bc_dtype = _scan_bc(B, C)
     zs = (z.stride(0), z.stride(1)) if z is not None else (0, 0)
     with _on_device(u):
         rc = load().ak_selective_scan_fwd(
@@ -420,30 +453,31 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
             _ptr(out), _ptr(last_state), _ptr(out_prez), _ptr(chunk_states), _ptr(checkpoints),
             batch, dim, seqlen, dstate, ngroups,
             u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
-            B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),
-            zs[0], zs[1], out.stride(0), out.stride(1),
-            int(bool(delta_softplus)), dtype_code(u.dtype), dtype_code(delta.dtype),
-            dtype_code(B.dtype), _stream(u))
+            *bs, *cs, zs[0], zs[1], out.stride(0), out.stride(1),
+            int(bool(delta_softplus)), flags, dtype_code(u.dtype), dtype_code(delta.dtype),
+            bc_dtype, _a_code(A), _stream(u))
     _check(rc, "ak_selective_scan_fwd")
 
 
 def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
                        ddelta_bias, delta_softplus: bool, checkpoints=None, out_prez=None) -> None:
-    """Mamba-1 backward. u/delta/z/dout [b, d, l] (last dim contiguous); B/C [b, g, n, l];
-    A [d, n]; outputs du/ddelta/dz contiguous [b, d, l], dB/dC contiguous [b, g, n, l] in
-    B's dtype, dA [d, n] / dD [d] / ddelta_bias [d] fp32. With the forward's
-    ``checkpoints`` (and, with z, its contiguous ``out_prez``) the states are not
-    recomputed."""
+    """Mamba-1 backward. u/delta/z/dout [b, d, l] (last dim contiguous); B/C
+    [b, g, n, l] or input-independent [d, n] fp32; A [d, n]; outputs du/ddelta/dz
+    contiguous [b, d, l], dB/dC contiguous in B's / C's layout (a variable one in
+    its dtype, an input-independent one fp32), dA [d, n] / dD [d] / ddelta_bias [d]
+    fp32. With the forward's ``checkpoints`` (and, with z, its contiguous
+    ``out_prez``) the states are not recomputed."""
     require_device(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
                    ddelta_bias, checkpoints, out_prez)
     if out_prez is not None and not out_prez.is_contiguous():
         raise ValueError("out_prez must be contiguous")
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
-    ngroups = B.shape[1]
+    flags, bs, cs, ngroups, bc_dtype = _scan_bc(B, C)
     zs = (z.stride(0), z.stride(1)) if z is not None else (0, 0)
     lib = load()
-    ws = torch.empty(int(lib.ak_selective_scan_bwd_workspace_bytes(batch, dim, seqlen, dstate, ngroups)),
+    ws = torch.empty(int(lib.ak_selective_scan_bwd_workspace_bytes(batch, dim, seqlen, dstate,
+                                                                   ngroups, flags)),
                      dtype=torch.uint8, device=u.device)
     with _on_device(u):
         rc = lib.ak_selective_scan_bwd(
@@ -452,10 +486,9 @@ def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA
             _ptr(ddelta_bias), _ptr(checkpoints), _ptr(out_prez), _ptr(ws), ws.numel(),
             batch, dim, seqlen, dstate, ngroups,
             u.stride(0), u.stride(1), delta.stride(0), delta.stride(1), A.stride(0),
-            B.stride(0), B.stride(1), B.stride(2), C.stride(0), C.stride(1), C.stride(2),
-            zs[0], zs[1], dout.stride(0), dout.stride(1),
-            int(bool(delta_softplus)), dtype_code(u.dtype), dtype_code(delta.dtype),
-            dtype_code(B.dtype), _stream(u))
+            *bs, *cs, zs[0], zs[1], dout.stride(0), dout.stride(1),
+            int(bool(delta_softplus)), flags, dtype_code(u.dtype), dtype_code(delta.dtype),
+            bc_dtype, _a_code(A), _stream(u))
     _check(rc, "ak_selective_scan_bwd")
 
 

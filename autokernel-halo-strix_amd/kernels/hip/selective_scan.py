@@ -18,14 +18,33 @@ Two entry points, both drop-ins:
   in fp32 rather than in ``z``'s dtype.
 
   Accepted layouts: ``u, delta, z`` ``[batch, dim, seqlen]`` (last dim
-  contiguous), ``A`` real ``[dim, dstate]`` with ``dstate <= 16``, ``B`` / ``C``
-  ``[batch, dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``.
-  ``delta`` may be fp32 or ``u``'s dtype; ``B`` / ``C`` fp32 or ``u``'s dtype.
-  Complex ``A`` and input-independent (2-D) ``B`` / ``C`` raise
-  ``NotImplementedError``. The backward (``ak_selective_scan_bwd``) returns
-  every input gradient of the reference's ``selective_scan_cuda.bwd``: ``du``,
+  contiguous), ``A`` real ``[dim, dstate]`` with ``dstate <= 256`` (the
+  reference binding's limit, ``selective_scan.cpp:262``), ``B`` / ``C``
+  ``[batch, dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``
+  (input-dependent, fp32 or ``u``'s dtype) or ``[dim, dstate]``
+  (input-independent, computed in fp32, as the reference's
+  ``!is_variable_B`` path, ``selective_scan_interface.py:138-160``).
+  ``delta`` may be fp32 or ``u``'s dtype. dstate <= 16 with input-dependent
+  B / C runs the specialised kernels; everything else the general ones.
+  Complex ``A`` raises ``NotImplementedError`` (the C-ABI rejects complex
+  weights). The backward (``ak_selective_scan_bwd``) returns every input
+  gradient of the reference's ``selective_scan_cuda.bwd``: ``du``,
   ``ddelta``, ``dA``, ``dB``, ``dC``, ``dD``, ``dz``, ``ddelta_bias``, each
-  computed deterministically (fixed summation order).
+  computed deterministically (fixed summation order); an input-dependent
+  ``dB`` / ``dC`` is summed in fp32 and rounded once to B's / C's dtype, as
+  the reference's fp32 accumulation and ``dB.to(B.dtype())``
+  (``selective_scan.cpp:461``, ``:488``).
+
+  Memory of the training path: when autograd records the call, the forward
+  keeps its state every 16 steps for the backward (fp32 ``[batch,
+  ceil(seqlen / 16), dim, dstate]``: 4 * dstate / 16 bytes per (batch, dim,
+  step), i.e. 134 MB at batch 4, seqlen 4096, dim 2048, dstate 16, about
+  twice a bf16 ``u``, and 16x that at dstate 256) plus, with a gate, its
+  pre-gate output (one more ``u``-sized tensor). The reference keeps only its
+  2048-step chunk states and recomputes. :func:`set_save_states` (or
+  ``AUTOKERNEL_SCAN_RECOMPUTE=1`` at import) switches to recomputation;
+  ``SAVE_STATES_MAX_BYTES`` caps the checkpoint size above which a call
+  recomputes instead.
 """
 
 import os
@@ -46,8 +65,23 @@ CHUNK = 2048
 CHECKPOINT_STEPS = 16
 # Training keeps those states (fp32, batch x ceil(seqlen / 16) x dim x dstate: at
 # dstate 16 about twice the bytes of a bf16 u) so that the backward does not re-run
-# the forward; AUTOKERNEL_SCAN_RECOMPUTE=1 (or setting this to False) recomputes.
+# the forward; AUTOKERNEL_SCAN_RECOMPUTE=1 (or set_save_states(False)) recomputes.
 SAVE_STATES = os.environ.get("AUTOKERNEL_SCAN_RECOMPUTE", "0") != "1"
+# Calls whose checkpoints would exceed this many bytes recompute instead (None: no cap).
+SAVE_STATES_MAX_BYTES = None
+
+
+def set_save_states(enabled: bool, max_bytes=None) -> None:
+    """Whether training keeps the forward's 16-step states (see the module
+    docstring for their size), and the per-call size above which it does not."""
+    global SAVE_STATES, SAVE_STATES_MAX_BYTES
+    SAVE_STATES = bool(enabled)
+    SAVE_STATES_MAX_BYTES = max_bytes
+
+
+def _checkpoint_bytes(u: torch.Tensor, A: torch.Tensor) -> int:
+    batch, dim, seqlen = u.shape
+    return 4 * batch * dim * A.shape[1] * ((seqlen + CHECKPOINT_STEPS - 1) // CHECKPOINT_STEPS)
 
 
 def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Tensor,
@@ -73,13 +107,15 @@ def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Ten
 
 def _normalise(u, delta, A, B, C, D, z, delta_bias):
     """Checks shapes and brings the inputs to the layouts the kernels take:
-    last dims contiguous, B / C 4-D, A / D / delta_bias fp32, z in u's dtype,
-    delta and B / C in fp32 or u's dtype."""
+    last dims contiguous, input-dependent B / C 4-D (fp32 or u's dtype, C in
+    B's dtype when both are input-dependent), input-independent B / C
+    ``[dim, dstate]`` fp32, A / D / delta_bias fp32, z in u's dtype, delta in
+    fp32 or u's dtype."""
     _lib.require_device(u, delta, A, B, C, D, z, delta_bias)
     if A.is_complex():
-        raise NotImplementedError("complex A is not supported by the gfx950 selective scan")
-    if B.dim() < 3 or C.dim() < 3:
-        raise NotImplementedError("input-independent (2-D) B / C are not supported; pass [b, n, l] or [b, g, n, l]")
+        raise NotImplementedError(
+            "complex A is not supported by the gfx950 selective scan (real fp32 A only; "
+            "the C-ABI rejects complex weights)")
     if u.dim() != 3:
         raise ValueError("u must be [batch, dim, seqlen]")
     batch, dim, seqlen = u.shape
@@ -89,19 +125,31 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
         delta = delta.contiguous()
     if delta.shape != u.shape:
         raise ValueError("delta must have the shape of u")
-    if B.dim() == 3:
-        B = B.unsqueeze(1)
-    if C.dim() == 3:
-        C = C.unsqueeze(1)
-    if B.stride(-1) != 1:
-        B = B.contiguous()
-    if C.stride(-1) != 1:
-        C = C.contiguous()
-    dstate = A.shape[1]
-    if A.shape[0] != dim:
+    if A.dim() != 2 or A.shape[0] != dim:
         raise ValueError("A must be [dim, dstate]")
-    if B.shape[0] != batch or B.shape[2] != dstate or B.shape[3] != seqlen or C.shape != B.shape:
-        raise ValueError(f"B / C must be [batch, ngroups, dstate, seqlen], got {tuple(B.shape)}, {tuple(C.shape)}")
+    dstate = A.shape[1]
+
+    def bc(t, name):
+        if t.dim() == 2:  # input-independent
+            if tuple(t.shape) != (dim, dstate):
+                raise ValueError(f"input-independent {name} must be [dim, dstate], got {tuple(t.shape)}")
+            return t.float()
+        if t.dim() == 3:
+            t = t.unsqueeze(1)
+        if t.dim() != 4 or t.shape[0] != batch or t.shape[2] != dstate or t.shape[3] != seqlen \
+                or dim % t.shape[1]:
+            raise ValueError(f"{name} must be [batch, ngroups, dstate, seqlen] or [dim, dstate], "
+                             f"got {tuple(t.shape)}")
+        if t.dtype not in (torch.float32, u.dtype):
+            t = t.float()
+        return t if t.stride(-1) == 1 else t.contiguous()
+
+    B, C = bc(B, "B"), bc(C, "C")
+    if B.dim() == 4 and C.dim() == 4:
+        if C.shape != B.shape:
+            raise ValueError(f"B / C must have one shape, got {tuple(B.shape)}, {tuple(C.shape)}")
+        if C.dtype != B.dtype:
+            C = C.to(B.dtype)
     A = A.float()
     if A.stride(1) != 1:
         A = A.contiguous()
@@ -118,10 +166,6 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
             z = z.contiguous()
     if delta.dtype not in (torch.float32, u.dtype):
         delta = delta.float()
-    if B.dtype not in (torch.float32, u.dtype):
-        B = B.float()
-    if C.dtype != B.dtype:
-        C = C.to(B.dtype)
     return u, delta, A, B, C, D, z, delta_bias
 
 
@@ -190,7 +234,9 @@ class SelectiveScanFn(torch.autograd.Function):
         # grad_mode: whether autograd was recording at the call (forward itself
         # runs without it); needs_input_grad alone is also true under no_grad
         # for inputs that require grad, e.g. parameters during inference
-        keep = SAVE_STATES and any(ctx.needs_input_grad[:8]) and grad_mode is not False
+        keep = (SAVE_STATES and any(ctx.needs_input_grad[:8]) and grad_mode is not False
+                and (SAVE_STATES_MAX_BYTES is None
+                     or _checkpoint_bytes(u, A) <= SAVE_STATES_MAX_BYTES))
         res = _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
                             want_checkpoints=keep)
         out, last_state, saved = res[:3]
@@ -200,6 +246,7 @@ class SelectiveScanFn(torch.autograd.Function):
         ctx.delta_softplus = bool(delta_softplus)
         ctx.squeeze_B = B.dim() == 3
         ctx.squeeze_C = C.dim() == 3
+        ctx.bc_dtypes = (B.dtype, C.dtype)
         ctx.has_D = D is not None
         ctx.has_z = z is not None
         ctx.has_bias = delta_bias is not None
@@ -224,6 +271,7 @@ class SelectiveScanFn(torch.autograd.Function):
             dB = dB.squeeze(1)
         if ctx.squeeze_C:
             dC = dC.squeeze(1)
+        dB, dC = dB.to(ctx.bc_dtypes[0]), dC.to(ctx.bc_dtypes[1])
         return du, ddelta, dA, dB, dC, dD, dz, dbias, None, None, None
 
 

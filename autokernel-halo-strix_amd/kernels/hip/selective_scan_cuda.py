@@ -10,11 +10,17 @@ this module in its place::
 
     from kernels.hip import selective_scan_cuda
 
+The binding's contract is kept: ``dstate <= 256``
+(``selective_scan.cpp:262``), input-dependent ``B`` / ``C`` (``[batch,
+dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``) or
+input-independent ones (``[dim, dstate]`` fp32, ``:115-121``), and the
+gradients of input-dependent ``B`` / ``C`` summed in fp32 and returned in
+their dtype (``:461``, ``:488``; an input-independent one is fp32).
+
 Differences, by design: the backward recomputes the states itself, so the
 chunk-state tensor ``x`` and the forward output ``out`` passed to ``bwd`` are
 accepted and not read; ``delta`` may be fp32 with half-precision ``u``;
-complex ``A`` and input-independent (2-D) ``B`` / ``C`` raise
-``NotImplementedError``.
+complex ``A`` raises ``NotImplementedError`` (real weights only).
 """
 
 from kernels.hip.selective_scan import _normalise, _scan_backward, _scan_forward

@@ -33,6 +33,12 @@ extern "C" {
 #define AK_DTYPE_F32 0
 #define AK_DTYPE_F16 1
 #define AK_DTYPE_BF16 2
+/* complex64; only named so that the selective scan can reject a complex A */
+#define AK_DTYPE_C64 3
+
+/* Selective-scan bc_flags: B / C input-independent, [dim, dstate] fp32 */
+#define AK_SCAN_B_CONST 1
+#define AK_SCAN_C_CONST 2
 
 #define AK_OK 0
 #define AK_ERR_INVALID_ARG (-1)
@@ -269,8 +275,16 @@ int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targ
  * state.
  *   u, z, out : [batch, dim, seqlen], element type u_dtype, last dim contiguous
  *   delta     : [batch, dim, seqlen], element type delta_dtype
- *   A         : [dim, dstate] fp32 (real)
- *   B, C      : [batch, ngroups, dstate, seqlen], element type bc_dtype
+ *   A         : [dim, dstate] fp32 (real): a_dtype must be AK_DTYPE_F32;
+ *               AK_DTYPE_C64 (the reference's complex weights,
+ *               selective_scan_interface.py:140-145) returns AK_ERR_UNSUPPORTED
+ *   B, C      : variable: [batch, ngroups, dstate, seqlen], element type
+ *               bc_dtype (strides batch / group / state);
+ *               with AK_SCAN_B_CONST / AK_SCAN_C_CONST in bc_flags:
+ *               input-independent [dim, dstate] fp32 (the reference's
+ *               !is_variable_B / !is_variable_C, selective_scan.cpp:115-121):
+ *               group_stride is then the dim stride, state_stride the state
+ *               stride, batch_stride is ignored
  *   D, delta_bias : [dim] fp32 or NULL;  z may be NULL
  *   last_state: [batch, dim, dstate] fp32 or NULL
  *   out_prez  : y + D u before the gate, like out (strides of out), or NULL
@@ -283,7 +297,10 @@ int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targ
  *               state before every 16-step block, for ak_selective_scan_bwd
  *               to restart from instead of re-running the forward (training
  *               keeps them; the reference's backward recomputes from `x`)
- * Strides are in elements. dim must be a multiple of ngroups; dstate <= 16.
+ * Strides are in elements. dim must be a multiple of ngroups; dstate <= 256
+ * (the reference binding's limit, selective_scan.cpp:262). dstate <= 16 with
+ * variable B / C runs the specialised kernels, everything else the general
+ * ones.
  */
 int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           const void* B, const void* C, const float* D,
@@ -299,8 +316,8 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
                           int64_t z_batch_stride, int64_t z_dim_stride,
                           int64_t out_batch_stride, int64_t out_dim_stride,
-                          int delta_softplus,
-                          int u_dtype, int delta_dtype, int bc_dtype, void* stream);
+                          int delta_softplus, int bc_flags,
+                          int u_dtype, int delta_dtype, int bc_dtype, int a_dtype, void* stream);
 
 /*
  * Mamba-1 selective scan backward: every input gradient of
@@ -309,11 +326,15 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  * external/mamba/mamba_ssm/ops/selective_scan_interface.py:59-83 (its
  * recompute_out_z option and the saved chunk states x are not needed: the
  * states are recomputed here, or taken from the forward's checkpoints).
- *   inputs as for ak_selective_scan_fwd; dout [batch, dim, seqlen] in u_dtype
+ *   inputs, bc_flags and a_dtype as for ak_selective_scan_fwd; dout
+ *               [batch, dim, seqlen] in u_dtype
  *   du, dz    : contiguous [batch, dim, seqlen], u_dtype (dz only with z)
  *   ddelta    : contiguous [batch, dim, seqlen], delta_dtype
  *   dA        : contiguous [dim, dstate] fp32
- *   dB, dC    : contiguous [batch, ngroups, dstate, seqlen], bc_dtype
+ *   dB, dC    : variable: contiguous [batch, ngroups, dstate, seqlen] in
+ *               bc_dtype (summed in fp32 and rounded once, as the reference's
+ *               fp32 accumulation and dB.to(B.dtype()), selective_scan.cpp:461,
+ *               :488); constant: contiguous [dim, dstate] fp32
  *   dD, ddelta_bias : [dim] fp32, required when D / delta_bias are given
  *   checkpoints, out_prez : NULL, or the forward's `checkpoints` and (with z)
  *               its `out_prez` as a contiguous [batch, dim, seqlen] tensor.
@@ -327,7 +348,7 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  * reduced in a fixed order: results are bitwise reproducible).
  */
 size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
-                                             int64_t dstate, int64_t ngroups);
+                                             int64_t dstate, int64_t ngroups, int bc_flags);
 int ak_selective_scan_bwd(const void* u, const void* delta, const float* A,
                           const void* B, const void* C, const float* D,
                           const void* z, const float* delta_bias, const void* dout,
@@ -344,8 +365,8 @@ int ak_selective_scan_bwd(const void* u, const void* delta, const float* A,
                           int64_t C_batch_stride, int64_t C_group_stride, int64_t C_state_stride,
                           int64_t z_batch_stride, int64_t z_dim_stride,
                           int64_t dout_batch_stride, int64_t dout_dim_stride,
-                          int delta_softplus,
-                          int u_dtype, int delta_dtype, int bc_dtype, void* stream);
+                          int delta_softplus, int bc_flags,
+                          int u_dtype, int delta_dtype, int bc_dtype, int a_dtype, void* stream);
 
 /*
  * Diagonal linear recurrence over [batch, seqlen, d_inner] fp32 tensors:

@@ -34,11 +34,23 @@ def _f32(t: Optional[torch.Tensor]):
 
 def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                    initial_state=None):
-    """Returns ``(out fp32 [b, d, l], last_state fp32 [b, d, n])``."""
+    """Returns ``(out fp32 [b, d, l], last_state fp32 [b, d, n])``.
+
+    An input-independent B or C (``[dim, n]``) is expanded to one group per
+    channel (with the other one repeated to match), which is the same scan."""
     if B.dim() == 3:
         B = B.unsqueeze(1)
     if C.dim() == 3:
         C = C.unsqueeze(1)
+    if B.dim() == 2 or C.dim() == 2:
+        b_, d_, l_ = u.shape
+
+        def per_channel(t):
+            if t.dim() == 2:
+                return t[None, :, :, None].expand(b_, d_, t.shape[1], l_)
+            return t.repeat_interleave(d_ // t.shape[1], dim=1)
+
+        B, C = per_channel(B), per_channel(C)
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     ngroups = B.shape[1]

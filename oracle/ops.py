@@ -223,13 +223,25 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
 # ---------------------------------------------------------------------------
 
 
+def _bc_per_channel(t: torch.Tensor, batch: int, dim: int, seqlen: int) -> torch.Tensor:
+    """B or C as ``[batch, dim, dstate, seqlen]``: an input-dependent one
+    (``[b, n, l]`` or ``[b, g, n, l]``) repeated over each group's channels, an
+    input-independent one (``[dim, n]``, ``selective_scan_interface.py:
+    151-152``) repeated over batch and steps."""
+    if t.dim() == 2:
+        return t[None, :, :, None].expand(batch, dim, t.shape[1], seqlen)
+    if t.dim() == 3:
+        t = t.unsqueeze(1)
+    return t.repeat_interleave(dim // t.shape[1], dim=1)
+
+
 def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                        return_last_state=False, initial_state: Optional[torch.Tensor] = None,
                        silu_fp32: bool = True, compute_dtype: torch.dtype = torch.float32):
     """``external/mamba/mamba_ssm/ops/selective_scan_interface.py:115-181`` (real A).
 
     fp32 state; B / C given as [b, n, l] or [b, g, n, l] (groups repeated over
-    dim). ``silu_fp32=True`` evaluates silu(z) in fp32 (the gfx950 kernel's
+    dim) or input-independent [dim, n]. ``silu_fp32=True`` evaluates silu(z) in fp32 (the gfx950 kernel's
     choice); ``False`` evaluates it in z's dtype as the reference does (:179).
     ``initial_state`` [b, d, n] (fp32) starts the recurrence from a given
     state; the reference starts from zeros. ``compute_dtype=torch.float64``
@@ -245,13 +257,8 @@ def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
     if delta_softplus:
         delta = F.softplus(delta)
     batch, dim, dstate = u.shape[0], A.shape[0], A.shape[1]
-    Bf, Cf = B.to(cd), C.to(cd)
-    if Bf.dim() == 3:
-        Bf = Bf.unsqueeze(1)
-    if Cf.dim() == 3:
-        Cf = Cf.unsqueeze(1)
-    Bf = Bf.repeat_interleave(dim // Bf.shape[1], dim=1)  # [b, d, n, l]
-    Cf = Cf.repeat_interleave(dim // Cf.shape[1], dim=1)
+    Bf = _bc_per_channel(B.to(cd), batch, dim, u.shape[2])  # [b, d, n, l]
+    Cf = _bc_per_channel(C.to(cd), batch, dim, u.shape[2])
     x = (torch.zeros(batch, dim, dstate, dtype=cd) if initial_state is None
          else initial_state.to(cd).clone())
     deltaA = torch.exp(delta[:, :, :, None] * A.to(cd)[None, :, None, :])         # [b, d, l, n]
@@ -284,8 +291,7 @@ def selective_scan_chunk_states_ref(u, delta, A, B, delta_bias=None, delta_softp
     dstate = A.shape[1]
     draw = delta.to(f) + (delta_bias.to(f)[..., None] if delta_bias is not None else 0.0)
     dl = F.softplus(draw) if delta_softplus else draw
-    B4 = B.to(f).unsqueeze(1) if B.dim() == 3 else B.to(f)
-    Bd = B4.repeat_interleave(dim // B4.shape[1], dim=1)  # [b, d, n, l]
+    Bd = _bc_per_channel(B.to(f), batch, dim, seqlen)  # [b, d, n, l]
     nch = (seqlen + chunk - 1) // chunk
     out = torch.empty(batch, dim, nch, dstate, 2, dtype=f)
     prod = torch.ones(batch, dim, dstate, dtype=f)
@@ -302,7 +308,8 @@ def selective_scan_chunk_states_ref(u, delta, A, B, delta_bias=None, delta_softp
 
 def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None,
                            delta_softplus=False):
-    """Gradients of :func:`selective_scan_ref` (real A, variable B / C), in
+    """Gradients of :func:`selective_scan_ref` (real A; B / C input-dependent or
+    input-independent [dim, n], whose gradients sum over batch and steps), in
     float64, by the reverse recurrence of the reference's backward kernel
     (``external/mamba/csrc/selective_scan/selective_scan_bwd_kernel.cuh``:
     dz and the gated dout :189-197, dD :219, the per-step terms :284-300,
@@ -324,11 +331,8 @@ def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=N
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     A64 = A.to(f)
-    B4 = B.to(f).unsqueeze(1) if B.dim() == 3 else B.to(f)
-    C4 = C.to(f).unsqueeze(1) if C.dim() == 3 else C.to(f)
-    ngroups = B4.shape[1]
-    Bd = B4.repeat_interleave(dim // ngroups, dim=1)  # [b, d, n, l]
-    Cd = C4.repeat_interleave(dim // ngroups, dim=1)
+    Bd = _bc_per_channel(B.to(f), batch, dim, seqlen)  # [b, d, n, l]
+    Cd = _bc_per_channel(C.to(f), batch, dim, seqlen)
     a = torch.exp(dl[:, :, None, :] * A64[None, :, :, None])  # [b, d, n, l]
     x = (dl * u64)[:, :, None, :] * Bd
     h = torch.empty(batch, dim, dstate, seqlen, dtype=f)
@@ -362,12 +366,17 @@ def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=N
     dA = (gh * dl[:, :, None] * ah).sum((0, 3))
     dB_d = gh * (dl * u64)[:, :, None]  # [b, d, n, l]
     dC_d = dy[:, :, None] * h
-    dB = dB_d.reshape(batch, ngroups, dim // ngroups, dstate, seqlen).sum(2)
-    dC = dC_d.reshape(batch, ngroups, dim // ngroups, dstate, seqlen).sum(2)
-    if B.dim() == 3:
-        dB = dB.squeeze(1)
-    if C.dim() == 3:
-        dC = dC.squeeze(1)
+
+    def fold(g_d, like):
+        """The per-channel gradient back to the layout of B / C: summed over
+        each group's channels, or over batch and steps for [dim, n]."""
+        if like.dim() == 2:
+            return g_d.sum((0, 3))
+        ng = 1 if like.dim() == 3 else like.shape[1]
+        out = g_d.reshape(batch, ng, dim // ng, dstate, seqlen).sum(2)
+        return out.squeeze(1) if like.dim() == 3 else out
+
+    dB, dC = fold(dB_d, B), fold(dC_d, C)
     if delta_softplus:
         ddelta = torch.where(draw <= 20.0, ddl * torch.sigmoid(draw), ddl)
     else:

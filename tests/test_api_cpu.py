@@ -204,8 +204,18 @@ def test_selective_scan_fn_api(fake_backend):
     out, last = selective_scan_fn(u, delta, A, B, C, torch.ones(4), return_last_state=True)
     ref, rl = ops.selective_scan_ref(u, delta, A, B, C, torch.ones(4), return_last_state=True)
     assert torch.allclose(out, ref) and torch.allclose(last, rl)
-    with pytest.raises(NotImplementedError):
-        selective_scan_fn(u, delta, A, torch.randn(4, 8), C)
+    # input-independent B / C ([dim, dstate]) and complex A
+    B2, C2 = torch.randn(4, 8, generator=g), torch.randn(4, 8, generator=g)
+    for bb, cc in ((B2, C), (B, C2), (B2, C2)):
+        out2 = selective_scan_fn(u, delta, A, bb, cc, torch.ones(4))
+        assert torch.allclose(out2, ops.selective_scan_ref(u, delta, A, bb, cc, torch.ones(4)))
+    with pytest.raises(NotImplementedError, match="complex"):
+        selective_scan_fn(u, delta, A.to(torch.complex64), B, C)
+    with pytest.raises(ValueError):
+        selective_scan_fn(u, delta, A, torch.randn(5, 8), C)
+    Bl = B2.clone().requires_grad_()
+    selective_scan_fn(u, delta, A, Bl, C).sum().backward()
+    assert Bl.grad.shape == (4, 8) and Bl.grad.dtype == torch.float32
     # backward: the autograd function hands the layouts it normalised to the
     # backward entry point and maps the gradients back (dB / dC squeezed to
     # B's / C's [b, n, l], dtype casts by autograd)

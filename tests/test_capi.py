@@ -70,7 +70,8 @@ def test_argument_errors_return_codes(lib):
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
         rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, 0.0, ls, 2, None)
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
-    rc = _lib.load().ak_selective_scan_fwd(*([None] * 13), 2, 4, 16, 32, 1, *([0] * 15), 0, 2, 0, 2, None)
+    rc = _lib.load().ak_selective_scan_fwd(*([None] * 13), 2, 4, 16, 300, 1, *([0] * 15), 0, 0, 2, 0,
+                                           2, 0, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     # zero-size work is a no-op success
     assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0
@@ -86,23 +87,23 @@ def test_selective_scan_bwd_workspace_and_argument_errors(lib):
     tiles = (d // g + 15) // 16
     want = (a256(b * ((l + 15) // 16) * d * n * 4) + 2 * a256(tiles * b * g * n * l * 4)
             + a256(b * d * n * 4) + 2 * a256(b * d * 4))
-    assert lib.ak_selective_scan_bwd_workspace_bytes(b, d, l, n, g) == want
-    assert lib.ak_selective_scan_bwd_workspace_bytes(0, d, l, n, g) == 0
-    assert lib.ak_selective_scan_bwd_workspace_bytes(b, 41, l, n, g) == 0  # dim % ngroups
+    assert lib.ak_selective_scan_bwd_workspace_bytes(b, d, l, n, g, 0) == want
+    assert lib.ak_selective_scan_bwd_workspace_bytes(0, d, l, n, g, 0) == 0
+    assert lib.ak_selective_scan_bwd_workspace_bytes(b, 41, l, n, g, 0) == 0  # dim % ngroups
     fn = _lib.load().ak_selective_scan_bwd
     strides = [0] * 15
-    rc = fn(*([None] * 19), None, 0, 2, 4, 16, 32, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*([None] * 19), None, 0, 2, 4, 16, 300, 1, *strides, 0, 0, 2, 0, 2, 0, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()
     fake = 4096  # never dereferenced: every check below fails first
     ptrs = [fake] * 17 + [None, None]  # no saved checkpoints / out_prez
     ptrs[14] = None  # dD missing while D is given
-    rc = fn(*ptrs, None, 0, 2, 4, 16, 8, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*ptrs, None, 0, 2, 4, 16, 8, 1, *strides, 0, 0, 2, 0, 2, 0, None)
     assert rc == -1 and b"dD" in lib.ak_last_error()
-    rc = fn(*([fake] * 17), fake, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*([fake] * 17), fake, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 0, 2, 0, 2, 0, None)
     assert rc == -1 and b"out_prez" in lib.ak_last_error()  # checkpoints and z without out_prez
-    rc = fn(*([fake] * 17), None, None, fake, 1024, 2, 4, 64, 8, 1, *strides, 0, 2, 0, 2, None)
+    rc = fn(*([fake] * 17), None, None, fake, 1024, 2, 4, 64, 8, 1, *strides, 0, 0, 2, 0, 2, 0, None)
     assert rc < 0 and b"workspace" in lib.ak_last_error()
-    rc = fn(*([fake] * 17), None, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 2, 3, 2, None)
+    rc = fn(*([fake] * 17), None, None, fake, 1 << 30, 2, 4, 64, 8, 1, *strides, 0, 0, 2, 3, 2, 0, None)
     assert rc == -2 and b"dtype" in lib.ak_last_error()  # delta neither fp32 nor u's type
 
 
@@ -158,3 +159,29 @@ def test_no_alloc_entry_rejects_beyond_its_scratch(lib):
     rc = lib.ak_fused_add_rmsnorm_bwd_noalloc(None, None, None, None, None, ctypes.c_void_p(16),
                                               512, 16384, 16384, 16384, 16384, 16384, 1e-6, 0, None)
     assert rc == -1 and b"null" in lib.ak_last_error()
+
+
+def _scan_fwd_args(dstate=16, bc_flags=0, bc_dtype=2, a_dtype=0, batch=0):
+    # batch 0: every argument check runs, then the call returns before any HIP work
+    return ([None] * 13 + [batch, 8, 64, dstate, 1] + [0] * 15
+            + [1, bc_flags, 2, 0, bc_dtype, a_dtype, None])
+
+
+def test_selective_scan_argument_contract(lib):
+    f = lib.ak_selective_scan_fwd
+    assert f(*_scan_fwd_args(dstate=256)) == 0            # the reference binding's limit
+    assert f(*_scan_fwd_args(dstate=64, bc_flags=3)) == 0  # input-independent B and C
+    rc = f(*_scan_fwd_args(dstate=257))
+    assert rc == -2 and b"256" in lib.ak_last_error()
+    rc = f(*_scan_fwd_args(a_dtype=3))
+    assert rc == -2 and b"complex" in lib.ak_last_error()
+    rc = f(*_scan_fwd_args(bc_flags=4))
+    assert rc == -1 and b"bc_flags" in lib.ak_last_error()
+    rc = f(*_scan_fwd_args(batch=2))                      # real shape: null pointers
+    assert rc == -1 and b"null" in lib.ak_last_error()
+    ws = lib.ak_selective_scan_bwd_workspace_bytes
+    var, kb = ws(4, 2048, 4096, 64, 1, 0), ws(4, 2048, 4096, 64, 1, 1)
+    # a constant B drops its [tiles, batch, groups, dstate, seqlen] partial rows
+    # and keeps a [batch, dim, dstate] one instead
+    tiles = 2048 // 16
+    assert var - kb == tiles * 4 * 64 * 4096 * 4 - 4 * 2048 * 64 * 4

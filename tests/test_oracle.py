@@ -369,6 +369,78 @@ def test_c_oracle_matches_torch_oracle():
         assert torch.allclose(lc, last, rtol=1e-5, atol=1e-6)
 
 
+def _scan_brute(u, delta, A, Bfn, Cfn, D=None, z=None, bias=None, softplus=False):
+    """Scalar float64 loops over (b, d, l, n): h = exp(delta' A) h + delta' u B;
+    y = sum_n h C + D u; out = y silu(z). Bfn / Cfn(b, d, n, l) give the B / C
+    entry that channel d sees at step l (any layout)."""
+    bsz, dim, L = u.shape
+    N = A.shape[1]
+    out = torch.zeros(bsz, dim, L, dtype=torch.float64)
+    last = torch.zeros(bsz, dim, N, dtype=torch.float64)
+    for b in range(bsz):
+        for d in range(dim):
+            h = [0.0] * N
+            for l in range(L):
+                x = float(delta[b, d, l]) + (float(bias[d]) if bias is not None else 0.0)
+                if softplus:
+                    x = x if x > 20 else math.log1p(math.exp(x))
+                y = 0.0
+                for n in range(N):
+                    h[n] = math.exp(x * float(A[d, n])) * h[n] + x * float(u[b, d, l]) * Bfn(b, d, n, l)
+                    y += h[n] * Cfn(b, d, n, l)
+                if D is not None:
+                    y += float(D[d]) * float(u[b, d, l])
+                if z is not None:
+                    zz = float(z[b, d, l])
+                    y *= zz / (1 + math.exp(-zz))
+                out[b, d, l] = y
+            last[b, d] = torch.tensor(h, dtype=torch.float64)
+    return out, last
+
+
+@pytest.mark.parametrize("layout", ["const_B", "const_C", "const_BC", "wide_var"])
+def test_selective_scan_input_independent_bc_and_wide_state_brute_force(layout):
+    """Input-independent B / C ([dim, n], selective_scan_interface.py:151-152,
+    :168-169) and dstate 20 (past 16) against scalar float64 loops."""
+    n = 20 if layout == "wide_var" else 6
+    u, delta, A, B, C, D, z, bias = _scan_inputs(b=2, d=3, l=11, n=n, seed=61)
+    gen = torch.Generator().manual_seed(62)
+    B2, C2 = torch.randn(3, n, generator=gen), torch.randn(3, n, generator=gen)
+    Bv = lambda b, d, k, l: float(B[b, 0, k, l])
+    Cv = lambda b, d, k, l: float(C[b, 0, k, l])
+    Bk = lambda b, d, k, l: float(B2[d, k])
+    Ck = lambda b, d, k, l: float(C2[d, k])
+    Bt, Bf = (B2, Bk) if layout in ("const_B", "const_BC") else (B[:, 0], Bv)
+    Ct, Cf = (C2, Ck) if layout in ("const_C", "const_BC") else (C[:, 0], Cv)
+    out, last = ops.selective_scan_ref(u, delta, A, Bt, Ct, D, z, bias, True, return_last_state=True)
+    ref, rlast = _scan_brute(u, delta, A, Bf, Cf, D, z, bias, True)
+    assert torch.allclose(out.double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(last.double(), rlast, rtol=1e-5, atol=1e-5)
+    c_out, c_last = c_oracle.selective_scan(u, delta, A, Bt, Ct, D, z, bias, True)
+    assert torch.allclose(c_out.double(), ref, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(c_last.double(), rlast, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("const_b,const_c", [(True, False), (False, True), (True, True)])
+def test_selective_scan_bwd_input_independent_bc_matches_autograd(const_b, const_c):
+    """dB / dC of an input-independent B / C (summed over batch and steps) and
+    every other gradient, against torch autograd of the float64 forward, with a
+    grouped input-dependent partner (2 groups) and dstate 18."""
+    u, delta, A, B, C, D, z, bias = _scan_inputs(d=4, l=23, n=18, g=2, seed=71)
+    gen = torch.Generator().manual_seed(72)
+    Bt = torch.randn(4, 18, generator=gen) if const_b else B
+    Ct = torch.randn(4, 18, generator=gen) if const_c else C
+    dout = torch.randn(u.shape, generator=gen)
+    leaves = [t.double().requires_grad_() for t in (u, delta, A, Bt, Ct, D, z, bias)]
+    out = ops.selective_scan_ref(*leaves[:5], D=leaves[5], z=leaves[6], delta_bias=leaves[7],
+                                 delta_softplus=True, compute_dtype=torch.float64)
+    out.backward(dout.double())
+    ref = ops.selective_scan_bwd_ref(u, delta, A, Bt, Ct, dout, D, z, bias, True)
+    for name, r, leaf in zip("du ddelta dA dB dC dD dz dbias".split(), ref, leaves):
+        assert r.shape == leaf.grad.shape, name
+        assert torch.allclose(r, leaf.grad, rtol=1e-10, atol=1e-12), name
+
+
 def test_silu_dtype_choice_is_rounding_only():
     u, delta, A, B, C, D, z, bias = _scan_inputs()
     zb = z.bfloat16()
