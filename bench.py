@@ -1,14 +1,16 @@
 """Benchmark of the gfx950 kernel set on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1,c2,...] [--no-cpu]
+    python bench.py --harness [KERNEL_TYPE] [--quick]
 
-Prints ONE JSON line. The headline (``value``) is the HBM throughput of the
+Prints ONE JSON line (the second form runs the staged correctness and timing
+harness of harness.py for one kernel type and prints its report instead). The headline (``value``) is the HBM throughput of the
 configuration the benchmark's metric is quoted on at one GPU: the
 causal-masked fp16 row softmax [8, 12, 1024, 1024] (C2). A "step" is one
 launch of that kernel over one batch of synthetic input already resident in
 HBM; ``value`` = algorithmic bytes x K / wall-clock time of the K timed steps.
-``roofline`` gives the kernel's achieved bandwidth from HIP-event kernel
-durations against MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle on
+``roofline`` gives the kernel's achieved bandwidth from the median of at
+least 100 per-launch HIP event pairs against MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle on
 the GPU box's host on a bounded sample of the same workload. ``kernels``
 reports every configuration (C1..C5) the same way: time per launch, GB/s or
 TFLOP/s, roofline fraction, tokens/s and the CPU figure beside it.
@@ -122,6 +124,9 @@ C4_MIN_BYTES = 8192 * 768 * 2 + 50304 * 768 * 2 + 8192 * 8 + 8192 * 4 + 4
 # grad_weight GEMMs: three products of 2 N V D flop each
 C4B_FLOP = 3 * C4_FLOP
 C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2 + 2048 * 16 * 4 + 2048 * 4
+# the reference's N=64 mamba-ssm shape: u, delta, out fp16 [8, 384, 512];
+# B, C fp16 [8, 64, 512]; A [384, 64] and D fp32
+N64_BYTES = 3 * 8 * 384 * 512 * 2 + 2 * 8 * 64 * 512 * 2 + 384 * 64 * 4 + 384 * 4
 # Mamba-1 backward at the C5 shape: read u, z, dout (bf16), delta (fp32), B, C,
 # A, D; write du, dz (bf16), ddelta (fp32), dB, dC (bf16), dA, dD (fp32)
 C5B_BYTES = (4 * 2048 * 4096 * (2 + 2 + 2 + 4 + 2 + 2 + 4) + 4 * 4 * 16 * 4096 * 2
@@ -147,9 +152,28 @@ def _replicate(tensors, k):
 class Case:
     """One configuration: device state, one launch per step, algorithmic work."""
 
-    def __init__(self, name, workload, bound, work, unit_tokens, launch, sets, kernel_name):
+    def __init__(self, name, workload, bound, work, unit_tokens, launch, sets, kernel_name,
+                 valu_cycles=None, valu_model=None):
         self.name, self.workload, self.bound, self.work = name, workload, bound, work
         self.tokens, self.launch, self.sets, self.kernel_name = unit_tokens, launch, sets, kernel_name
+        # VALU issue cycles of the whole launch (wave64 instructions x their
+        # issue cost per SIMD), for kernels whose floor is instruction issue
+        self.valu_cycles, self.valu_model = valu_cycles, valu_model
+
+
+# gfx950 issue cost per wave64 instruction and SIMD, measured with a
+# throughput probe on the box (8 independent chains per lane, 8 waves per SIMD)
+CYC_DPP_MUL, CYC_EXP, CYC_FMA = 4.7, 9.8, 3.0
+# The scan's work per (step, state) and lane: 2 DPP-broadcast multiplies
+# (decay exponent, delta u B), 1 exp2, the state FMA and the output FMA.
+SCAN_CYC_PER_STATE_STEP = 2 * CYC_DPP_MUL + CYC_EXP + 2 * CYC_FMA
+SCAN_VALU_MODEL = ("per (step, state) and wave64: 2 v_mul_f32_dpp (4.7 cyc) + v_exp_f32 (9.8) "
+                   "+ 2 v_fmac_f32 (3.0), 64 (channel, state) lanes per wave, 1024 SIMDs at 2.4 GHz")
+
+
+def scan_valu_cycles(batch, dim, dstate, seqlen):
+    waves = batch * dim * max(16, dstate) / 64
+    return waves * seqlen * SCAN_CYC_PER_STATE_STEP
 
 
 def make_case(name):
@@ -246,7 +270,25 @@ def make_case(name):
         launch = lambda s: _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"],
                                                s["z"], None, s["out"], None, False)
         return Case(name, "C5 Mamba-1 selective scan B4 L4096 D2048 N16", "hbm", C5_BYTES, 4 * 4096,
-                    launch, sets, "mamba_scan_fast_kernel")
+                    launch, sets, "mamba_scan_fast_kernel",
+                    valu_cycles=scan_valu_cycles(4, 2048, 16, 4096), valu_model=SCAN_VALU_MODEL)
+    if name == "n64":
+        # the reference's own mamba-ssm benchmark shape (scripts/bench_external_kernels.py:140)
+        g = torch.Generator().manual_seed(0)
+        cpu = {"u": torch.randn(8, 384, 512, generator=g).half(),
+               "delta": torch.randn(8, 384, 512, generator=g).half(),
+               "A": -torch.rand(384, 64, generator=g),
+               "B": torch.randn(8, 1, 64, 512, generator=g).half(),
+               "C": torch.randn(8, 1, 64, 512, generator=g).half(),
+               "D": torch.randn(384, generator=g)}
+        sets = _replicate(cpu, _sets(N64_BYTES))
+        for s in sets:
+            s["out"] = torch.empty_like(s["u"])
+        launch = lambda s: _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"],
+                                               None, None, s["out"], None, True)
+        return Case(name, "Mamba-1 scan at the reference's benchmark shape B8 D384 L512 N64 fp16",
+                    "hbm", N64_BYTES, 8 * 512, launch, sets, "mamba_scan_wide_fwd_kernel",
+                    valu_cycles=scan_valu_cycles(8, 384, 64, 512), valu_model=SCAN_VALU_MODEL)
     if name == "c5b":
         cpu = gen_c5()
         cpu["dout"] = torch.randn(cpu["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
@@ -293,14 +335,19 @@ def make_case(name):
     raise ValueError(name)
 
 
-def time_case(case, steps, warmup):
+# Launches timed one by one (an event pair each) for the roofline figures,
+# whatever --steps is.
+ROOFLINE_PAIRS = 100
+
+
+def time_case(case, steps, warmup, pairs=ROOFLINE_PAIRS):
     """W untimed steps, then K timed steps bracketed by synchronisations.
 
     Returns (wall seconds of the K steps, mean ms per launch from one HIP
     event pair around the K back-to-back launches on the launch stream,
-    median ms per launch from a second pass with an event pair around each
-    launch; those pairs add the event overhead to each launch, which shows
-    for launches of a few microseconds)."""
+    median ms per launch over ``pairs`` (>= 100) launches each bracketed by
+    its own event pair; those pairs add the event overhead to each launch,
+    which shows for launches of a few microseconds)."""
     nset = len(case.sets)
     for i in range(warmup):
         case.launch(case.sets[i % nset])
@@ -315,9 +362,10 @@ def time_case(case, steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     mean_ms = ev0.elapsed_time(ev1) / steps
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for i in range(steps):
+    n = max(pairs, ROOFLINE_PAIRS)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for i in range(n):
         starts[i].record()
         case.launch(case.sets[i % nset])
         ends[i].record()
@@ -413,22 +461,57 @@ def cpu_baseline(name, budget_s=4.0):
                                                       c["D"], c["z"])), 2)
         return ((32 * 4096) / t / 2048 / 1e6, "Mtok/s",
                 "batch 1, 32 of 2048 channels, full L=4096 (forward oracle + float64 backward oracle)")
+    if name == "n64":
+        g = torch.Generator().manual_seed(0)
+        u = torch.randn(1, 48, 512, generator=g).half()
+        delta = torch.randn(1, 48, 512, generator=g).half()
+        A = -torch.rand(48, 64, generator=g)
+        B = torch.randn(1, 64, 512, generator=g).half()
+        C = torch.randn(1, 64, 512, generator=g).half()
+        D = torch.randn(48, generator=g)
+        t = timed(lambda: ops.selective_scan_ref(u, delta, A, B, C, D, None, None, True), 3)
+        return (48 * 512) / t / 384 / 1e6, "Mtok/s", "batch 1, 48 of 384 channels, full L=512"
     raise ValueError(name)
 
 
 # ---------------------------------------------------------------------------
+
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b,c5t")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b,c5t,n64")
+    ap.add_argument("--harness", nargs="?", const="", default=None, metavar="KERNEL_TYPE",
+                    help="run the staged correctness + timing harness for one kernel type "
+                         "(softmax, cross_entropy, rmsnorm, fused_residual_add_rmsnorm, "
+                         "selective_scan; default: kernel.py's) instead of the JSON benchmark")
+    ap.add_argument("--quick", action="store_true", help="harness: skip stages 3-5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run 3 device copies of 256 MiB (a known-size kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args(argv)
+    if args.harness is not None:
+        if not torch.cuda.is_available():
+            print("the harness needs a GPU", file=sys.stderr)
+            return 2
+        import harness
+        hargs = (["--kernel", args.harness] if args.harness else []) + (["--quick"] if args.quick else [])
+        out = harness.main(hargs)
+        return 0 if out["correctness"]["correctness"] == "PASS" else 1
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
@@ -451,28 +534,37 @@ def main(argv=None):
     head = None
     for name in names:
         case = make_case(name)
-        wall, mean_ms, med_ms = time_case(case, args.steps, args.warmup)
+        wall, mean_ms, med_ms = time_case(case, args.steps, args.warmup, args.steps)
+        # rooflines from the median of the per-launch event pairs
         if case.bound == "hbm":
-            achieved = case.work / (mean_ms * 1e-3) / 1e9
+            achieved = case.work / (med_ms * 1e-3) / 1e9
             peak, unit = HBM_PEAK_GBS, "GB/s"
         else:
-            achieved = case.work / (mean_ms * 1e-3) / 1e12
+            achieved = case.work / (med_ms * 1e-3) / 1e12
             peak, unit = BF16_PEAK_TFLOPS, "TFLOP/s"
         rec = {
             "workload": case.workload,
             "kernel": case.kernel_name,
-            "us_per_launch_mean": round(mean_ms * 1e3, 2),
             "us_per_launch_median_event_pairs": round(med_ms * 1e3, 2),
+            "event_pairs": max(ROOFLINE_PAIRS, args.steps),
+            "us_per_launch_mean": round(mean_ms * 1e3, 2),
             "achieved": round(achieved, 1),
             "unit": unit,
             "peak": peak,
             "frac": round(achieved / peak, 4),
-            "tokens_per_s": round(case.tokens / (mean_ms * 1e-3), 1),
+            "tokens_per_s": round(case.tokens / (med_ms * 1e-3), 1),
             "input_sets": len(case.sets),
             "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
         }
-        if name in ("c5", "c5b", "c5t"):
-            rec["Mtok_per_s"] = round(case.tokens / (mean_ms * 1e-3) / 1e6, 2)
+        if case.valu_cycles:
+            # the VALU issue floor: instruction cycles per wave64 and SIMD over
+            # MI355X's 1024 SIMDs at the 2.4 GHz peak clock
+            floor_us = case.valu_cycles / 1024 / 2.4e3
+            rec["valu_roofline"] = {"floor_us": round(floor_us, 1),
+                                    "frac": round(floor_us / (med_ms * 1e3), 4),
+                                    "model": case.valu_model}
+        if name.startswith("c5") or name == "n64":
+            rec["Mtok_per_s"] = round(case.tokens / (med_ms * 1e-3) / 1e6, 2)
         if not args.no_cpu:
             rate, cunit, sample = cpu_baseline(name)
             rec["cpu"] = {"value": round(rate, 4), "unit": cunit, "sample": sample}
@@ -503,12 +595,17 @@ def main(argv=None):
         "config": {"workload": case.workload, "rows": 98304, "cols": 1024, "mask": "causal -inf",
                    "accumulate": "fp32", "input_sets_rotated": len(case.sets)},
         "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": h["frac"], "traffic": measured_traffic("softmax_vec_kernel")},
+                     "frac": h["frac"], "traffic": measured_traffic("softmax_vec_kernel"),
+                     "achieved_from": f"median of {h['event_pairs']} per-launch HIP event pairs",
+                     "traffic_from": "profiles/hbm_traffic_pmc.md: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                     "per dispatch, scaled by a 256 MiB copy's readings"},
         "cpu_baseline": None,
         "kernels": kernels,
         "host": {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
-                 "cpu": platform.processor() or platform.machine(), "torch": torch.__version__,
-                 "gpu": torch.cuda.get_device_name(0)},
+                 "cpu": cpu_model(), "torch": torch.__version__,
+                 "gpu": torch.cuda.get_device_name(0),
+                 "gpu_arch": getattr(torch.cuda.get_device_properties(0), "gcnArchName", "unknown"),
+                 "gpu_cus": torch.cuda.get_device_properties(0).multi_processor_count},
     }
     if "cpu" in h:
         line["cpu_baseline"] = {"value": h["cpu"]["value"], "unit": "GB/s",

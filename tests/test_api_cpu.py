@@ -471,3 +471,116 @@ def test_rmsnorm_replacement_takes_the_modules_own_eps(fake_backend):
     assert _norm_eps(nn.Module()) == 1e-6
     assert _norm_eps(nn.RMSNorm(8, eps=3e-5)) == 3e-5
     assert _norm_eps(nn.RMSNorm(8)) == torch.finfo(torch.float32).eps
+
+
+def test_harness_configs_and_compare():
+    """The harness's KERNEL_CONFIGS cover the kernel set with the reference's
+    entry fields; its comparison treats matching NaN / Inf as equal and
+    reports the first mismatch."""
+    import harness
+    for k in ("softmax", "cross_entropy", "rmsnorm", "fused_residual_add_rmsnorm", "selective_scan"):
+        spec = harness.KERNEL_CONFIGS[k]
+        assert spec.kernel_type == k and spec.test_sizes and spec.edge_sizes and spec.test_dtypes
+        assert all(dt in spec.tolerances for dt in spec.test_dtypes)
+        lbl, size = spec.test_sizes[0]
+        assert spec.flops_fn(size) > 0 and spec.bytes_fn(size, spec.test_dtypes[0]) > 0
+    assert "matmul" not in harness.KERNEL_CONFIGS
+    a = torch.tensor([1.0, float("nan"), float("inf"), 2.0])
+    b = torch.tensor([1.0 + 1e-7, float("nan"), float("inf"), 2.0])
+    assert harness.compare(a, b, 1e-6, 0.0)["match"]
+    c = harness.compare(a, torch.tensor([1.0, float("nan"), float("inf"), 2.1]), 1e-3, 1e-3)
+    assert not c["match"] and "max_abs_error" in c["reason"]
+    assert not harness.compare(a, a[:3], 1.0, 1.0)["match"]
+    # the eager references follow reference.py with fp32 arithmetic
+    x = torch.randn(4, 33).half()
+    assert torch.allclose(harness._softmax_ref({"x": x}).float(), torch.softmax(x.float(), -1), atol=1e-3)
+    w = torch.randn(33).half()
+    r = harness._fused_ref({"x": x, "residual": x, "weight": w})
+    assert torch.equal(r, ops.fused_residual_add_rmsnorm_ref(x, x, w, 1e-6)[1])
+
+
+def test_harness_stages_run_on_the_fake_backend(fake_backend, monkeypatch):
+    """The five correctness stages and their verdicts, driven on the CPU
+    through the oracle-backed launchers (device 'cpu'); a planted error in the
+    kernel makes the sweep fail."""
+    import harness
+    from kernels.hip import rmsnorm
+    spec = harness.KernelSpec(
+        "rmsnorm", [("tiny", {"M": 8, "N": 64}), ("small", {"M": 16, "N": 96})], [torch.float32],
+        {torch.float32: {"atol": 1e-5, "rtol": 1e-5}}, harness._rms_inputs, harness._rms_ref,
+        rmsnorm.kernel_fn, lambda s: 6 * s["M"] * s["N"], lambda s, dt: 8 * s["M"] * s["N"],
+        [("edge_7", {"M": 7, "N": 7})])
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a: None)
+    res = harness.run_correctness(spec, device="cpu", log=lambda *a: None)
+    assert res["correctness"] == "PASS", res
+    assert all(res[k].startswith("PASS") for k in ("smoke_test", "shape_sweep", "numerical_stability",
+                                                   "determinism", "edge_cases"))
+    bad = harness.KernelSpec(**{**spec.__dict__, "kernel_fn": lambda x, weight: rmsnorm.kernel_fn(x, weight) * 1.01})
+    res = harness.run_correctness(bad, device="cpu", log=lambda *a: None)
+    assert res["correctness"] == "FAIL" and res["smoke_test"] == "FAIL"
+
+
+def test_optimized_model_context_swaps_and_restores(fake_backend):
+    """verify.OptimizedModelContext: RMSNorm modules and pre-norm blocks are
+    replaced inside the context (outputs within tolerance of the original
+    model) and every original module object is back afterwards, in either
+    replacement order."""
+    import torch.nn as nn
+    import verify
+
+    class Norm(nn.Module):
+        def __init__(self, d):
+            super().__init__()
+            self.weight = nn.Parameter(1 + 0.1 * torch.randn(d))
+            self.eps = 1e-5
+
+        def forward(self, x):
+            return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight
+
+    class Block(nn.Module):
+        def __init__(self, d):
+            super().__init__()
+            self.attention = lambda x, f: x * 0.5  # stand-in mixer
+            self.attention_norm = Norm(d)
+            self.feed_forward = nn.Linear(d, d)
+            self.ffn_norm = Norm(d)
+
+        def forward(self, x, freqs_cis):
+            h = x + self.attention(self.attention_norm(x), freqs_cis)
+            return h + self.feed_forward(self.ffn_norm(h))
+
+    class Model(nn.Module):
+        def __init__(self, d=32):
+            super().__init__()
+            self.layers = nn.ModuleList([Block(d), Block(d)])
+            self.norm = Norm(d)
+
+        def forward(self, x):
+            for l in self.layers:
+                x = l(x, None)
+            return self.norm(x)
+
+    torch.manual_seed(0)
+    m = Model()
+    x = torch.randn(2, 5, 32)
+    before = {n: mod for n, mod in m.named_modules()}
+    ref = m(x)
+    for order in ((0, 1), (1, 0)):
+        reps = [verify.KernelReplacement("fused_residual_add_rmsnorm", rank=order[0]),
+                verify.KernelReplacement("rmsnorm", rank=order[1]),
+                verify.KernelReplacement("rotary_embedding", rank=2)]
+        ctx = verify.OptimizedModelContext(m, reps)
+        with ctx as mm:
+            out = mm(x)
+            kinds = {type(mod).__name__ for mod in mm.modules()}
+            assert "_FusedResidualRMSNormBlockReplacement" in kinds and "_RMSNormReplacement" in kinds
+        assert any("rotary_embedding" in n for n in ctx.notes)
+        assert torch.allclose(out, ref, rtol=1e-4, atol=1e-5)
+        after = {n: mod for n, mod in m.named_modules()}
+        assert after.keys() == before.keys() and all(after[k] is before[k] for k in before)
+    res = verify.verify_model.__doc__
+    assert res
+    cmp = verify.compare_outputs(ref, ref + 1e-6, torch.float32)
+    assert cmp["correctness"] == "PASS"
+    bad = verify.compare_outputs(ref, ref.clone().fill_(float("nan")), torch.float32)
+    assert bad["correctness"] == "FAIL" and "NaN" in bad["reason"]
