@@ -339,9 +339,19 @@ __device__ __forceinline__ void bstore1(Rsrc r, uint32_t voff, float v) {
 }
 
 // kPrep: the backward's preparation pass (as in mamba_scan_fwd_kernel).
-template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false>
+// kLean (forward only): a gate z and none of out_prez, checkpoints or chunk
+// states, all known at compile time. The runtime tests of those pointers split
+// the tile loop into basic blocks that the scheduler cannot interleave across
+// (about 8% of the kernel at the C5 shape).
+template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false,
+          bool kLean = false>
 __global__ void __launch_bounds__(256)
 mamba_scan_fast_kernel(ScanParams p) {
+  static_assert(!(kPrep && kLean), "the lean variant is a forward");
+  const bool has_z = kLean || p.z != nullptr;
+  const bool has_prez = !kLean && !kPrep && p.out_prez != nullptr;
+  float* const ck_out = kLean ? nullptr : p.ck;
+  float* const xs_out = kLean ? nullptr : p.chunk_states;
   __shared__ float Bs[2][16 * kBStride];
   __shared__ float Cs[2][kScanT * kCStride];
   __shared__ float hbuf[4][4 * kHC];
@@ -374,11 +384,11 @@ mamba_scan_fast_kernel(ScanParams p) {
   };
   const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
   const Rsrc rs_d = row_rsrc(p.delta, p.d_bs, p.d_ds, sizeof(TD));
-  const Rsrc rs_z = p.z ? row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU)) : rs_u;
-  const int64_t zds = p.z ? p.z_ds : p.u_ds;
+  const Rsrc rs_z = has_z ? row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU)) : rs_u;
+  const int64_t zds = has_z ? p.z_ds : p.u_ds;
   // the forward's output, or the preparation pass's dz (with a gate)
   const Rsrc rs_o = row_rsrc(kPrep ? p.dz : p.out, p.o_bs, p.o_ds, sizeof(TU));
-  const Rsrc rs_oz = (!kPrep && p.out_prez) ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
+  const Rsrc rs_oz = has_prez ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
   const Rsrc rs_go = kPrep ? row_rsrc(p.dout, p.go_bs, p.go_ds, sizeof(TU)) : rs_u;
   const uint32_t vo_go1 = kPrep ? (uint32_t)(wc * p.go_ds + n) * sizeof(TU) : 0u;
   const uint32_t bc_bytes_B = (uint32_t)(((p.dstate - 1) * p.B_ns + L) * sizeof(TBC));
@@ -447,13 +457,13 @@ mamba_scan_fast_kernel(ScanParams p) {
     for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
     float o = fmaf(dskip, p_uo, (y4[0] + y4[1]) + (y4[2] + y4[3]));
     if constexpr (kPrep) {
-      if (p.z) {
+      if (has_z) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p_zo * kLog2e));
         bstore1<TU>(rs_o, p_off, p_go * o * sg * fmaf(p_zo, 1.0f - sg, 1.0f));
       }
     } else {
-      if (p.out_prez) bstore1<TU>(rs_oz, p_off, o);
-      if (p.z) o *= silu_fast(p_zo);
+      if (has_prez) bstore1<TU>(rs_oz, p_off, o);
+      if (has_z) o *= silu_fast(p_zo);
       bstore1<TU>(rs_o, p_off, o);
     }
   };
@@ -479,9 +489,9 @@ mamba_scan_fast_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
-      if (kPrep || p.ck) {
+      if (kPrep || ck_out) {
         if (n_ok)
-          p.ck[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
+          ck_out[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
       }
       float hv[16], av[16], xv[16];
       auto steps4 = [&](auto src_c, int j4) {
@@ -530,16 +540,16 @@ mamba_scan_fast_kernel(ScanParams p) {
       }
       __builtin_amdgcn_wave_barrier();
       p_uo = raw_f32<TU>(cur.uo[blk]);
-      p_zo = p.z ? raw_f32<TU>(cur.zo[blk]) : 0.0f;
+      p_zo = has_z ? raw_f32<TU>(cur.zo[blk]) : 0.0f;
       if constexpr (kPrep) p_go = raw_f32<TU>(cur.go[blk]);
       p_off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
       pending = true;
     }
-    if (!kPrep && p.chunk_states) {
+    if (!kPrep && xs_out) {
       dsum += row16_sum((dl[0] + dl[1]) + (dl[2] + dl[3]));
       const int l1 = (t + 1) * kScanT;
       if ((l1 % kXChunk == 0 || l1 >= p.seqlen) && n_ok) {
-        float* xs = p.chunk_states +
+        float* xs = xs_out +
                     ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + n) * 2;
         xs[0] = __builtin_amdgcn_exp2f(a_scaled * dsum);
         xs[1] = h;
@@ -1107,7 +1117,12 @@ bool scan_fast_ok(const ScanParams& p, bool prep = false) {
 template <typename TU, typename TD, typename TBC>
 void launch_scan(const ScanParams& p, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
-  if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
+  const bool lean = p.z && !p.out_prez && !p.ck && !p.chunk_states;
+  if (scan_fast_ok<TU, TD, TBC>(p) && lean && p.softplus)
+    mamba_scan_fast_kernel<TU, TD, TBC, true, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p) && lean)
+    mamba_scan_fast_kernel<TU, TD, TBC, false, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
     mamba_scan_fast_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p))
     mamba_scan_fast_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
