@@ -26,7 +26,7 @@
 // 2048-step chunk, the running prefix (decay product, state) of every state
 // (the reference binding's chunk-state tensor x). The backward's design is
 // described above mamba_scan_bwd_kernel.
-#include "scan_common.h"
+#include "scan_buffer.h"
 
 namespace ak {
 namespace {
@@ -279,79 +279,25 @@ mamba_scan_fwd_kernel(ScanParams p) {
 // * softplus chosen at compile time (as a run-time branch the compiler
 //   if-converts it and evaluates log1p(exp(x)) on every tile).
 // ---------------------------------------------------------------------------
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-
-// Raw bits of 4 consecutive elements of T.
-template <typename T>
-using Raw4 = std::conditional_t<sizeof(T) == 4, u32x4, u32x2>;
-// Raw bits of one element of T.
-template <typename T>
-using Raw1 = std::conditional_t<sizeof(T) == 4, uint32_t, uint16_t>;
-
-// Buffer resource over `bytes` bytes at `base` (raw, unswizzled; gfx9 data
-// format field as used for untyped buffer access).
-__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-template <typename T>
-__device__ __forceinline__ Raw4<T> bload4(Rsrc r, uint32_t voff, uint32_t soff) {
-  if constexpr (sizeof(T) == 4)
-    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-  else
-    return __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
-}
-
-template <typename T>
-__device__ __forceinline__ Raw1<T> bload1(Rsrc r, uint32_t voff, uint32_t soff) {
-  if constexpr (sizeof(T) == 4)
-    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
-  else
-    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
-}
-
-template <typename T>
-__device__ __forceinline__ float raw_f32(Raw1<T> v) {
-  return to_f32(__builtin_bit_cast(T, v));
-}
-
-// Element k (compile-time after unrolling) of a Raw4 as fp32.
-template <typename T>
-__device__ __forceinline__ float raw4_f32(const Raw4<T>& v, int k) {
-  if constexpr (sizeof(T) == 4) {
-    // the element goes through a scalar first: hipcc (ROCm 7.2) folds a
-    // __builtin_bit_cast of an ext_vector element to element 0 for every k
-    const uint32_t w = v[k];
-    return __builtin_bit_cast(float, w);
-  } else {
-    const uint32_t w = v[k >> 1];
-    return raw_f32<T>((uint16_t)((k & 1) ? (w >> 16) : (w & 0xFFFFu)));
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void bstore1(Rsrc r, uint32_t voff, float v) {
-  if constexpr (sizeof(T) == 4)
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)voff, 0, 0);
-  else
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, (int)voff, 0, 0);
-}
-
 // kPrep: the backward's preparation pass (as in mamba_scan_fwd_kernel).
-// kLean (forward only): a gate z and none of out_prez, checkpoints or chunk
-// states, all known at compile time. The runtime tests of those pointers split
-// the tile loop into basic blocks that the scheduler cannot interleave across
-// (about 8% of the kernel at the C5 shape).
+// kVar (forward only) fixes the optional outputs at compile time: kFwdAny
+// tests the pointers at run time; kFwdLean has a gate z and none of out_prez,
+// checkpoints or chunk states (inference); kFwdTrain has a gate, out_prez and
+// checkpoints but no chunk states (the training forward that keeps its
+// states). The run-time tests split the tile loop into basic blocks that the
+// scheduler cannot interleave across (about 8% of the kernel at the C5 shape).
+enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
+
 template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false,
-          bool kLean = false>
+          int kVar = kFwdAny>
 __global__ void __launch_bounds__(256)
 mamba_scan_fast_kernel(ScanParams p) {
-  static_assert(!(kPrep && kLean), "the lean variant is a forward");
-  const bool has_z = kLean || p.z != nullptr;
-  const bool has_prez = !kLean && !kPrep && p.out_prez != nullptr;
-  float* const ck_out = kLean ? nullptr : p.ck;
-  float* const xs_out = kLean ? nullptr : p.chunk_states;
+  static_assert(!(kPrep && kVar != kFwdAny), "the fixed variants are forwards");
+  const bool has_z = kVar != kFwdAny || p.z != nullptr;
+  const bool has_prez = kVar == kFwdTrain || (kVar == kFwdAny && !kPrep && p.out_prez != nullptr);
+  float* const ck_out = kVar == kFwdLean ? nullptr : p.ck;
+  const bool has_ck = kPrep || kVar == kFwdTrain || (kVar == kFwdAny && ck_out != nullptr);
+  float* const xs_out = kVar != kFwdAny ? nullptr : p.chunk_states;
   __shared__ float Bs[2][16 * kBStride];
   __shared__ float Cs[2][kScanT * kCStride];
   __shared__ float hbuf[4][4 * kHC];
@@ -489,7 +435,7 @@ mamba_scan_fast_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
-      if (kPrep || ck_out) {
+      if (has_ck) {
         if (n_ok)
           ck_out[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
       }
@@ -1118,10 +1064,15 @@ template <typename TU, typename TD, typename TBC>
 void launch_scan(const ScanParams& p, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
   const bool lean = p.z && !p.out_prez && !p.ck && !p.chunk_states;
+  const bool train = p.z && p.out_prez && p.ck && !p.chunk_states;
   if (scan_fast_ok<TU, TD, TBC>(p) && lean && p.softplus)
-    mamba_scan_fast_kernel<TU, TD, TBC, true, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdLean><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && lean)
-    mamba_scan_fast_kernel<TU, TD, TBC, false, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdLean><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p) && train && p.softplus)
+    mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdTrain><<<dim3(grid), dim3(256), 0, s>>>(p);
+  else if (scan_fast_ok<TU, TD, TBC>(p) && train)
+    mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdTrain><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
     mamba_scan_fast_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p))
@@ -1180,6 +1131,11 @@ int finish_for(int bc_dtype, const ScanParams& p, void* dB, void* dC, float* dA,
   return 0;
 }
 
+template <typename T>
+constexpr int dtype_code_of() {
+  return std::is_same_v<T, float> ? AK_DTYPE_F32 : (std::is_same_v<T, f16> ? AK_DTYPE_F16 : AK_DTYPE_BF16);
+}
+
 // With the forward's states (p.ck) and pre-gate output (p.out_prez) saved,
 // the preparation pass is skipped: the reverse pass restarts from the saved
 // states and computes dz itself.
@@ -1195,10 +1151,13 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
     else
       mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   }
-  if (p.softplus)
+  if (launch_scan_bwd_fast(p, dtype_code_of<TU>(), dtype_code_of<TD>(), dtype_code_of<TBC>(), s)) {
+    // whole tiles: the buffer-resource reverse pass (same arithmetic, same bits)
+  } else if (p.softplus) {
     mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
-  else
+  } else {
     mamba_scan_bwd_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+  }
   scan_bwd_finish<TBC>(p, dB, dC, dA, dD, dbias, s);
 }
 
