@@ -167,6 +167,11 @@ struct GradArgs {
   float cap;               // logit softcap (> 0 with kCap; the forward uses it too)
   float ls;                // label smoothing alpha (0 = off)
   float* zsum;             // forward with label smoothing: per-partial sums of the logits
+  // backward over a vocab range: the kernels see the weight rows [v0, v0 +
+  // vocab) as a vocab of their own; targets and a / vocab refer to the full
+  // vocabulary of vocab_total entries
+  int64_t v0;
+  int64_t vocab_total;
 };
 
 // Logit softcap z' = cap * tanh(z / cap), evaluated without cancellation
@@ -413,8 +418,8 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
         const float lse2 = ga.lse[tok_c] * kLog2e;
         const float cl2 = kCap ? ga.cap * kLog2e - lse2 : 0.0f;  // log2 of exp(cap - lse)
         const int64_t tg = ga.targets[tok_c];
-        const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= vocab) ? NAN : gs);
-        const float nls = -(ga.ls / (float)vocab) * st;  // label smoothing's uniform term
+        const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= ga.vocab_total) ? NAN : gs);
+        const float nls = -(ga.ls / (float)ga.vocab_total) * st;  // label smoothing's uniform term
         T* drow = dzp + (int64_t)tok_c * ga.ld_dz + v_first + wv * 128;
 #pragma unroll
         for (int vb = 0; vb < 4; ++vb) {
@@ -744,9 +749,11 @@ lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, G
   const int tok = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (tok >= n_rows) return;  // the whole wave
   const int64_t tg = ga.targets[tok];
-  if (tg == ga.ignore_index || tg < 0 || tg >= vocab) return;
+  if (tg == ga.ignore_index || tg < 0 || tg >= ga.vocab_total) return;
+  const int64_t tl = tg - ga.v0;  // the target's column in this range (W starts at row v0)
+  if (tl < 0 || tl >= vocab) return;
   const T* hp = H + (int64_t)tok * ldh;
-  const T* wp = W + tg * ldw;
+  const T* wp = W + tl * ldw;
   float acc = 0.0f;
   for (int c = lane; c < d / 8; c += 64) {
     const Vec16<T> a = load16<T>(hp + 8 * c);
@@ -763,12 +770,12 @@ lmhead_ce_grad_target_kernel(const T* __restrict__ H, const T* __restrict__ W, G
       const float q = cp.q(acc);
       const float r = __builtin_amdgcn_rcpf(q + 1.0f);
       const float p = __builtin_amdgcn_exp2f(fmaf(cp.nc, r, (ga.cap - ga.lse[tok]) * kLog2e));
-      g = (p - (1.0f - ga.ls) - ga.ls / (float)vocab) * gs * (4.0f * q * r * r);
+      g = (p - (1.0f - ga.ls) - ga.ls / (float)ga.vocab_total) * gs * (4.0f * q * r * r);
     } else {
       const float p = __builtin_amdgcn_exp2f((acc - ga.lse[tok]) * kLog2e);
-      g = (p - (1.0f - ga.ls) - ga.ls / (float)vocab) * gs;
+      g = (p - (1.0f - ga.ls) - ga.ls / (float)ga.vocab_total) * gs;
     }
-    static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tg] = from_f32<T>(g);
+    static_cast<T*>(ga.dz)[(int64_t)tok * ga.ld_dz + tl] = from_f32<T>(g);
   }
 }
 
@@ -834,6 +841,7 @@ void launch_lmhead(const void* h, const void* w, const int64_t* targets, float* 
   GradArgs ga{};
   ga.cap = cap;
   ga.ls = ls;
+  ga.vocab_total = vocab;
   ga.zsum = ls > 0.0f ? reinterpret_cast<float*>(base + L.zsum) : nullptr;
   if (cap > 0.0f && ls > 0.0f)
     launch_tiles_fwd<T, true, true>(hp, wp, part, n_rows, vocab, d, ldh, ldw, n_vt, n_tt, ga, gd, bd, s);
@@ -932,12 +940,14 @@ extern "C" int ak_lmhead_ce_fwd(const void* hidden, const void* weight, const in
   return ak_check_launch(name);
 }
 
-extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
-                                const float* lse, const float* grad_loss, const float* denom,
-                                void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
-                                int64_t d, int64_t ld_h, int64_t ld_w, int64_t ignore_index,
-                                float softcap, float label_smoothing, int dtype, void* stream) {
-  const char* name = "ak_lmhead_ce_bwd";
+extern "C" int ak_lmhead_ce_bwd_range(const void* hidden, const void* weight,
+                                      const int64_t* targets, const float* lse,
+                                      const float* grad_loss, const float* denom, void* grad_logits,
+                                      int64_t ld_gl, int64_t n_rows, int64_t vocab, int64_t v_begin,
+                                      int64_t v_count, int64_t d, int64_t ld_h, int64_t ld_w,
+                                      int64_t ignore_index, float softcap, float label_smoothing,
+                                      int dtype, void* stream) {
+  const char* name = "ak_lmhead_ce_bwd_range";
   if (!(softcap >= 0.0f) || softcap == INFINITY)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: softcap must be finite and >= 0", name);
   if (!(label_smoothing >= 0.0f && label_smoothing <= 1.0f))
@@ -947,6 +957,10 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
   if (n_rows <= 0 || vocab <= 0 || d <= 0)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape n_rows=%lld vocab=%lld d=%lld", name,
                         (long long)n_rows, (long long)vocab, (long long)d);
+  if (v_begin < 0 || v_count <= 0 || v_begin > vocab - v_count)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: vocab range [%lld, %lld + %lld) outside [0, %lld)",
+                        name, (long long)v_begin, (long long)v_begin, (long long)v_count,
+                        (long long)vocab);
   if (d % ak::kKB)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: d=%lld must be a multiple of %d", name,
                         (long long)d, ak::kKB);
@@ -955,22 +969,35 @@ extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const in
   if (ld_h < d || ld_w < d || ld_h % 8 || ld_w % 8 || ld_h >= (1 << 23) || ld_w >= (1 << 23))
     return ak_set_error(AK_ERR_INVALID_ARG,
                         "%s: row pitches must be >= d, multiples of 8 and < 2^23 elements", name);
-  if (ld_gl < vocab)
-    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grad_logits pitch must be >= vocab", name);
+  if (ld_gl < v_count)
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: grad_logits pitch must be >= the range's width", name);
   if (!hidden || !weight || !targets || !lse || !grad_loss || !denom || !grad_logits)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
   if (!ak::aligned16(hidden) || !ak::aligned16(weight) ||
       (reinterpret_cast<uintptr_t>(grad_logits) & 1u))
     return ak_set_error(AK_ERR_INVALID_ARG,
                         "%s: hidden and weight must be 16-byte aligned, grad_logits element-aligned", name);
-  const int64_t n_tiles = ((vocab + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
+  const int64_t n_tiles = ((v_count + ak::kTV - 1) / ak::kTV) * ((n_rows + ak::kTT - 1) / ak::kTT);
   if (n_tiles > 0x7FFFFFFF) return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many tiles", name);
   ak::GradArgs ga{lse, targets, grad_loss, denom, grad_logits, ld_gl, ignore_index, softcap,
-                  label_smoothing, nullptr};
+                  label_smoothing, nullptr, v_begin, vocab};
   hipStream_t s = ak_stream(stream);
+  // the range's weight rows start at v_begin (16-byte aligned: ld_w is a multiple of 8)
+  const void* wr = static_cast<const char*>(weight) + (size_t)v_begin * (size_t)ld_w * 2;
   if (dtype == AK_DTYPE_BF16)
-    ak::launch_lmhead_bwd<ak::bf16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);
+    ak::launch_lmhead_bwd<ak::bf16>(hidden, wr, ga, (int)n_rows, (int)v_count, (int)d, ld_h, ld_w, s);
   else
-    ak::launch_lmhead_bwd<ak::f16>(hidden, weight, ga, (int)n_rows, (int)vocab, (int)d, ld_h, ld_w, s);
+    ak::launch_lmhead_bwd<ak::f16>(hidden, wr, ga, (int)n_rows, (int)v_count, (int)d, ld_h, ld_w, s);
   return ak_check_launch(name);
+}
+
+extern "C" int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targets,
+                                const float* lse, const float* grad_loss, const float* denom,
+                                void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
+                                int64_t d, int64_t ld_h, int64_t ld_w, int64_t ignore_index,
+                                float softcap, float label_smoothing, int dtype, void* stream) {
+  // the whole vocabulary as one range (errors name ak_lmhead_ce_bwd_range)
+  return ak_lmhead_ce_bwd_range(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ld_gl,
+                                n_rows, vocab, 0, vocab, d, ld_h, ld_w, ignore_index, softcap,
+                                label_smoothing, dtype, stream);
 }

@@ -68,6 +68,7 @@ _SIGNATURES = {
                          _c_void_p, ctypes.c_size_t, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
                          _int, _c_void_p],
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _f32, _int, _c_void_p],
+    "ak_lmhead_ce_bwd_range": [_c_void_p] * 7 + [_i64] * 9 + [_f32, _f32, _int, _c_void_p],
     "ak_selective_scan_fwd": [_c_void_p] * 13 + [_i64] * 5 + [_i64] * 15 + [_int] * 6 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
@@ -401,6 +402,25 @@ def lmhead_ce_bwd(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
             _rows_view(hidden, "hidden"), _rows_view(weight, "weight"), int(ignore_index),
             float(softcap), float(label_smoothing), dtype_code(hidden.dtype), _stream(hidden))
     _check(rc, "ak_lmhead_ce_bwd")
+
+
+def lmhead_ce_bwd_range(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
+                        lse: torch.Tensor, grad_loss: torch.Tensor, denom: torch.Tensor,
+                        grad_logits: torch.Tensor, v_begin: int, ignore_index: int,
+                        softcap: float = 0.0, label_smoothing: float = 0.0) -> None:
+    """:func:`lmhead_ce_bwd` for the vocab columns ``[v_begin, v_begin +
+    grad_logits.shape[1])`` of the full ``weight``'s vocabulary."""
+    require_device(hidden, weight, targets, lse, grad_loss, denom, grad_logits)
+    n_rows, d = hidden.shape
+    vocab = weight.shape[0]
+    with _on_device(hidden):
+        rc = load().ak_lmhead_ce_bwd_range(
+            _ptr(hidden), _ptr(weight), _ptr(targets), _ptr(lse), _ptr(grad_loss), _ptr(denom),
+            _ptr(grad_logits), _rows_view(grad_logits, "grad_logits"), n_rows, vocab,
+            int(v_begin), grad_logits.shape[1], d, _rows_view(hidden, "hidden"),
+            _rows_view(weight, "weight"), int(ignore_index), float(softcap),
+            float(label_smoothing), dtype_code(hidden.dtype), _stream(hidden))
+    _check(rc, "ak_lmhead_ce_bwd_range")
 
 
 # bc_flags of the selective-scan entry points: B / C input-independent ([dim, dstate] fp32)

@@ -29,11 +29,17 @@ upstream gradient over the counted rows, times ``1 - tanh^2`` under the
 softcap, less ``a / vocab`` under label smoothing) directly from registers in the
 input dtype; the device scalars stay on the device (no host sync). Then
 ``grad_hidden = dlogits @ W`` and ``grad_W = dlogits^T @ h`` are two plain
-GEMMs with fp32 accumulation (hipBLASLt via torch). Rows are processed in
-chunks whose ``dlogits`` block stays under ``GRAD_LOGITS_BUDGET`` bytes (one
-chunk at the C4 shape: 8192 x 50304 bf16 = 824 MB of the 288 GB of HBM), so
-``grad_W`` is normally one GEMM rounded once to the weight dtype; beyond the
-budget each chunk's product is rounded and the chunks are summed in fp32.
+GEMMs with fp32 accumulation (hipBLASLt via torch). The vocabulary is
+walked in ranges whose ``dlogits`` slice ``[n_rows, width]`` stays under
+``GRAD_LOGITS_BUDGET`` bytes (``ak_lmhead_ce_bwd_range``; the width a
+multiple of the tile kernel's 256 vocab rows). Each range's ``grad_W`` rows
+are one complete GEMM rounded once to the weight dtype; ``grad_hidden`` is
+summed over the ranges in an fp32 buffer (``addmm`` with fp32 output) and
+rounded once at the end. The default budget (4 GiB) keeps the C4 shape in one
+range (8192 x 50304 bf16 = 824 MB, 0.3% of the 288 GB of HBM): measured on
+MI355X, 16384-column ranges (268 MB) cost 2102 us against 1826 us, the fp32
+accumulation of grad_hidden over ranges being slower than one GEMM over the
+whole vocabulary. Lower the budget where memory matters more than time.
 Otherwise (fp32 or unaligned inputs) per row chunk
 the logits are recomputed with a GEMM and turned into ``dL/dlogits`` by the
 CE row kernel from the saved logsumexp, then ``grad_hidden = dlogits @ W``
@@ -89,8 +95,13 @@ def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch
     return loss, lse, n_valid
 
 
-# Largest dlogits block (bytes) the fused backward materialises at once.
+# Largest dlogits slice (bytes) the fused backward materialises at once.
 GRAD_LOGITS_BUDGET = 4 << 30
+# Row pitch padding of a range's slice (elements): keeps the pitch off powers
+# of two, whose rows would all start in the same memory channels.
+_RANGE_PAD = 64
+# Vocab ranges are whole multiples of the tile kernel's vocab tile.
+_VOCAB_TILE = 256
 
 
 def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
@@ -116,24 +127,33 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     g1 = grad_loss.reshape(1).to(torch.float32).contiguous()
     den1 = denom.reshape(1).to(torch.float32).contiguous()
     lse = lse.contiguous()
-    rows = max(1, min(n, GRAD_LOGITS_BUDGET // (vocab * hidden.element_size())))
-    grad_hidden = torch.empty_like(hidden) if need_hidden else None
-    grad_w32 = None
-    for start in range(0, n, rows):
-        end = min(start + rows, n)
-        # exactly [rows, vocab]: a padded pitch would leave uninitialised
-        # columns that a GEMM may read past K (0 * NaN)
-        g = torch.empty((end - start, vocab), dtype=hidden.dtype, device=hidden.device)
-        _lib.lmhead_ce_bwd(hidden[start:end], weight, targets[start:end], lse[start:end], g1, den1,
-                           g, ignore_index, softcap, label_smoothing)
-        if need_hidden:
-            torch.mm(g, weight, out=grad_hidden[start:end])
+    width = GRAD_LOGITS_BUDGET // (n * hidden.element_size())
+    width = max(_VOCAB_TILE, width - width % _VOCAB_TILE)
+    if width >= vocab:
+        # one range: exactly [n, vocab] (a padded pitch would leave
+        # uninitialised columns that a GEMM may read past K: 0 * NaN)
+        g = torch.empty((n, vocab), dtype=hidden.dtype, device=hidden.device)
+        _lib.lmhead_ce_bwd(hidden, weight, targets, lse, g1, den1, g, ignore_index, softcap,
+                           label_smoothing)
+        grad_hidden = torch.mm(g, weight) if need_hidden else None
+        grad_weight = torch.mm(g.t(), hidden) if need_weight else None
+        return grad_hidden, grad_weight
+    grad_weight = torch.empty_like(weight) if need_weight else None
+    grad_h32 = torch.zeros((n, d), dtype=torch.float32, device=hidden.device) if need_hidden else None
+    for v0 in range(0, vocab, width):
+        v1 = min(v0 + width, vocab)
+        # [n, v1 - v0] view of a padded buffer whose padding is zeroed (a GEMM
+        # kernel may load past K and multiply by zero: 0 * NaN would leak in)
+        gp = torch.empty((n, v1 - v0 + _RANGE_PAD), dtype=hidden.dtype, device=hidden.device)
+        gp[:, v1 - v0:].zero_()
+        g = gp[:, :v1 - v0]
+        _lib.lmhead_ce_bwd_range(hidden, weight, targets, lse, g1, den1, g, v0, ignore_index,
+                                 softcap, label_smoothing)
         if need_weight:
-            part = torch.mm(g.t(), hidden[start:end])
-            if start == 0 and end == n:
-                return grad_hidden, part
-            grad_w32 = part.float() if grad_w32 is None else grad_w32.add_(part.float())
-    grad_weight = grad_w32.to(weight.dtype) if need_weight else None
+            torch.mm(g.t(), hidden, out=grad_weight[v0:v1])
+        if need_hidden:
+            torch.addmm(grad_h32, g, weight[v0:v1], out_dtype=torch.float32, out=grad_h32)
+    grad_hidden = grad_h32.to(hidden.dtype) if need_hidden else None
     return grad_hidden, grad_weight
 
 

@@ -267,6 +267,26 @@ int ak_lmhead_ce_bwd(const void* hidden, const void* weight, const int64_t* targ
                      float softcap, float label_smoothing, int dtype, void* stream);
 
 /*
+ * ak_lmhead_ce_bwd over the vocab columns [v_begin, v_begin + v_count) of a
+ * vocab-entry problem: grad_logits holds v_count columns (ld_gl >= v_count),
+ * column j being vocab entry v_begin + j; weight is the full [vocab, d]
+ * matrix. Targets, the NaN rule for targets outside [0, vocab) and label
+ * smoothing's a / vocab refer to the full vocabulary. A caller walks the
+ * vocabulary in ranges so that only a [n_rows, v_count] slice of the
+ * gradient exists at a time; each range's grad_weight rows are then a
+ * complete GEMM and grad_hidden a sum over ranges. Same reference interface
+ * as ak_lmhead_ce_bwd (kernels/hip/chunked_linear_cross_entropy.py:97-132,
+ * which bounds the materialised gradient by chunking rows); ak_lmhead_ce_bwd
+ * is this entry point with the range [0, vocab).
+ */
+int ak_lmhead_ce_bwd_range(const void* hidden, const void* weight, const int64_t* targets,
+                           const float* lse, const float* grad_loss, const float* denom,
+                           void* grad_logits, int64_t ld_gl, int64_t n_rows, int64_t vocab,
+                           int64_t v_begin, int64_t v_count, int64_t d, int64_t ld_h,
+                           int64_t ld_w, int64_t ignore_index, float softcap,
+                           float label_smoothing, int dtype, void* stream);
+
+/*
  * Mamba-1 selective scan forward (selective_scan_fn semantics).
  * Replaces selective_scan_cuda.fwd, external/mamba/csrc/selective_scan/
  * selective_scan.cpp:227-335, as called by

@@ -138,6 +138,14 @@ def _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, grad_logits, ign
     grad_logits[:, :V].copy_(g)
 
 
+def _lmhead_bwd_range(hidden, weight, targets, lse, grad_loss, denom, grad_logits, v_begin,
+                      ignore_index, softcap=0.0, label_smoothing=0.0):
+    full = torch.empty((hidden.shape[0], weight.shape[0]), dtype=grad_logits.dtype)
+    _lmhead_bwd(hidden, weight, targets, lse, grad_loss, denom, full, ignore_index, softcap,
+                label_smoothing)
+    grad_logits.copy_(full[:, v_begin:v_begin + grad_logits.shape[1]])
+
+
 def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, out_prez=None,
           chunk_states=None, checkpoints=None):
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
@@ -187,6 +195,7 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "lmhead_ce", _lmhead)
     monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
     monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)
+    monkeypatch.setattr(_lib, "lmhead_ce_bwd_range", _lmhead_bwd_range)
     monkeypatch.setattr(_lib, "selective_scan", _scan)
     monkeypatch.setattr(_lib, "selective_scan_bwd", _scan_bwd)
     monkeypatch.setattr(_lib, "diag_scan", _diag)

@@ -70,6 +70,13 @@ def test_argument_errors_return_codes(lib):
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
         rc = lib.ak_lmhead_ce_bwd(*([None] * 7), 16, 8, 16, 64, 64, 64, -100, 0.0, ls, 2, None)
         assert rc == -1 and b"label_smoothing" in lib.ak_last_error()
+    # vocab ranges: inside [0, vocab), grad_logits pitch >= the range's width
+    for v_begin, v_count in ((-1, 8), (0, 0), (60, 8), (0, 65)):
+        rc = lib.ak_lmhead_ce_bwd_range(*([None] * 7), 16, 8, 64, v_begin, v_count, 64, 64, 64, -100,
+                                        0.0, 0.0, 2, None)
+        assert rc == -1 and b"vocab range" in lib.ak_last_error()
+    rc = lib.ak_lmhead_ce_bwd_range(*([None] * 7), 8, 8, 64, 16, 32, 64, 64, 64, -100, 0.0, 0.0, 2, None)
+    assert rc == -1 and b"pitch" in lib.ak_last_error()
     rc = _lib.load().ak_selective_scan_fwd(*([None] * 13), 2, 4, 16, 300, 1, *([0] * 15), 0, 0, 2, 0,
                                            2, 0, None)
     assert rc == -2 and b"dstate" in lib.ak_last_error()

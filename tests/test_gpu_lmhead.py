@@ -382,6 +382,51 @@ def test_lmhead_ce_backward_grads(dtype, n, vocab, d):
         assert torch.allclose(got, want, rtol=2e-2, atol=2e-2 * float(want.abs().max()))
 
 
+@pytest.mark.parametrize("softcap,ls", [(0.0, 0.0), (30.0, 0.1)])
+def test_lmhead_ce_backward_vocab_ranges(monkeypatch, softcap, ls):
+    """A dlogits budget below the full matrix walks the vocabulary in ranges
+    (ak_lmhead_ce_bwd_range, the last one ragged): the range's dlogits equal
+    the full matrix's columns bitwise, and the gradients match the one-range
+    result and float64 autograd."""
+    need_gpu()
+    from kernels.hip import _lib
+    from kernels.hip import chunked_linear_cross_entropy as clce
+    g = torch.Generator().manual_seed(31)
+    n, vocab, d = 700, 3000, 128
+    h = torch.randn(n, d, generator=g).bfloat16()
+    W = (0.05 * torch.randn(vocab, d, generator=g)).bfloat16()
+    t = torch.randint(0, vocab, (n,), generator=g)
+    t[::9] = -100
+    t[5] = vocab - 1
+    t[6] = 0
+    say("lmhead_ce backward vocab ranges", softcap, ls)
+    hd, Wd, td = h.to(DEV), W.to(DEV), t.to(DEV)
+    _, lse, nv = clce.lmhead_ce_forward(hd, Wd, td, softcap=softcap, label_smoothing=ls)
+    denom = nv.to(torch.float32).clamp(min=1.0)
+    up = torch.tensor(0.7, device=DEV)
+    full = torch.empty(n, vocab, dtype=torch.bfloat16, device=DEV)
+    _lib.lmhead_ce_bwd(hd, Wd, td, lse, up.reshape(1), denom.reshape(1), full, -100, softcap, ls)
+    for v0, v1 in ((0, 1024), (1024, 2816), (2816, 3000)):
+        part = torch.empty(n, v1 - v0, dtype=torch.bfloat16, device=DEV)
+        _lib.lmhead_ce_bwd_range(hd, Wd, td, lse, up.reshape(1), denom.reshape(1), part, v0, -100,
+                                 softcap, ls)
+        assert torch.equal(part, full[:, v0:v1]), (v0, v1)
+    gh1, gw1 = clce.lmhead_ce_backward(hd, Wd, td, lse, denom, up, softcap=softcap,
+                                       label_smoothing=ls)
+    monkeypatch.setattr(clce, "GRAD_LOGITS_BUDGET", n * 1024 * 2)  # ranges of 1024 columns
+    gh, gw = clce.lmhead_ce_backward(hd, Wd, td, lse, denom, up, softcap=softcap, label_smoothing=ls)
+    # grad_weight rows: the same GEMM per row range
+    assert float((gw.float() - gw1.float()).norm() / gw1.float().norm()) < 1e-3
+    hr, Wr = h.double().requires_grad_(), W.double().requires_grad_()
+    z = hr @ Wr.t()
+    if softcap > 0:
+        z = softcap * torch.tanh(z / softcap)
+    (0.7 * F.cross_entropy(z, t, label_smoothing=ls)).backward()
+    for got, want in ((gh, hr.grad), (gw, Wr.grad), (gh1, hr.grad)):
+        got = got.double().cpu()
+        assert float((got - want).norm() / want.norm()) < 5e-3
+
+
 def test_c4_full_size_backward():
     """C4: dlogits rows against float64, grad_hidden rows against float64,
     grad_weight against an fp32 torch reference on the GPU; deterministic."""
