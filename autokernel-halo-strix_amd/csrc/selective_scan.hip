@@ -288,36 +288,52 @@ mamba_scan_fwd_kernel(ScanParams p) {
 // scheduler cannot interleave across (about 8% of the kernel at the C5 shape).
 enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 
+// kRPC (forward only): 16-lane rows per channel, for dstate up to 16 * kRPC.
+// With kRPC > 1 a channel's states span kRPC rows of its wave (state = 16 *
+// row-in-channel + lane); each row sums its 16 states' outputs through the LDS
+// transpose as with one row, and the rows' partials are added with permlane
+// swaps. A workgroup then holds 16 / kRPC channels, and the larger B / C
+// staging is single-buffered (two barriers per tile) so that two workgroups
+// still fit in a CU's LDS.
 template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false,
-          int kVar = kFwdAny>
+          int kVar = kFwdAny, int kRPC = 1>
 __global__ void __launch_bounds__(256)
 mamba_scan_fast_kernel(ScanParams p) {
   static_assert(!(kPrep && kVar != kFwdAny), "the fixed variants are forwards");
+  static_assert(kRPC == 1 || kRPC == 2 || kRPC == 4, "1, 2 or 4 rows per channel");
+  static_assert(!(kPrep && kRPC != 1), "the preparation pass has 16 states");
+  constexpr int kNS = 16 * kRPC;                         // state slots per channel
+  constexpr int kCPW = 4 / kRPC;                         // channels per wave
+  constexpr int kWGC = 16 / kRPC;                        // channels per workgroup
+  constexpr int kCSt = kRPC == 1 ? kCStride : kNS + 4;   // Cs step pitch (floats)
+  constexpr int kNB = kRPC == 1 ? 2 : 1;                 // staging buffers
   const bool has_z = kVar != kFwdAny || p.z != nullptr;
   const bool has_prez = kVar == kFwdTrain || (kVar == kFwdAny && !kPrep && p.out_prez != nullptr);
   float* const ck_out = kVar == kFwdLean ? nullptr : p.ck;
   const bool has_ck = kPrep || kVar == kFwdTrain || (kVar == kFwdAny && ck_out != nullptr);
   float* const xs_out = kVar != kFwdAny ? nullptr : p.chunk_states;
-  __shared__ float Bs[2][16 * kBStride];
-  __shared__ float Cs[2][kScanT * kCStride];
+  __shared__ float Bs[kNB][kNS * kBStride];
+  __shared__ float Cs[kNB][kScanT * kCSt];
   __shared__ float hbuf[4][4 * kHC];
 
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
-  const int c = lane / 16;  // channel within the wave
-  const int n = lane % 16;  // state owned by this lane
+  const int c = lane / 16;       // row of the wave (the channel when kRPC == 1)
+  const int n = lane % 16;       // lane in the row: owned step block / state
+  const int sr = c % kRPC;       // row within the channel
+  const int ns = 16 * sr + n;    // state owned by this lane
 
   const int per_batch = p.ngroups * p.tiles_per_group;
   const int b = blockIdx.x / per_batch;
   const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
   const int tile = blockIdx.x % p.tiles_per_group;
-  const int d0 = g * p.ch_per_group + tile * kScanCh;  // first channel of the workgroup
-  const int wc = wave * 4 + c;                          // channel within the workgroup
+  const int d0 = g * p.ch_per_group + tile * kWGC;      // first channel of the workgroup
+  const int wc = wave * kCPW + c / kRPC;                // channel within the workgroup
   const int d = d0 + wc;
-  const bool n_ok = n < p.dstate;
+  const bool n_ok = ns < p.dstate;
 
-  const float a_scaled = n_ok ? p.A[(int64_t)d * p.A_ds + n] * kLog2e : 0.0f;
+  const float a_scaled = n_ok ? p.A[(int64_t)d * p.A_ds + ns] * kLog2e : 0.0f;
   const float dbias = p.delta_bias ? p.delta_bias[d] : 0.0f;
   const float dskip = p.D ? p.D[d] : 0.0f;
 
@@ -326,7 +342,7 @@ mamba_scan_fast_kernel(ScanParams p) {
   const uint32_t L = (uint32_t)p.seqlen;
   auto row_rsrc = [&](const void* base, int64_t bs, int64_t ds, int esz) {
     const char* q = static_cast<const char*>(base) + ((int64_t)b * bs + (int64_t)d0 * ds) * esz;
-    return make_rsrc(q, (uint32_t)(((kScanCh - 1) * ds + L) * esz));
+    return make_rsrc(q, (uint32_t)(((kWGC - 1) * ds + L) * esz));
   };
   const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
   const Rsrc rs_d = row_rsrc(p.delta, p.d_bs, p.d_ds, sizeof(TD));
@@ -352,9 +368,13 @@ mamba_scan_fast_kernel(ScanParams p) {
   // different states, so the transposed Cs writes of a wave hit 64 distinct
   // banks (with 16 lanes per state they conflicted 8-way)
   const int sn = tid % 16, q = tid / 16;
-  const int sn_c = min(sn, p.dstate - 1);
-  const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
-  const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
+  uint32_t vo_B[kRPC], vo_C[kRPC];  // state sn + 16 k
+#pragma unroll
+  for (int k = 0; k < kRPC; ++k) {
+    const int sn_c = min(sn + 16 * k, p.dstate - 1);
+    vo_B[k] = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
+    vo_C[k] = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
+  }
 
   struct Regs {
     Raw4<TD> dv;
@@ -363,7 +383,7 @@ mamba_scan_fast_kernel(ScanParams p) {
     Raw1<TU> go[kPrep ? 4 : 1];
   };
   struct Stage {
-    Raw4<TBC> bv, cv;
+    Raw4<TBC> bv[kRPC], cv[kRPC];
   };
   const int nt = p.seqlen / kScanT;
   auto load_regs = [&](int t, Regs& r) {
@@ -379,15 +399,22 @@ mamba_scan_fast_kernel(ScanParams p) {
   };
   auto load_stage = [&](int t, Stage& s) {
     const uint32_t l0 = (uint32_t)t * kScanT;
-    s.bv = bload4<TBC>(rs_B, vo_B, l0 * sizeof(TBC));
-    s.cv = bload4<TBC>(rs_C, vo_C, l0 * sizeof(TBC));
+#pragma unroll
+    for (int k = 0; k < kRPC; ++k) {
+      s.bv[k] = bload4<TBC>(rs_B, vo_B[k], l0 * sizeof(TBC));
+      s.cv[k] = bload4<TBC>(rs_C, vo_C[k], l0 * sizeof(TBC));
+    }
   };
   auto write_stage = [&](const Stage& s, int buf) {
-    const bool ok = sn < p.dstate;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      Bs[buf][sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(s.bv, k) : 0.0f;
-      Cs[buf][(4 * q + k) * kCStride + sn] = ok ? raw4_f32<TBC>(s.cv, k) : 0.0f;
+    for (int kk = 0; kk < kRPC; ++kk) {
+      const int st = sn + 16 * kk;
+      const bool ok = st < p.dstate;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        Bs[buf][st * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(s.bv[kk], k) : 0.0f;
+        Cs[buf][(4 * q + k) * kCSt + st] = ok ? raw4_f32<TBC>(s.cv[kk], k) : 0.0f;
+      }
     }
   };
 
@@ -401,7 +428,12 @@ mamba_scan_fast_kernel(ScanParams p) {
     float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
-    float o = fmaf(dskip, p_uo, (y4[0] + y4[1]) + (y4[2] + y4[3]));
+    float ysum = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+    // rows of one channel: add their partial sums (every row gets the total)
+    if constexpr (kRPC == 4) ysum = swap32_sum(ysum, ysum);
+    if constexpr (kRPC >= 2) ysum = swap16_sum(ysum, ysum);
+    if (kRPC > 1 && sr != 0) return;  // the channel's first row stores
+    float o = fmaf(dskip, p_uo, ysum);
     if constexpr (kPrep) {
       if (has_z) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-p_zo * kLog2e));
@@ -429,15 +461,16 @@ mamba_scan_fast_kernel(ScanParams p) {
     asm volatile("s_nop 1"
                  : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
                    "+v"(du[2]), "+v"(du[3]));
+    const int bb = kNB == 2 ? buf : 0;
     float bt[kScanT];
 #pragma unroll
-    for (int l = 0; l < kScanT; ++l) bt[l] = Bs[buf][n * kBStride + l];
+    for (int l = 0; l < kScanT; ++l) bt[l] = Bs[bb][ns * kBStride + l];
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
       if (has_ck) {
         if (n_ok)
-          ck_out[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + n] = h;
+          ck_out[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + ns] = h;
       }
       float hv[16], av[16], xv[16];
       auto steps4 = [&](auto src_c, int j4) {
@@ -482,7 +515,7 @@ mamba_scan_fast_kernel(ScanParams p) {
 #pragma unroll
       for (int s2 = 0; s2 < 16; ++s2) {
         ph[s2] = hb[c * kHC + n * kHJ + s2];
-        pc[s2] = Cs[buf][(16 * blk + n) * kCStride + s2];
+        pc[s2] = Cs[bb][(16 * blk + n) * kCSt + 16 * sr + s2];
       }
       __builtin_amdgcn_wave_barrier();
       p_uo = raw_f32<TU>(cur.uo[blk]);
@@ -496,7 +529,7 @@ mamba_scan_fast_kernel(ScanParams p) {
       const int l1 = (t + 1) * kScanT;
       if ((l1 % kXChunk == 0 || l1 >= p.seqlen) && n_ok) {
         float* xs = xs_out +
-                    ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + n) * 2;
+                    ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + ns) * 2;
         xs[0] = __builtin_amdgcn_exp2f(a_scaled * dsum);
         xs[1] = h;
       }
@@ -508,9 +541,18 @@ mamba_scan_fast_kernel(ScanParams p) {
   // to the last tile: unconditional loads of valid addresses), then compute.
   Stage st;
   auto tile_body = [&](int t, const Regs& cur, Regs& nxt) {
-    __syncthreads();
-    write_stage(st, (t + 1) & 1);
-    load_stage(min(t + 2, nt - 1), st);
+    if constexpr (kNB == 2) {
+      __syncthreads();
+      write_stage(st, (t + 1) & 1);
+      load_stage(min(t + 2, nt - 1), st);
+    } else {
+      // single buffer: tile t's stage (in st since the previous tile) goes in
+      // once every wave is done with tile t - 1's
+      __syncthreads();
+      write_stage(st, 0);
+      __syncthreads();
+      load_stage(min(t + 1, nt - 1), st);
+    }
     load_regs(min(t + 1, nt - 1), nxt);
     asm volatile("" ::: "memory");
     compute(t, cur);
@@ -519,15 +561,17 @@ mamba_scan_fast_kernel(ScanParams p) {
   Regs ra, rb;
   load_stage(0, st);
   load_regs(0, ra);
-  write_stage(st, 0);
-  load_stage(min(1, nt - 1), st);
+  if constexpr (kNB == 2) {
+    write_stage(st, 0);
+    load_stage(min(1, nt - 1), st);
+  }
   for (int t = 0; t < nt; t += 2) {
     tile_body(t, ra, rb);
     if (t + 1 < nt) tile_body(t + 1, rb, ra);
   }
   finish_pending();
   if (!kPrep && p.last_state && n_ok) {
-    p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
+    p.last_state[((int64_t)b * p.dim + d) * p.dstate + ns] = h;
   }
 }
 
@@ -1038,7 +1082,7 @@ scan_bwd_finalize_kernel(const float* __restrict__ dB_part, const float* __restr
 // and every buffer resource's extent (16 channel rows, or dstate B / C rows)
 // below 2 GiB.
 template <typename TU, typename TD, typename TBC>
-bool scan_fast_ok(const ScanParams& p, bool prep = false) {
+bool scan_fast_ok(const ScanParams& p, bool prep = false, int wgc = kScanCh) {
   auto al4 = [](const void* ptr, int64_t s0, int64_t s1, int64_t s2, size_t esz) {
     return (reinterpret_cast<uintptr_t>(ptr) % (4 * esz)) == 0 && s0 % 4 == 0 && s1 % 4 == 0 &&
            s2 % 4 == 0;
@@ -1046,7 +1090,7 @@ bool scan_fast_ok(const ScanParams& p, bool prep = false) {
   auto fits = [&](int64_t rows, int64_t pitch, size_t esz) {
     return pitch >= 0 && ((rows - 1) * pitch + p.seqlen) * (int64_t)esz < ((int64_t)1 << 31);
   };
-  if (p.seqlen % kScanT != 0 || p.ch_per_group % kScanCh != 0) return false;
+  if (p.seqlen % kScanT != 0 || p.ch_per_group % wgc != 0) return false;
   if (!al4(p.u, p.u_bs, p.u_ds, 0, sizeof(TU)) || !al4(p.delta, p.d_bs, p.d_ds, 0, sizeof(TD)))
     return false;
   if (!al4(p.B, p.B_bs, p.B_gs, p.B_ns, sizeof(TBC)) || !al4(p.C, p.C_bs, p.C_gs, p.C_ns, sizeof(TBC)))
@@ -1054,9 +1098,9 @@ bool scan_fast_ok(const ScanParams& p, bool prep = false) {
   if (p.u_bs < 0 || p.d_bs < 0 || p.o_bs < 0 || p.z_bs < 0 || p.B_bs < 0 || p.C_bs < 0 ||
       p.B_gs < 0 || p.C_gs < 0)
     return false;
-  if (prep && (p.go_bs < 0 || !fits(kScanCh, p.go_ds, sizeof(TU)))) return false;
-  return fits(kScanCh, p.u_ds, sizeof(TU)) && fits(kScanCh, p.d_ds, sizeof(TD)) &&
-         fits(kScanCh, p.o_ds, sizeof(TU)) && (!p.z || fits(kScanCh, p.z_ds, sizeof(TU))) &&
+  if (prep && (p.go_bs < 0 || !fits(wgc, p.go_ds, sizeof(TU)))) return false;
+  return fits(wgc, p.u_ds, sizeof(TU)) && fits(wgc, p.d_ds, sizeof(TD)) &&
+         fits(wgc, p.o_ds, sizeof(TU)) && (!p.z || fits(wgc, p.z_ds, sizeof(TU))) &&
          fits(p.dstate, p.B_ns, sizeof(TBC)) && fits(p.dstate, p.C_ns, sizeof(TBC));
 }
 
@@ -1079,6 +1123,40 @@ void launch_scan(const ScanParams& p, hipStream_t s) {
     mamba_scan_fast_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
   else
     mamba_scan_fwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
+}
+
+// dstate in (16, 64] with variable B / C: the specialised kernel with 2 or 4
+// rows per channel, when the whole-tile conditions hold. Returns whether it
+// launched.
+template <typename TU, typename TD, typename TBC>
+bool launch_scan_rows(const ScanParams& p, hipStream_t s) {
+  const int rpc = p.dstate <= 32 ? 2 : 4;
+  const int wgc = kScanCh / rpc;
+  if (p.dstate <= 16 || p.dstate > 64 || p.b_const || p.c_const) return false;
+  if (!scan_fast_ok<TU, TD, TBC>(p, false, wgc)) return false;
+  ScanParams q = p;
+  q.tiles_per_group = p.ch_per_group / wgc;
+  const int grid = q.batch * q.ngroups * q.tiles_per_group;
+  if (rpc == 2) {
+    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdAny, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
+    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdAny, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
+  } else {
+    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdAny, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
+    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdAny, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
+  }
+  return true;
+}
+
+template <typename TU>
+bool dispatch_scan_rows(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, hipStream_t s) {
+  const bool d32 = delta_dtype == AK_DTYPE_F32;
+  const bool bc32 = bc_dtype == AK_DTYPE_F32;
+  if (!d32 && delta_dtype != u_dtype) return false;
+  if (!bc32 && bc_dtype != u_dtype) return false;
+  if (d32 && bc32) return launch_scan_rows<TU, float, float>(p, s);
+  if (d32) return launch_scan_rows<TU, float, TU>(p, s);
+  if (bc32) return launch_scan_rows<TU, TU, float>(p, s);
+  return launch_scan_rows<TU, TU, TU>(p, s);
 }
 
 template <typename TU>
@@ -1256,7 +1334,17 @@ extern "C" int ak_selective_scan_fwd(
   p.z_bs = z_batch_stride; p.z_ds = z_dim_stride; p.o_bs = out_batch_stride; p.o_ds = out_dim_stride;
   p.softplus = delta_softplus ? 1 : 0;
   hipStream_t s = ak_stream(stream);
-  if (ak::scan_needs_wide(p)) {
+  bool rows = false;  // dstate in (16, 64]: the specialised kernel with 2 / 4 rows per channel
+  if (p.dstate > 16 && p.dstate <= 64) {
+    switch (u_dtype) {
+      case AK_DTYPE_F32: rows = ak::dispatch_scan_rows<float>(p, u_dtype, delta_dtype, bc_eff, s); break;
+      case AK_DTYPE_F16: rows = ak::dispatch_scan_rows<ak::f16>(p, u_dtype, delta_dtype, bc_eff, s); break;
+      default: rows = ak::dispatch_scan_rows<ak::bf16>(p, u_dtype, delta_dtype, bc_eff, s); break;
+    }
+  }
+  if (rows) {
+    rc = 0;
+  } else if (ak::scan_needs_wide(p)) {
     rc = ak::launch_scan_wide_fwd(p, false, u_dtype, delta_dtype, bc_eff, s);
   } else {
     switch (u_dtype) {

@@ -227,3 +227,57 @@ def test_wide_chunk_states_and_binding():
     assert res[3].shape == (16, 64) and res[3].dtype == torch.float32
     gref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
     assert torch.allclose(res[3].cpu().double(), gref[3], rtol=1e-3, atol=1e-3)
+
+
+@pytest.mark.parametrize("itype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("layout", ["var1", "var2"])
+@pytest.mark.parametrize("dstate", [24, 32, 48, 64])
+def test_forward_rows_per_channel_kernels(itype, layout, dstate):
+    """dstate 17-64 with input-dependent B / C on whole 64-step tiles runs the
+    specialised forward with 2 or 4 lane rows per channel (dim 16: every
+    channel tile whole): output and last state against the C oracle, with a
+    gate, delta_bias and softplus, partial state slots at 24 and 48."""
+    need_gpu()
+    dt = ITYPES[itype]
+    u, delta, A, B, C, D, z, bias, _ = _inputs(2, 16, dstate, 256, layout, dt, dstate + 3)
+    say("mamba rows fwd", itype, layout, dstate)
+    out, last = _fwd(u, delta, A, B, C, D, z, bias, True)
+    ref, rlast = c_oracle.selective_scan(u, delta, A, B, C, D, z, bias, True)
+    rtol, atol = GRID["tolerances"][itype]
+    assert torch.allclose(out.float(), ref, rtol=rtol, atol=atol)
+    assert torch.allclose(last, rlast, rtol=1e-4, atol=1e-3)
+
+
+@pytest.mark.parametrize("dstate", [32, 64])
+def test_rows_kernel_training_path_and_chunk_states(dstate):
+    """The training forward on the rows kernels keeps its 16-step states, which
+    the general backward then starts from: every gradient against the float64
+    oracle, and the same gradients (dz within rounding) as the path that
+    recomputes the states. The binding's chunk states x from the rows kernels
+    against the chunk-state oracle over three 2048-step chunks."""
+    need_gpu()
+    from kernels.hip import selective_scan as ss
+    from kernels.hip import selective_scan_cuda
+    args = _inputs(2, 8, dstate, 512, "var1", torch.float32, 70 + dstate)
+    say("mamba rows training path", dstate)
+    saved = ss.SAVE_STATES
+    try:
+        ss.set_save_states(True)
+        kept = _grads(*args, softplus=True)
+        ss.set_save_states(False)
+        recomputed = _grads(*args, softplus=True)
+    finally:
+        ss.set_save_states(saved)
+    u, delta, A, B, C, D, z, bias, dout = args
+    gref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    _check(kept, gref, _tols("float32", True, False, False), (u, delta, A, B, C, D, z, bias))
+    for name, a, b in zip(NAMES, kept, recomputed):
+        assert torch.allclose(a.double(), b.double(), rtol=1e-4, atol=1e-5), name
+    u, delta, A, B, C, D, z, bias, _ = _inputs(1, 8, dstate, 4160, "var1", torch.float32, 5)
+    d = lambda t: t.to(DEV)
+    out, x, out_z = selective_scan_cuda.fwd(d(u), d(delta), d(A), d(B), d(C), d(D), d(z), d(bias), True)
+    assert x.shape == (1, 8, 3, 2 * dstate)
+    xr = ops.selective_scan_chunk_states_ref(u, delta, A, B, bias, True)
+    assert torch.allclose(x.cpu().double().view(1, 8, 3, dstate, 2), xr, rtol=1e-4, atol=1e-5)
+    ref_z, _ = c_oracle.selective_scan(u, delta, A, B, C, D, z, bias, True)
+    assert torch.allclose(out_z.cpu(), ref_z, rtol=6e-4, atol=2e-3)
