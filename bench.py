@@ -287,7 +287,7 @@ def make_case(name):
         launch = lambda s: _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"],
                                                None, None, s["out"], None, True)
         return Case(name, "Mamba-1 scan at the reference's benchmark shape B8 D384 L512 N64 fp16",
-                    "hbm", N64_BYTES, 8 * 512, launch, sets, "mamba_scan_wide_fwd_kernel",
+                    "hbm", N64_BYTES, 8 * 512, launch, sets, "mamba_scan_fast_kernel (4 lane rows per channel)",
                     valu_cycles=scan_valu_cycles(8, 384, 64, 512), valu_model=SCAN_VALU_MODEL)
     if name == "c5b":
         cpu = gen_c5()
@@ -306,7 +306,7 @@ def make_case(name):
             s["ddelta"], s["dA"], s["dB"], s["dC"], s["dD"], s["dz"], None, False)
         return Case(name, "C5-shape Mamba-1 selective scan backward B4 L4096 D2048 N16", "hbm",
                     C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
+                    "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel + scan_bwd_finalize_kernel")
     if name == "c5t":
         # one training step of the scan: the forward keeps its states every 16
         # steps and its pre-gate output, the backward restarts from them
@@ -331,7 +331,7 @@ def make_case(name):
                                     s["dz"], None, False, checkpoints=s["ck"], out_prez=s["prez"])
         return Case(name, "C5-shape Mamba-1 training step (forward keeping its states + backward from them)",
                     "hbm", C5_BYTES + C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel + mamba_scan_bwd_kernel + scan_bwd_finalize_kernel")
+                    "mamba_scan_fast_kernel (training variant) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel + scan_bwd_finalize_kernel")
     raise ValueError(name)
 
 
