@@ -2,7 +2,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "ak_common.h"
+#include <atomic>
+
+#include "mfma_ring.h"
 
 namespace {
 thread_local char g_last_error[512] = "";
@@ -30,3 +32,22 @@ extern "C" const char* ak_last_error(void) { return g_last_error; }
 extern "C" int ak_abi_version(void) { return AK_ABI_VERSION; }
 
 extern "C" const char* ak_target_arch(void) { return "gfx950"; }
+
+namespace ak {
+
+// The cache entries are atomics: concurrent first calls may both query the
+// attribute, but they store the same value and no caller reads a torn entry.
+int cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+}  // namespace ak

@@ -42,52 +42,19 @@
 //   the 16 MFMAs of a 16-wide K slice run over 16 different accumulators
 //   while the fragments of the slice after next are read; one barrier per K
 //   block (after its second slice) publishes the next block's slots.
-#include <atomic>
-
-#include "ak_common.h"
+#include "mfma_ring.h"
 
 namespace ak {
 namespace {
 
 constexpr int kTV = 256;      // vocab rows per tile
 constexpr int kTT = 256;      // tokens per tile
-constexpr int kKB = 64;       // K per block (one 128-byte line per bf16 row)
-constexpr int kSlots = 5;     // LDS ring slots
 constexpr int kLThreads = 256;
-constexpr int kChunks = kKB / 8;                         // 16-byte chunks per staged row
-constexpr int kSlotChunks = 256 * kChunks;               // u32x4 per slot (32 KiB)
-constexpr int kDma = 256 / 8 / 4;                        // DMA instructions per wave per slot
 constexpr int kGroupV = 4;                               // vocab tiles per XCD group
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ f32x16_t mfma32(bf16, u32x4 a, u32x4 b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x16_t mfma32(f16, u32x4 a, u32x4 b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
-                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-// s_waitcnt immediate (gfx9 encoding): vmcnt(n), expcnt and lgkmcnt(0).
-constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
 struct MSPair {
   float m, s;
 };
-
-// One accumulator element copied from its AGPR to a VGPR at this point of
-// the program (an explicit read keeps the compiler from copying all 256
-// accumulators into VGPRs at once ahead of the epilogue).
-__device__ __forceinline__ float acc_read(float a) {
-  float v;
-  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-  return v;
-}
 
 // Tile coordinates of this workgroup's i-th tile. Work item w = block + i *
 // grid runs on XCD w % 8 (workgroups are dealt to the 8 XCDs round-robin);
@@ -128,17 +95,6 @@ __device__ __forceinline__ void slice_order() {
   }
   if (16 - kDs - kDmaN > 0) __builtin_amdgcn_sched_group_barrier(0x008, 16 - kDs - kDmaN, 0);
   __builtin_amdgcn_sched_barrier(0);
-}
-
-// Workgroup barrier that publishes LDS filled by this workgroup's
-// global_load_lds DMA: the caller has already waited (s_waitcnt) for its own
-// DMA loads. A release fence here would wait for every outstanding DMA load
-// (vmcnt(0)) and so drain the ring; the empty asm statements keep the
-// compiler from moving LDS accesses across the barrier instead.
-__device__ __forceinline__ void ring_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // Row range of a tile along one dimension of `n` rows: the tile owns rows
@@ -793,22 +749,6 @@ WsLayout ws_layout(int64_t n_rows, int64_t vocab) {
   w.zsum = w.losses + align256((size_t)n_rows * 4);
   w.total = w.zsum + align256((size_t)2 * n_vt * n_rows * 4);
   return w;
-}
-
-// Compute units of the current device, queried once per device. The cache
-// entries are atomics: concurrent first calls may both query the attribute,
-// but they store the same value and no caller reads a torn entry.
-int cu_count() {
-  static std::atomic<int> cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cached[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
 }
 
 template <typename T, bool kCap, bool kLs>

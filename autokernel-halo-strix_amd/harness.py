@@ -466,17 +466,28 @@ def run_correctness(spec: KernelSpec, quick: bool = False, device: str = "cuda",
 
 def median_launch_ms(fn: Callable[[], object], reps: int = 100, warmup: int = 10) -> float:
     """Median over ``reps`` launches of the time between an event pair recorded
-    on the current stream around each launch."""
+    on the current stream around each launch.
+
+    The pairs are issued while a spin kernel holds the stream (about 1 ms,
+    doubled while the GPU still drains the queue before the host is done), so
+    that launches shorter than their host issue time are timed on the GPU."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in range(reps)]
-    for a, b in pairs:
-        a.record()
-        fn()
-        b.record()
-    torch.cuda.synchronize()
+    hold = 2_000_000
+    while True:
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(reps)]
+        torch.cuda._sleep(hold)
+        for a, b in pairs:
+            a.record()
+            fn()
+            b.record()
+        drained = pairs[-1][1].query()
+        torch.cuda.synchronize()
+        if not drained or hold >= 16_000_000:
+            break
+        hold *= 2
     ts = sorted(a.elapsed_time(b) for a, b in pairs)
     return ts[len(ts) // 2]
 

@@ -69,6 +69,11 @@ _SIGNATURES = {
                          _int, _c_void_p],
     "ak_lmhead_ce_bwd": [_c_void_p] * 7 + [_i64] * 7 + [_f32, _f32, _int, _c_void_p],
     "ak_lmhead_ce_bwd_range": [_c_void_p] * 7 + [_i64] * 9 + [_f32, _f32, _int, _c_void_p],
+    "ak_lmhead_grad_workspace_bytes": [_i64, _i64, _i64],
+    "ak_lmhead_grad_hidden": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
+                              _int, _c_void_p, ctypes.c_size_t, _int, _c_void_p],
+    "ak_lmhead_grad_weight": [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64, _i64,
+                              _int, _c_void_p, ctypes.c_size_t, _int, _c_void_p],
     "ak_selective_scan_fwd": [_c_void_p] * 13 + [_i64] * 5 + [_i64] * 15 + [_int] * 6 + [_c_void_p],
     "ak_diag_scan_fwd": [_c_void_p] * 6 + [_i64] * 3 + [_c_void_p],
     "ak_diag_scan_bwd_workspace_bytes": [_i64, _i64],
@@ -81,6 +86,7 @@ _RESTYPES = {
     "ak_last_error": ctypes.c_char_p,
     "ak_target_arch": ctypes.c_char_p,
     "ak_lmhead_ce_workspace_bytes": ctypes.c_size_t,
+    "ak_lmhead_grad_workspace_bytes": ctypes.c_size_t,
     "ak_rmsnorm_bwd_workspace_bytes": ctypes.c_size_t,
     "ak_diag_scan_bwd_workspace_bytes": ctypes.c_size_t,
     "ak_selective_scan_bwd_workspace_bytes": ctypes.c_size_t,
@@ -139,13 +145,14 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 # in about 5 us on the GPU): the raw-stream query and the device check below
 # avoid building a torch Stream object and entering a device guard per call.
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+if _raw_stream is None:
+    def _raw_stream(index: int) -> int:
+        return torch.cuda.current_stream(index).cuda_stream
 _NO_GUARD = contextlib.nullcontext()
 
 
 def _stream(t: torch.Tensor) -> int:
-    if _raw_stream is not None:
-        return _raw_stream(t.device.index)
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _raw_stream(t.device.index)
 
 
 def _on_device(t: torch.Tensor):
@@ -218,6 +225,29 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor, eps: float) 
                                    _rows_view(x, "x"), _rows_view(y, "y"), float(eps),
                                    dtype_code(x.dtype), _stream(x))
     _check(rc, "ak_rmsnorm_fwd")
+
+
+def rmsnorm_contig(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor, cols: int,
+                   eps: float) -> None:
+    """RMSNorm of a contiguous ``x`` into a contiguous ``y`` of its shape and
+    dtype, rows of ``cols`` elements, ``weight`` a contiguous ``[cols]`` of
+    the same dtype. The caller has checked that all three are on one GPU;
+    this launcher passes the dense pitch without building 2-D views (a view
+    costs about 1 us of host time, the whole call about 4 us)."""
+    n = x.numel()
+    if n == 0:
+        return
+    dev = x.get_device()
+    fn = (_lib or load()).ak_rmsnorm_fwd
+    if dev == torch.cuda.current_device():
+        rc = fn(x.data_ptr(), weight.data_ptr(), y.data_ptr(), n // cols, cols, cols, cols,
+                eps, AK_DTYPE[x.dtype], _raw_stream(dev))
+    else:
+        with torch.cuda.device(dev):
+            rc = fn(x.data_ptr(), weight.data_ptr(), y.data_ptr(), n // cols, cols, cols, cols,
+                    eps, AK_DTYPE[x.dtype], _raw_stream(dev))
+    if rc:
+        _check(rc, "ak_rmsnorm_fwd")
 
 
 def fused_add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
@@ -421,6 +451,51 @@ def lmhead_ce_bwd_range(hidden: torch.Tensor, weight: torch.Tensor, targets: tor
             _rows_view(weight, "weight"), int(ignore_index), float(softcap),
             float(label_smoothing), dtype_code(hidden.dtype), _stream(hidden))
     _check(rc, "ak_lmhead_ce_bwd_range")
+
+
+# out_mode of the lm-head gradient GEMMs
+GEMM_OUT_DTYPE = 0     # store in the operands' dtype
+GEMM_OUT_F32 = 1       # store fp32
+GEMM_OUT_F32_ADD = 2   # add into an fp32 output
+
+
+def lmhead_grad_workspace_bytes(n_rows: int, vocab: int, d: int) -> int:
+    return int(load().ak_lmhead_grad_workspace_bytes(n_rows, vocab, d))
+
+
+def _grad_gemm(entry: str, grad_logits: torch.Tensor, operand: torch.Tensor,
+               out: torch.Tensor, out_mode: int, workspace: Optional[torch.Tensor]) -> None:
+    require_device(grad_logits, operand, out, workspace)
+    n_rows, vocab = grad_logits.shape
+    d = operand.shape[1]
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with _on_device(grad_logits):
+        rc = getattr(load(), entry)(
+            _ptr(grad_logits), grad_logits.stride(0), _ptr(operand), _rows_view(operand, "operand"),
+            _ptr(out), _rows_view(out, "out"), n_rows, vocab, d, int(out_mode), _ptr(workspace),
+            ws_bytes, dtype_code(grad_logits.dtype), _stream(grad_logits))
+    _check(rc, entry)
+
+
+def lmhead_grad_hidden(grad_logits: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+                       out_mode: int, workspace: Optional[torch.Tensor]) -> None:
+    """out (=, or += with GEMM_OUT_F32_ADD) grad_logits @ weight.
+
+    ``grad_logits`` is a ``[n_rows, vocab]`` view whose row pitch covers
+    vocab rounded up to 64 with zeros in the padding columns; ``weight`` is
+    ``[vocab, d]``; ``out`` is ``[n_rows, d]``."""
+    if grad_logits.stride(1) != 1:
+        raise ValueError("grad_logits must have a contiguous last dimension")
+    _grad_gemm("ak_lmhead_grad_hidden", grad_logits, weight, out, out_mode, workspace)
+
+
+def lmhead_grad_weight(grad_logits: torch.Tensor, hidden: torch.Tensor, out: torch.Tensor,
+                       out_mode: int, workspace: Optional[torch.Tensor]) -> None:
+    """out (=, or += with GEMM_OUT_F32_ADD) grad_logits^T @ hidden; ``out``
+    is ``[vocab, d]``, the other operands as in :func:`lmhead_grad_hidden`."""
+    if grad_logits.stride(1) != 1:
+        raise ValueError("grad_logits must have a contiguous last dimension")
+    _grad_gemm("ak_lmhead_grad_weight", grad_logits, hidden, out, out_mode, workspace)
 
 
 # bc_flags of the selective-scan entry points: B / C input-independent ([dim, dstate] fp32)

@@ -28,18 +28,19 @@ logsumexp and writes ``dL/dlogits`` (softmax minus one-hot, times the
 upstream gradient over the counted rows, times ``1 - tanh^2`` under the
 softcap, less ``a / vocab`` under label smoothing) directly from registers in the
 input dtype; the device scalars stay on the device (no host sync). Then
-``grad_hidden = dlogits @ W`` and ``grad_W = dlogits^T @ h`` are two plain
-GEMMs with fp32 accumulation (hipBLASLt via torch). The vocabulary is
-walked in ranges whose ``dlogits`` slice ``[n_rows, width]`` stays under
-``GRAD_LOGITS_BUDGET`` bytes (``ak_lmhead_ce_bwd_range``; the width a
-multiple of the tile kernel's 256 vocab rows). Each range's ``grad_W`` rows
-are one complete GEMM rounded once to the weight dtype; ``grad_hidden`` is
-summed over the ranges in an fp32 buffer (``addmm`` with fp32 output) and
-rounded once at the end. The default budget (4 GiB) keeps the C4 shape in one
-range (8192 x 50304 bf16 = 824 MB, 0.3% of the 288 GB of HBM): measured on
-MI355X, 16384-column ranges (268 MB) cost 2102 us against 1826 us, the fp32
-accumulation of grad_hidden over ranges being slower than one GEMM over the
-whole vocabulary. Lower the budget where memory matters more than time.
+``grad_hidden = dlogits @ W`` and ``grad_W = dlogits^T @ h`` run as two
+hand-written MFMA GEMMs with fp32 accumulation (``ak_lmhead_grad_hidden``,
+``ak_lmhead_grad_weight``, ``csrc/lmhead_grad_gemm.hip``): dlogits is read
+in place, token-major, by both (the transposed operand through gfx950's
+transposing LDS reads). The vocabulary is walked in ranges whose
+``dlogits`` slice ``[n_rows, width]`` stays under ``GRAD_LOGITS_BUDGET``
+bytes (``ak_lmhead_ce_bwd_range``; the width a multiple of the tile kernel's
+256 vocab rows). Each range's ``grad_W`` rows are one complete GEMM rounded
+once to the weight dtype; ``grad_hidden`` is summed over the ranges in an
+fp32 buffer (the GEMM's add-into-fp32 output) and rounded once at the end.
+The default budget (4 GiB) keeps the C4 shape in one range (8192 x 50304
+bf16 = 824 MB, 0.3% of the 288 GB of HBM); lower it where memory matters
+more than time.
 Otherwise (fp32 or unaligned inputs) per row chunk
 the logits are recomputed with a GEMM and turned into ``dL/dlogits`` by the
 CE row kernel from the saved logsumexp, then ``grad_hidden = dlogits @ W``
@@ -129,31 +130,37 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     lse = lse.contiguous()
     width = GRAD_LOGITS_BUDGET // (n * hidden.element_size())
     width = max(_VOCAB_TILE, width - width % _VOCAB_TILE)
-    if width >= vocab:
-        # one range: exactly [n, vocab] (a padded pitch would leave
-        # uninitialised columns that a GEMM may read past K: 0 * NaN)
-        g = torch.empty((n, vocab), dtype=hidden.dtype, device=hidden.device)
-        _lib.lmhead_ce_bwd(hidden, weight, targets, lse, g1, den1, g, ignore_index, softcap,
-                           label_smoothing)
-        grad_hidden = torch.mm(g, weight) if need_hidden else None
-        grad_weight = torch.mm(g.t(), hidden) if need_weight else None
-        return grad_hidden, grad_weight
+    width = min(width, vocab)
+    ranges = [(v0, min(v0 + width, vocab)) for v0 in range(0, vocab, width)]
+    # each range's dlogits slice lives in a buffer whose pitch covers the
+    # slice rounded up to 64 columns, the padding zeroed (the gradient GEMMs
+    # read whole 64-column K blocks); a pitch off powers of two keeps the rows
+    # from all starting in the same memory channels
+    pitch = -(-width // 64) * 64
+    if pitch & (pitch - 1) == 0:
+        pitch += 64
+    gp = torch.empty((n, pitch), dtype=hidden.dtype, device=hidden.device)
+    ws_bytes = max(_lib.lmhead_grad_workspace_bytes(n, v1 - v0, d) for v0, v1 in ranges)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden.device) if ws_bytes else None
+    single = len(ranges) == 1
     grad_weight = torch.empty_like(weight) if need_weight else None
-    grad_h32 = torch.zeros((n, d), dtype=torch.float32, device=hidden.device) if need_hidden else None
-    for v0 in range(0, vocab, width):
-        v1 = min(v0 + width, vocab)
-        # [n, v1 - v0] view of a padded buffer whose padding is zeroed (a GEMM
-        # kernel may load past K and multiply by zero: 0 * NaN would leak in)
-        gp = torch.empty((n, v1 - v0 + _RANGE_PAD), dtype=hidden.dtype, device=hidden.device)
+    if need_hidden:
+        grad_hidden = torch.empty_like(hidden) if single else \
+            torch.zeros((n, d), dtype=torch.float32, device=hidden.device)
+    else:
+        grad_hidden = None
+    for v0, v1 in ranges:
         gp[:, v1 - v0:].zero_()
         g = gp[:, :v1 - v0]
         _lib.lmhead_ce_bwd_range(hidden, weight, targets, lse, g1, den1, g, v0, ignore_index,
                                  softcap, label_smoothing)
         if need_weight:
-            torch.mm(g.t(), hidden, out=grad_weight[v0:v1])
+            _lib.lmhead_grad_weight(g, hidden, grad_weight[v0:v1], _lib.GEMM_OUT_DTYPE, ws)
         if need_hidden:
-            torch.addmm(grad_h32, g, weight[v0:v1], out_dtype=torch.float32, out=grad_h32)
-    grad_hidden = grad_h32.to(hidden.dtype) if need_hidden else None
+            _lib.lmhead_grad_hidden(g, weight[v0:v1], grad_hidden,
+                                    _lib.GEMM_OUT_DTYPE if single else _lib.GEMM_OUT_F32_ADD, ws)
+    if need_hidden and not single:
+        grad_hidden = grad_hidden.to(hidden.dtype)
     return grad_hidden, grad_weight
 
 

@@ -31,6 +31,18 @@ DEFAULT_EPS = 1e-6
 
 def kernel_fn(x: torch.Tensor, weight: torch.Tensor, eps: float = DEFAULT_EPS) -> torch.Tensor:
     """RMSNorm over the last dimension. Matches ``reference.rmsnorm_ref``."""
+    # Common case first: contiguous x on a GPU, weight a contiguous [cols]
+    # of x's dtype on the same GPU. It goes straight to the C-ABI with the
+    # dense pitch (host time per call about 4 us above the HIP launch
+    # instead of 7 us for the general path below).
+    if (x.is_cuda and x.is_contiguous() and weight.is_contiguous() and weight.dtype == x.dtype
+            and x.dtype in _lib.AK_DTYPE and x.dim() >= 1 and weight.dim() == 1
+            and weight.get_device() == x.get_device()):
+        cols = x.shape[-1]
+        if weight.shape[0] == cols:
+            y = torch.empty_like(x)
+            _lib.rmsnorm_contig(x, weight, y, cols, eps)
+            return y
     _lib.require_device(x, weight)
     _lib.dtype_code(x.dtype)
     if weight.dim() != 1 or weight.numel() != x.shape[-1]:

@@ -10,7 +10,10 @@ causal-masked fp16 row softmax [8, 12, 1024, 1024] (C2). A "step" is one
 launch of that kernel over one batch of synthetic input already resident in
 HBM; ``value`` = algorithmic bytes x K / wall-clock time of the K timed steps.
 ``roofline`` gives the kernel's achieved bandwidth from the median of at
-least 100 per-launch HIP event pairs against MI355X's 8 TB/s; ``cpu_baseline`` times the CPU oracle on
+least 100 per-launch HIP event pairs (issued while a spin kernel holds the
+stream, so that they time the GPU and not the host's issue rate) against
+MI355X's 8 TB/s; ``host_us_per_call`` is the host's issue time per launch;
+``cpu_baseline`` times the CPU oracle on
 the GPU box's host on a bounded sample of the same workload. ``kernels``
 reports every configuration (C1..C5) the same way: time per launch, GB/s or
 TFLOP/s, roofline fraction, tokens/s and the CPU figure beside it.
@@ -346,8 +349,8 @@ def time_case(case, steps, warmup, pairs=ROOFLINE_PAIRS):
     Returns (wall seconds of the K steps, mean ms per launch from one HIP
     event pair around the K back-to-back launches on the launch stream,
     median ms per launch over ``pairs`` (>= 100) launches each bracketed by
-    its own event pair; those pairs add the event overhead to each launch,
-    which shows for launches of a few microseconds)."""
+    its own event pair and queued behind a held stream, host us per
+    launcher call)."""
     nset = len(case.sets)
     for i in range(warmup):
         case.launch(case.sets[i % nset])
@@ -363,15 +366,58 @@ def time_case(case, steps, warmup, pairs=ROOFLINE_PAIRS):
     wall = time.perf_counter() - t0
     mean_ms = ev0.elapsed_time(ev1) / steps
     n = max(pairs, ROOFLINE_PAIRS)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
-    for i in range(n):
-        starts[i].record()
-        case.launch(case.sets[i % nset])
-        ends[i].record()
-    torch.cuda.synchronize()
-    med_ms = statistics.median(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return wall, mean_ms, med_ms
+    durations, host_us = held_event_pairs(case, n)
+    return wall, mean_ms, statistics.median(durations), host_us
+
+
+# GPU cycles of the spin kernel that holds the stream before each batch of
+# event pairs (about 1 ms at MI355X clocks); doubled when a batch drained.
+HOLD_CYCLES = 2_000_000
+PAIR_BATCH = 25
+
+
+def held_event_pairs(case, n):
+    """Per-launch GPU durations (ms) from ``n`` event pairs, and the host time
+    per launcher call (us).
+
+    A launch of a few microseconds takes less GPU time than the host needs to
+    issue it and its two event records, so pairs issued back to back would
+    time the host's issue rate, not the kernel. Each batch of pairs is
+    therefore queued behind a spin kernel (``torch.cuda._sleep``): the host
+    issues the whole batch while the GPU spins, and the GPU then runs the
+    pairs back to back. A batch whose last event has already completed when
+    the host finishes issuing it may hold host gaps; it is issued again with a
+    longer spin. The host time per call is the issue time of a batch of
+    launches without event records, also behind a held stream, over its
+    launches (median of four batches)."""
+    nset = len(case.sets)
+    durations, host = [], []
+    hold = HOLD_CYCLES
+    i = 0
+    while i < n:
+        b = min(PAIR_BATCH, n - i)
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(b)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(b)]
+        torch.cuda._sleep(hold)
+        for j in range(b):
+            starts[j].record()
+            case.launch(case.sets[(i + j) % nset])
+            ends[j].record()
+        drained = ends[-1].query()
+        torch.cuda.synchronize()
+        if drained and hold < 64 * HOLD_CYCLES:
+            hold *= 2
+            continue
+        durations += [s.elapsed_time(e) for s, e in zip(starts, ends)]
+        i += b
+    for _ in range(4):
+        torch.cuda._sleep(hold)
+        t0 = time.perf_counter()
+        for j in range(PAIR_BATCH):
+            case.launch(case.sets[j % nset])
+        host.append((time.perf_counter() - t0) / PAIR_BATCH * 1e6)
+        torch.cuda.synchronize()
+    return durations, statistics.median(host)
 
 
 # ---------------------------------------------------------------------------
@@ -534,7 +580,7 @@ def main(argv=None):
     head = None
     for name in names:
         case = make_case(name)
-        wall, mean_ms, med_ms = time_case(case, args.steps, args.warmup, args.steps)
+        wall, mean_ms, med_ms, host_us = time_case(case, args.steps, args.warmup, args.steps)
         # rooflines from the median of the per-launch event pairs
         if case.bound == "hbm":
             achieved = case.work / (med_ms * 1e-3) / 1e9
@@ -555,6 +601,7 @@ def main(argv=None):
             "tokens_per_s": round(case.tokens / (med_ms * 1e-3), 1),
             "input_sets": len(case.sets),
             "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+            "host_us_per_call": round(host_us, 2),
         }
         if case.valu_cycles:
             # the VALU issue floor: instruction cycles per wave64 and SIMD over
@@ -596,7 +643,8 @@ def main(argv=None):
                    "accumulate": "fp32", "input_sets_rotated": len(case.sets)},
         "roofline": {"bound": "hbm", "achieved": h["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": h["frac"], "traffic": measured_traffic("softmax_vec_kernel"),
-                     "achieved_from": f"median of {h['event_pairs']} per-launch HIP event pairs",
+                     "achieved_from": f"median of {h['event_pairs']} per-launch HIP event pairs, "
+                                      "issued in batches queued behind a held stream",
                      "traffic_from": "profiles/hbm_traffic_pmc.md: rocprofv3 FETCH_SIZE + WRITE_SIZE "
                                      "per dispatch, scaled by a 256 MiB copy's readings"},
         "cpu_baseline": None,

@@ -287,6 +287,43 @@ int ak_lmhead_ce_bwd_range(const void* hidden, const void* weight, const int64_t
                            float label_smoothing, int dtype, void* stream);
 
 /*
+ * Gradient GEMMs of the lm-head + CE backward, from the dlogits written by
+ * ak_lmhead_ce_bwd / ak_lmhead_ce_bwd_range (hand-written MFMA kernels,
+ * fp32 accumulation). They replace the two torch.mm calls of the
+ * reference's backward, kernels/hip/chunked_linear_cross_entropy.py:121-132
+ * (grad_hidden = grad_logits @ weight, grad_weight = grad_logits^T @ hidden).
+ *   grad_logits : [n_rows, ld_gl] of dtype; columns [0, vocab) hold the
+ *                 gradient, columns [vocab, round_up(vocab, 64)) must be zero
+ *                 (ld_gl >= round_up(vocab, 64), a multiple of 8, < 2^23,
+ *                 every row readable to ld_gl)
+ *   weight      : [vocab, d] rows of ld_w (the vocab range's rows)
+ *   hidden      : [n_rows, d] rows of ld_h
+ *   d           : multiple of 64; ld_w, ld_h >= d, multiples of 8, < 2^23
+ *   out_mode    : 0 store in dtype, 1 store fp32, 2 add into fp32 (sums over
+ *                 vocab ranges)
+ *   workspace   : >= ak_lmhead_grad_workspace_bytes(n_rows, vocab, d) bytes
+ *                 (fp32 partial tiles of K-split work; 0 when none is split),
+ *                 16-byte aligned. The partial sums are added in a fixed order:
+ *                 results are bitwise reproducible.
+ * dtype: AK_DTYPE_BF16 or AK_DTYPE_F16.
+ */
+size_t ak_lmhead_grad_workspace_bytes(int64_t n_rows, int64_t vocab, int64_t d);
+
+/* grad_hidden[t, :] = sum_v grad_logits[t, v] weight[v, :]; grad_hidden
+ * [n_rows, d] rows of ld_gh (>= d). */
+int ak_lmhead_grad_hidden(const void* grad_logits, int64_t ld_gl, const void* weight,
+                          int64_t ld_w, void* grad_hidden, int64_t ld_gh, int64_t n_rows,
+                          int64_t vocab, int64_t d, int out_mode, void* workspace,
+                          size_t workspace_bytes, int dtype, void* stream);
+
+/* grad_weight[v, :] = sum_t grad_logits[t, v] hidden[t, :]; grad_weight
+ * [vocab, d] rows of ld_gw (>= d). */
+int ak_lmhead_grad_weight(const void* grad_logits, int64_t ld_gl, const void* hidden,
+                          int64_t ld_h, void* grad_weight, int64_t ld_gw, int64_t n_rows,
+                          int64_t vocab, int64_t d, int out_mode, void* workspace,
+                          size_t workspace_bytes, int dtype, void* stream);
+
+/*
  * Mamba-1 selective scan forward (selective_scan_fn semantics).
  * Replaces selective_scan_cuda.fwd, external/mamba/csrc/selective_scan/
  * selective_scan.cpp:227-335, as called by

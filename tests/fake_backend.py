@@ -146,6 +146,21 @@ def _lmhead_bwd_range(hidden, weight, targets, lse, grad_loss, denom, grad_logit
     grad_logits.copy_(full[:, v_begin:v_begin + grad_logits.shape[1]])
 
 
+def _grad_gemm_out(out, val, out_mode):
+    if out_mode == 2:
+        out.add_(val.float())
+    else:
+        out.copy_(val.to(out.dtype))
+
+
+def _grad_hidden(grad_logits, weight, out, out_mode, workspace):
+    _grad_gemm_out(out, grad_logits.double() @ weight.double(), out_mode)
+
+
+def _grad_weight(grad_logits, hidden, out, out_mode, workspace):
+    _grad_gemm_out(out, grad_logits.double().t() @ hidden.double(), out_mode)
+
+
 def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, out_prez=None,
           chunk_states=None, checkpoints=None):
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
@@ -196,6 +211,9 @@ def install(monkeypatch):
     monkeypatch.setattr(_lib, "lmhead_ce_workspace_bytes", lambda n, v: 256)
     monkeypatch.setattr(_lib, "lmhead_ce_bwd", _lmhead_bwd)
     monkeypatch.setattr(_lib, "lmhead_ce_bwd_range", _lmhead_bwd_range)
+    monkeypatch.setattr(_lib, "lmhead_grad_workspace_bytes", lambda n, v, d: 256)
+    monkeypatch.setattr(_lib, "lmhead_grad_hidden", _grad_hidden)
+    monkeypatch.setattr(_lib, "lmhead_grad_weight", _grad_weight)
     monkeypatch.setattr(_lib, "selective_scan", _scan)
     monkeypatch.setattr(_lib, "selective_scan_bwd", _scan_bwd)
     monkeypatch.setattr(_lib, "diag_scan", _diag)

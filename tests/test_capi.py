@@ -84,6 +84,27 @@ def test_argument_errors_return_codes(lib):
     assert lib.ak_rmsnorm_fwd(None, None, None, 0, 8, 8, 8, 1e-6, 0, None) == 0
 
 
+def test_lmhead_grad_gemm_workspace_and_argument_errors(lib):
+    """The gradient GEMMs' workspace holds the fp32 partial tiles of the
+    K-split work; with no GPU the CU count defaults to MI355X's 256. At the C4
+    shape grad_hidden's 96 tiles run 8 K ranges each (the larger of the two
+    GEMMs' needs)."""
+    assert _lib.lmhead_grad_workspace_bytes(8192, 50304, 768) == 96 * 8 * 256 * 256 * 4
+    assert _lib.lmhead_grad_workspace_bytes(0, 10, 64) == 0
+    f = lib.ak_lmhead_grad_hidden
+    # (grad_logits, ld_gl, operand, ld_op, out, ld_out, n_rows, vocab, d, out_mode, ws, ws_bytes, dtype, stream)
+    rc = f(None, 1024, None, 64, None, 64, 8, 1000, 64, 0, None, 0, 0, None)
+    assert rc == -2 and b"dtype" in lib.ak_last_error()
+    rc = f(None, 1024, None, 96, None, 96, 8, 1000, 96, 0, None, 0, 2, None)
+    assert rc == -2 and b"multiple of 64" in lib.ak_last_error()
+    rc = f(None, 1000, None, 64, None, 64, 8, 1000, 64, 0, None, 0, 2, None)   # pitch < round_up(vocab, 64)
+    assert rc == -1 and b"pitch" in lib.ak_last_error()
+    rc = f(None, 1024, None, 64, None, 64, 8, 1000, 64, 3, None, 0, 2, None)
+    assert rc == -1 and b"out_mode" in lib.ak_last_error()
+    rc = lib.ak_lmhead_grad_weight(None, 1024, None, 64, None, 64, 8, 1000, 64, 0, None, 0, 2, None)
+    assert rc == -1 and b"null" in lib.ak_last_error()
+
+
 def test_selective_scan_bwd_workspace_and_argument_errors(lib):
     """Workspace query of the Mamba-1 backward (saved states every 16 steps,
     per-tile dB / dC partials, per-batch dA / dD / ddelta_bias partials, each
