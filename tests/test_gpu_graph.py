@@ -48,7 +48,12 @@ def test_capture_and_replay_all_families():
     ws_l = torch.empty(_lib.lmhead_ce_workspace_bytes(512, 3000), dtype=torch.uint8, device=DEV)
     one = torch.ones(1, device=DEV)
     den = torch.full((1,), 512.0, device=DEV)
-    dz_l = torch.empty(512, 3000, dtype=torch.bfloat16, device=DEV)
+    # dlogits in a buffer whose zeroed padding covers vocab rounded up to 64
+    # (what the gradient GEMMs read)
+    dz_l = torch.zeros(512, 3008 + 64, dtype=torch.bfloat16, device=DEV)[:, :3000]
+    g_h = torch.empty(512, 256, dtype=torch.bfloat16, device=DEV)
+    g_w = torch.empty(3000, 256, dtype=torch.bfloat16, device=DEV)
+    ws_g = torch.empty(_lib.lmhead_grad_workspace_bytes(512, 3000, 256), dtype=torch.uint8, device=DEV)
     # Mamba-1 scan
     u = d(torch.randn(2, 32, 256, generator=g).bfloat16())
     delta = d(F.softplus(0.5 * torch.randn(2, 32, 256, generator=g) - 2))
@@ -72,12 +77,14 @@ def test_capture_and_replay_all_families():
         _lib.ce_fwd(logits, t, losses, lse, None, None, None, 30.0, -100, 0.1, 1.0)
         _lib.lmhead_ce(hid, W, tt, loss, lse2, None, nv, ws_l, -100, 0.0, 0.0)
         _lib.lmhead_ce_bwd(hid, W, tt, lse2, one, den, dz_l, -100)
+        _lib.lmhead_grad_hidden(dz_l, W, g_h, _lib.GEMM_OUT_DTYPE, ws_g)
+        _lib.lmhead_grad_weight(dz_l, hid, g_w, _lib.GEMM_OUT_DTYPE, ws_g)
         _lib.selective_scan(u, delta, A, B, C, Dv, z, None, out, None, False)
         _lib.selective_scan_bwd(u, delta, A, B, C, Dv, z, None, dout, du, ddelta, dA, dB, dC, dD,
                                 dzs, None, False)
 
-    outs = [y1, h2, y2, gx, gw, ys, losses, lse, loss, lse2, nv, dz_l, out, du, ddelta, dA, dB, dC,
-            dD, dzs]
+    outs = [y1, h2, y2, gx, gw, ys, losses, lse, loss, lse2, nv, dz_l, g_h, g_w, out, du, ddelta, dA,
+            dB, dC, dD, dzs]
     say("graph: eager reference")
     run()
     torch.cuda.synchronize()
