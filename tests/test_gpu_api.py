@@ -38,8 +38,24 @@ def test_ops_forward_backward(dtype):
     for a, b in ((x.grad, xr.grad), (w.grad, wr.grad)):
         rel = float((a.double().cpu() - b).norm() / b.norm())
         assert rel < tol, rel
-    y = torch.ops.autokernel.rmsnorm(x.detach(), w.detach())
-    assert y.dtype == dtype and y.shape == x.shape
+    # the plain RMSNorm op: values against the oracle, gradients against
+    # float64 autograd of the reference formula
+    from oracle import ops
+    xa = x0.to(dtype).to(DEV).requires_grad_()
+    wa = w0.to(dtype).to(DEV).requires_grad_()
+    y = torch.ops.autokernel.rmsnorm(xa, wa, 1e-6)
+    assert y.dtype == dtype and y.shape == xa.shape
+    want = ops.rmsnorm_f32_ref(x0.to(dtype), w0.to(dtype), 1e-6)  # fp32, rounded once
+    ytol = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1.6e-2}[dtype]  # about 1 ulp
+    assert torch.allclose(y.detach().cpu().double(), want.double(), rtol=ytol, atol=ytol)
+    (y.float() * gy.to(DEV)).sum().backward()
+    xb = x0.to(dtype).double().requires_grad_()
+    wb = w0.to(dtype).double().requires_grad_()
+    yb = xb / torch.sqrt(xb.pow(2).mean(-1, keepdim=True) + 1e-6) * wb
+    (yb * gy.double()).sum().backward()
+    for a, b in ((xa.grad, xb.grad), (wa.grad, wb.grad)):
+        rel = float((a.double().cpu() - b).norm() / b.norm())
+        assert rel < tol, rel
 
 
 def test_autocast_follows_dtype():

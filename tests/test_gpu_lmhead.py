@@ -131,6 +131,13 @@ def test_c4_full_size():
     _, rlse, rl = ops.lmhead_ce_ref(c["h"][idx], c["W"], t[idx])
     assert torch.allclose(lse.cpu()[idx].double(), rlse.double(), rtol=1e-4)
     assert torch.allclose(losses.cpu()[idx].double(), rl.double(), rtol=1e-3, atol=1e-3)
+    # every row's logsumexp against an fp32 GPU reference (fp32 GEMM of the
+    # bf16 operands in 1024-row chunks, then logsumexp): the oracle above
+    # covers a subset in float64, this one all 8192 rows
+    hd, Wd = c["h"].to(DEV).float(), c["W"].to(DEV).float().contiguous()
+    ref_all = torch.cat([torch.logsumexp(hd[i:i + 1024] @ Wd.t(), dim=-1) for i in range(0, 8192, 1024)])
+    assert torch.allclose(lse.double(), ref_all.double(), rtol=1e-4, atol=0.0)
+    del hd, Wd
     # the mean over all rows: GPU lse with exact target logits from the CPU
     tv = t.clamp(min=0)
     xt = (c["h"].float() * c["W"][tv].float()).sum(-1)
