@@ -114,6 +114,23 @@ def test_grad_gemms_c4_shape_and_determinism():
     _check(gw, torch.mm(dlt, h.float()), _bound(dlt, h), torch.bfloat16, "c4 grad_weight")
 
 
+def test_grad_gemms_c4_homogeneous_bitwise():
+    """Both GEMMs are linear in dlogits and doubling it is exact through the
+    fp32 accumulation, the K-split partial sums and the final rounding:
+    gemm(2 dlogits) == 2 gemm(dlogits) bit for bit at the C4 shape."""
+    need_gpu()
+    from kernels.hip import _lib
+    n, vocab, d = 8192, 50304, 768
+    gen = torch.Generator().manual_seed(6)
+    dl, W, h, gh, gw = _run_pair(n, vocab, d, torch.bfloat16, gen)
+    ws = torch.empty(_lib.lmhead_grad_workspace_bytes(n, vocab, d), dtype=torch.uint8, device=DEV)
+    dl2 = (2 * dl).contiguous()
+    gh2, gw2 = torch.empty_like(gh), torch.empty_like(gw)
+    _lib.lmhead_grad_hidden(dl2, W, gh2, 0, ws)
+    _lib.lmhead_grad_weight(dl2, h, gw2, 0, ws)
+    assert torch.equal(gh2, 2 * gh) and torch.equal(gw2, 2 * gw)
+
+
 def test_grad_gemm_workspace_too_small_is_an_error():
     need_gpu()
     from kernels.hip import _lib

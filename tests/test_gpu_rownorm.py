@@ -49,6 +49,24 @@ def test_c3_fused_bf16_full():
     assert torch.equal(y1.cpu(), y.cpu())
 
 
+def test_c1_c3_weight_homogeneity_bitwise():
+    """Full C1 and C3: y is linear in the weight and doubling it is exact in the
+    kernel's fp32 arithmetic and in the final rounding, so y(2w) == 2 y(w)
+    bit for bit; new_residual does not depend on the weight."""
+    need_gpu()
+    import bench
+    from kernels.hip import fused_residual_add_rmsnorm as frn
+    from kernels.hip import rmsnorm
+    c1 = bench.gen_c1()
+    x, w = c1["x"].to(DEV), c1["w"].to(DEV)
+    assert torch.equal(rmsnorm.kernel_fn(x, 2 * w, c1["eps"]), 2 * rmsnorm.kernel_fn(x, w, c1["eps"]))
+    c3 = bench.gen_c3()
+    x, r, w = c3["x"].to(DEV), c3["r"].to(DEV), c3["w"].to(DEV)
+    h1, y1 = frn.kernel_fn_dual(x, r, w, eps=c3["eps"])
+    h2, y2 = frn.kernel_fn_dual(x, r, 2 * w, eps=c3["eps"])
+    assert torch.equal(h1, h2) and torch.equal(y2, 2 * y1)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("cols", [1, 7, 64, 100, 512, 768, 1000, 2048, 4096, 4104, 8192, 16384, 40000, 70000])
 def test_rownorm_shapes(dtype, cols):

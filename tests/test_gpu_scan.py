@@ -141,6 +141,20 @@ def test_c5_full_size():
     assert torch.allclose(out[:1, sl].float(), tref.float(), rtol=1e-2, atol=1e-4)
 
 
+def test_c5_homogeneous_in_u_bitwise():
+    """Full C5: the output is homogeneous of degree 1 in u, and scaling u by 2
+    is exact at every step (delta u B, the state FMA, the sum over states,
+    D u and the gate all scale by a power of two without new rounding), so
+    scan(2u) must equal 2 scan(u) bit for bit."""
+    need_gpu()
+    import bench
+    c = bench.gen_c5()
+    say("C5 homogeneity in u")
+    out = _gpu(c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"], None, False, last=False)
+    out2 = _gpu(2 * c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"], None, False, last=False)
+    assert torch.equal(out2, 2 * out)
+
+
 def test_split_equivalence_on_gpu():
     """scan(L) == scan(L/2) continued from its last_state (closed-form invariant)."""
     need_gpu()
