@@ -192,6 +192,24 @@ def test_c5_shape_backward():
         assert bool(((gv - rv).abs() <= at + rt * rv.abs()).all()), name
 
 
+def test_c5_backward_homogeneous_in_dout_bitwise():
+    """Full C5 shape: every gradient is linear in dout and doubling dout is
+    exact through the reverse recurrence, the sums over states, channels and
+    the batch and the final rounding, so grads(2 dout) == 2 grads(dout) bit
+    for bit (all outputs, all channels)."""
+    need_gpu()
+    import bench
+    c = bench.gen_c5()
+    g = torch.Generator().manual_seed(3)
+    dout = torch.randn(c["u"].shape, generator=g).bfloat16()
+    say("C5-shape mamba backward homogeneity in dout")
+    args = (c["u"], c["delta"], c["A"], c["B"], c["C"], c["D"], c["z"], None)
+    one = _gpu_grads(*args, dout, False)
+    two = _gpu_grads(*args, 2 * dout, False)
+    for a, b in zip(one, two):
+        assert (a is None and b is None) or torch.equal(b, 2 * a)
+
+
 @pytest.mark.parametrize("seqlen,fast", [(4196, False), (4096, True)])
 def test_binding_fwd_chunk_states_and_prez(seqlen, fast):
     """kernels.hip.selective_scan_cuda.fwd on the GPU: ``out`` (before the
