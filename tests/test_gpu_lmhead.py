@@ -148,6 +148,21 @@ def test_c4_full_size():
     assert torch.equal(lse2, lse) and torch.equal(loss2, loss)
 
 
+def test_c4_token_permutation_equivariance_bitwise():
+    """Full C4: each token's logits, logsumexp and loss are computed by the same
+    operations in the same order wherever the token sits (every token tile is
+    whole at 8192 tokens), so permuting the tokens permutes lse and the per-row
+    losses bit for bit."""
+    need_gpu()
+    import bench
+    c = bench.gen_c4()
+    perm = torch.randperm(8192, generator=torch.Generator().manual_seed(9))
+    _, lse, _, losses = _run(c["h"], c["W"], c["t"])
+    _, lse_p, _, losses_p = _run(c["h"][perm], c["W"], c["t"][perm])
+    assert torch.equal(lse_p.cpu(), lse.cpu()[perm])
+    assert torch.equal(losses_p.cpu(), losses.cpu()[perm])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("softcap,ls,zw", [(0.0, 0.0, 0.0), (0.0, 0.0, 1e-4), (20.0, 0.0, 0.0),
                                            (30.0, 0.0, 1e-4), (0.0, 0.1, 0.0), (30.0, 0.1, 1e-4)])
