@@ -488,6 +488,22 @@ def test_c4_full_size_backward():
     assert rel < 5e-3, rel
 
 
+def test_c4_backward_homogeneous_in_grad_loss_bitwise():
+    """Full C4: dlogits, and so both gradients, are linear in the upstream
+    gradient of the loss; doubling it is exact through the dlogits epilogue,
+    the GEMMs' fp32 accumulation, their partial sums and the rounding."""
+    need_gpu()
+    import bench
+    from kernels.hip.chunked_linear_cross_entropy import lmhead_ce_backward
+    c = bench.gen_c4()
+    h, W, t = c["h"].to(DEV), c["W"].to(DEV), c["t"].to(DEV)
+    _, lse, nv, _ = _run(c["h"], c["W"], c["t"])
+    denom = nv.to(torch.float32).clamp(min=1.0)
+    gh1, gw1 = lmhead_ce_backward(h, W, t, lse, denom, torch.ones((), device=DEV))
+    gh2, gw2 = lmhead_ce_backward(h, W, t, lse, denom, torch.full((), 2.0, device=DEV))
+    assert torch.equal(gh2, 2 * gh1) and torch.equal(gw2, 2 * gw1)
+
+
 @pytest.mark.parametrize("ls", [0.0, 0.1])
 def test_fused_and_row_chunked_softcap_paths_agree(ls):
     """The same softcapped (and label-smoothed) loss and gradients from the

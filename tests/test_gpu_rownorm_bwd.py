@@ -158,6 +158,25 @@ def test_c3_shape_fused_backward():
     _check_gw(gw, hidden, c["w"], gn, c["eps"])
 
 
+def test_c3_shape_fused_backward_homogeneous_bitwise():
+    """Full C3 shape: grad_x and grad_weight are linear in the upstream
+    gradients and doubling both is exact through the row sums, the fixed-order
+    column sums and the final rounding: grads(2 gh, 2 gn) == 2 grads(gh, gn)."""
+    need_gpu()
+    import bench
+    from kernels.hip import fused_residual_rmsnorm_backward as frb
+    c = bench.gen_c3()
+    g = torch.Generator().manual_seed(2)
+    gh = torch.randn(16384, 4096, generator=g).bfloat16().to(DEV)
+    gn = torch.randn(16384, 4096, generator=g).bfloat16().to(DEV)
+    hidden, _ = ops.fused_residual_add_rmsnorm_ref(c["x"], c["r"], c["w"], c["eps"])
+    hidden, w = hidden.to(DEV), c["w"].to(DEV)
+    say("C3-shape fused backward homogeneity")
+    gx1, _, gw1 = frb.kernel_fn(hidden, w, gh, gn, eps=c["eps"])
+    gx2, _, gw2 = frb.kernel_fn(hidden, w, 2 * gh, 2 * gn, eps=c["eps"])
+    assert torch.equal(gx2, 2 * gx1) and torch.equal(gw2, 2 * gw1)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_custom_op_autograd_uses_kernels(dtype):
     """torch.ops.autokernel.{rmsnorm, fused_res_rmsnorm} backward on the GPU
