@@ -996,6 +996,22 @@ scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restri
     const float4* part = reinterpret_cast<const float4*>(is_c ? dC_part : dB_part) + e4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     int t = 0;
+    // 16 loads in flight per lane: at 2 waves per SIMD (the C5 shape) the
+    // latency of each round is exposed, so fewer, wider rounds
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4* pv = reinterpret_cast<const f32x4*>(part);
+    for (; t + 16 <= tiles; t += 16) {
+      f32x4 v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = __builtin_nontemporal_load(pv + (int64_t)(t + k) * n4);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        acc.x += v[k][0];
+        acc.y += v[k][1];
+        acc.z += v[k][2];
+        acc.w += v[k][3];
+      }
+    }
     for (; t + 8 <= tiles; t += 8) {
       float4 v[8];
 #pragma unroll

@@ -11,14 +11,18 @@
 //   whole pass and the tile offset in the scalar offset: no 64-bit address
 //   arithmetic per tile (the general pass issues 48 scalar loads per lane
 //   and tile, each with its own address computation);
-// * the broadcast sources (delta, u, dout, z of steps 4n .. 4n + 3) arrive in
-//   one 8/16-byte load each;
+// * a step's delta', delta' u and dy are formed once, by the lane that also
+//   writes the step's du / ddelta, and reach the block's 16 state lanes
+//   through a small LDS table read back as float4 broadcasts: the multiplies
+//   by them are plain VALU operations rather than DPP row broadcasts, which
+//   take about twice the issue time on gfx950; each block's loads are issued
+//   one block ahead;
 // * the gate and the saved-states dz (kDz: the forward's pre-gate output is
 //   given, so dz is formed here) are compile-time choices, and whole tiles
 //   need no bounds tests, so each 16-step block is one basic block the
 //   scheduler can interleave.
 // At the C5 shape (batch 4, dim 2048, seqlen 4096, dstate 16) the pass takes
-// 471 us against 579 us for the general one on the same box.
+// 457 us against 579 us for the general one on the same box.
 #include "scan_buffer.h"
 
 namespace ak {
@@ -75,10 +79,6 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
   const Rsrc rs_ck = make_rsrc(p.ck + (int64_t)b * p.nchunks * ck_cs + (int64_t)d0 * p.dstate,
                                (uint32_t)(((int64_t)(p.nchunks - 1) * ck_cs + kCh * p.dstate) * 4));
 
-  const uint32_t vo_d4 = (uint32_t)(wc * p.d_ds + 4 * n) * sizeof(TD);
-  const uint32_t vo_u4 = (uint32_t)(wc * p.u_ds + 4 * n) * sizeof(TU);
-  const uint32_t vo_g4 = (uint32_t)(wc * p.go_ds + 4 * n) * sizeof(TU);
-  const uint32_t vo_z4 = kGate ? (uint32_t)(wc * p.z_ds + 4 * n) * sizeof(TU) : vo_u4;
   const uint32_t vo_d1 = (uint32_t)(wc * p.d_ds + n) * sizeof(TD);
   const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);
   const uint32_t vo_g1 = (uint32_t)(wc * p.go_ds + n) * sizeof(TU);
@@ -93,73 +93,80 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
 
   float* tb = tbuf[wave];
   float* wb = wbuf[wave];
+  // Per-wave tbuf use, channel c at c * kTC: the (g B, A w)[j][n] transpose
+  // in floats 0..31 of each 36-float step row; the block's per-step table
+  // (delta', delta' u, dy of its 16 steps, float4 slot s = 4 q + i: quantity
+  // q, steps 4 i .. 4 i + 3) in the row pads, floats 32..35 of row s (row
+  // s + 1 for channels 2, 3, so the four channels' slots fall on disjoint
+  // banks).
+  const int tab = c * kTC + (c >= 2 ? kTJ : 0) + 32;
 
-  struct Regs {
-    Raw4<TBC> bv, cv;
-    Raw4<TD> dv;
-    Raw4<TU> uv, gv, zv;
-    Raw1<TD> dr[4];
-    Raw1<TU> ur[4], gr[4], zr[4], yr[4];
-    uint32_t ck[4];
+  // one block's per-step values (step 16 blk + n of channel wc) and the
+  // state before the block
+  struct Blk {
+    Raw1<TD> dr;
+    Raw1<TU> ur, gr, zr, yr;
+    uint32_t ck;
   };
-  auto load_regs = [&](int t, Regs& r) {
-    const uint32_t l0 = (uint32_t)t * kScanT;
-    r.bv = bload4<TBC>(rs_B, vo_B, l0 * sizeof(TBC));
-    r.cv = bload4<TBC>(rs_C, vo_C, l0 * sizeof(TBC));
-    r.dv = bload4<TD>(rs_d, vo_d4, l0 * sizeof(TD));
-    r.uv = bload4<TU>(rs_u, vo_u4, l0 * sizeof(TU));
-    r.gv = bload4<TU>(rs_go, vo_g4, l0 * sizeof(TU));
-    if constexpr (kGate) r.zv = bload4<TU>(rs_z, vo_z4, l0 * sizeof(TU));
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk) {
-      r.dr[blk] = bload1<TD>(rs_d, vo_d1 + 16 * blk * sizeof(TD), l0 * sizeof(TD));
-      r.ur[blk] = bload1<TU>(rs_u, vo_u1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
-      r.gr[blk] = bload1<TU>(rs_go, vo_g1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
-      if constexpr (kGate) r.zr[blk] = bload1<TU>(rs_z, vo_z1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
-      if constexpr (kGate && kDz) r.yr[blk] = bload1<TU>(rs_y, vo_o1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
-      const uint32_t chunk = (l0 + 16 * blk) / kCk;
-      r.ck[blk] = __builtin_amdgcn_raw_buffer_load_b32(rs_ck, (int)vo_ck, (int)(chunk * (uint32_t)ck_cs * 4u), 0);
-    }
+  auto load_blk = [&](int t, int blk, Blk& r) {
+    const uint32_t l = (uint32_t)(t * kScanT + 16 * blk);
+    r.dr = bload1<TD>(rs_d, vo_d1, l * sizeof(TD));
+    r.ur = bload1<TU>(rs_u, vo_u1, l * sizeof(TU));
+    r.gr = bload1<TU>(rs_go, vo_g1, l * sizeof(TU));
+    if constexpr (kGate) r.zr = bload1<TU>(rs_z, vo_z1, l * sizeof(TU));
+    if constexpr (kGate && kDz) r.yr = bload1<TU>(rs_y, vo_o1, l * sizeof(TU));
+    r.ck = __builtin_amdgcn_raw_buffer_load_b32(rs_ck, (int)vo_ck, (int)((l / kCk) * (uint32_t)ck_cs * 4u), 0);
   };
 
   float gs = 0.0f, a_next = 0.0f, dA_acc = 0.0f, dD_acc = 0.0f, dbias_acc = 0.0f;
   const int nt = p.seqlen / kScanT;
-  Regs cur, nxt;
-  load_regs(nt - 1, cur);
+  Raw4<TBC> bv = bload4<TBC>(rs_B, vo_B, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
+  Raw4<TBC> cv = bload4<TBC>(rs_C, vo_C, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
+  Blk pb;
+  load_blk(nt - 1, 3, pb);
   for (int t = nt - 1; t >= 0; --t) {
     const int l0 = t * kScanT;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const bool ok = sn < p.dstate;
-      Bs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(cur.bv, k) : 0.0f;
-      Cs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(cur.cv, k) : 0.0f;
+      Bs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(bv, k) : 0.0f;
+      Cs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(cv, k) : 0.0f;
     }
-    float bd[4], bdu[4], bdy[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float dv = raw4_f32<TD>(cur.dv, k) + dbias;
-      if constexpr (kSoftplus) dv = softplus_f32(dv);
-      bd[k] = dv;
-      bdu[k] = bd[k] * raw4_f32<TU>(cur.uv, k);
-      const float go = raw4_f32<TU>(cur.gv, k);
-      if constexpr (kGate) {
-        const float zv = raw4_f32<TU>(cur.zv, k);
-        bdy[k] = go * zv * sigmoid_f32(zv);
-      } else {
-        bdy[k] = go;
-      }
+    {
+      const uint32_t ln = (uint32_t)max(t - 1, 0) * kScanT;
+      bv = bload4<TBC>(rs_B, vo_B, ln * sizeof(TBC));
+      cv = bload4<TBC>(rs_C, vo_C, ln * sizeof(TBC));
     }
-    asm volatile("s_nop 1"
-                 : "+v"(bd[0]), "+v"(bd[1]), "+v"(bd[2]), "+v"(bd[3]), "+v"(bdu[0]), "+v"(bdu[1]),
-                   "+v"(bdu[2]), "+v"(bdu[3]), "+v"(bdy[0]), "+v"(bdy[1]), "+v"(bdy[2]), "+v"(bdy[3]));
-    load_regs(max(t - 1, 0), nxt);
     asm volatile("" ::: "memory");
     __syncthreads();
 
     auto block = [&](auto blk_c) {
       constexpr int BLK = decltype(blk_c)::value;
-      const float hstart = n_ok ? __builtin_bit_cast(float, cur.ck[BLK]) : 0.0f;
+      const Blk cb = pb;
+      // the next block's values: one block (about 2 us) of latency cover
+      if constexpr (BLK > 0) load_blk(t, BLK - 1, pb);
+      else load_blk(max(t - 1, 0), 3, pb);
+      asm volatile("" ::: "memory");
+      // step 16 BLK + n: delta', dy = dout silu(z) (dout without a gate)
+      const float go = raw_f32<TU>(cb.gr);
+      float dyv = go, zv = 0.0f, sg = 0.0f;
+      if constexpr (kGate) {
+        zv = raw_f32<TU>(cb.zr);
+        sg = sigmoid_f32(zv);
+        dyv = go * zv * sg;
+      }
+      const float uv = raw_f32<TU>(cb.ur);
+      const float x = raw_f32<TD>(cb.dr) + dbias;
+      const float dlt = kSoftplus ? softplus_f32(x) : x;
+      tb[tab + (n >> 2) * kTJ + (n & 3)] = dlt;
+      tb[tab + (4 + (n >> 2)) * kTJ + (n & 3)] = dlt * uv;
+      tb[tab + (8 + (n >> 2)) * kTJ + (n & 3)] = dyv;
+      __builtin_amdgcn_wave_barrier();
+      auto tab4 = [&](int slot) { return *reinterpret_cast<const float4*>(&tb[tab + slot * kTJ]); };
+      auto el = [](const float4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; };
+
+      const float hstart = n_ok ? __builtin_bit_cast(float, cb.ck) : 0.0f;
       float bt[16], ct[16], as[16], hs[16];
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -167,12 +174,15 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
         ct[j] = Cs[n * kBStride + 16 * BLK + j];
       }
       float xv[16];
-      static_for<0, 16>([&](auto j_c) {
-        constexpr int J = decltype(j_c)::value;
-        constexpr int kSrc = 4 * BLK + J / 4;
-        as[J] = mul_bcast<kSrc>(bd[J % 4], a_scaled);
-        xv[J] = mul_bcast<kSrc>(bdu[J % 4], bt[J]);
-      });
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float4 vd = tab4(i), vu = tab4(4 + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          as[4 * i + k] = el(vd, k) * a_scaled;
+          xv[4 * i + k] = el(vu, k) * bt[4 * i + k];
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 16; ++j) as[j] = __builtin_amdgcn_exp2f(as[j]);
       float h = hstart;
@@ -182,19 +192,26 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
         hs[j] = h;
       }
       float pB = 0.0f, pC = 0.0f;
+      asm volatile("" ::: "memory");  // the reverse sweep reads the table again
+      float4 gd, gu, gy;
       static_for<0, 16>([&](auto i_c) {
         constexpr int J = 15 - decltype(i_c)::value;
-        constexpr int kSrc = 4 * BLK + J / 4;
-        constexpr int K = J % 4;
-        gs = fmaf(gs, a_next, mul_bcast<kSrc>(bdy[K], ct[J]));
+        if constexpr (J % 4 == 3) {
+          gd = tab4(J / 4);
+          gu = tab4(4 + J / 4);
+          gy = tab4(8 + J / 4);
+        }
+        const float sdj = el(gd, J % 4), suj = el(gu, J % 4), syj = el(gy, J % 4);
+        gs = fmaf(gs, a_next, syj * ct[J]);
         a_next = as[J];
         const float hp = J > 0 ? hs[J > 0 ? J - 1 : 0] : hstart;
         const float w = gs * (as[J] * hp);
-        const float gB = gs * bt[J];
-        dA_acc = fma_bcast<kSrc>(bd[K], w, dA_acc);
-        const float cB = mul_bcast<kSrc>(bdu[K], gs);
-        const float cC = mul_bcast<kSrc>(bdy[K], hs[J]);
-        *reinterpret_cast<float2*>(&tb[c * kTC + J * kTJ + 2 * n]) = make_float2(gB, a_nat * w);
+        // dA += delta' w as an opaque FMA: as plain code the scheduler sinks the
+        // whole tile's chain to its end and keeps every w live (274 VGPRs)
+        asm("v_fmac_f32 %0, %1, %2" : "+v"(dA_acc) : "v"(sdj), "v"(w));
+        const float cB = suj * gs;
+        const float cC = syj * hs[J];
+        *reinterpret_cast<float2*>(&tb[c * kTC + J * kTJ + 2 * n]) = make_float2(gs * bt[J], a_nat * w);
         if constexpr (J % 2 == 1) {
           pB = cB;
           pC = cC;
@@ -205,6 +222,8 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
         }
       });
       __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+      // lane (c, j = n): sum(g B) and sum(A w) over the states of step 16 BLK + n
       float sgb = 0.0f, saw = 0.0f;
 #pragma unroll
       for (int s4 = 0; s4 < 8; ++s4) {
@@ -214,20 +233,10 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
       }
       __builtin_amdgcn_wave_barrier();
       const uint32_t lo = (uint32_t)(l0 + 16 * BLK);
-      const float go = raw_f32<TU>(cur.gr[BLK]);
-      float dyv = go;
-      if constexpr (kGate) {
-        const float zv = raw_f32<TU>(cur.zr[BLK]);
-        const float sg = sigmoid_f32(zv);
-        dyv = go * zv * sg;
-        if constexpr (kDz)
-          bstore1_at<TU>(rs_dz, vo_o1, lo * sizeof(TU), go * raw_f32<TU>(cur.yr[BLK]) * sg * fmaf(zv, 1.0f - sg, 1.0f));
-      }
-      const float uv = raw_f32<TU>(cur.ur[BLK]);
-      const float x = raw_f32<TD>(cur.dr[BLK]) + dbias;
-      float dlt = x, ddl = fmaf(uv, sgb, saw);
+      if constexpr (kGate && kDz)
+        bstore1_at<TU>(rs_dz, vo_o1, lo * sizeof(TU), go * raw_f32<TU>(cb.yr) * sg * fmaf(zv, 1.0f - sg, 1.0f));
+      float ddl = fmaf(uv, sgb, saw);
       if constexpr (kSoftplus) {
-        dlt = softplus_f32(x);
         if (x <= 20.0f) ddl *= sigmoid_f32(x);
       }
       bstore1_at<TU>(rs_du, vo_o1, lo * sizeof(TU), fmaf(dskip, dyv, dlt * sgb));
@@ -258,7 +267,6 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
         }
       }
     }
-    cur = nxt;
   }
   if (n_ok) p.dA_part[((int64_t)b * p.dim + d) * p.dstate + n] = dA_acc;
   dD_acc = row16_sum(dD_acc);
