@@ -557,6 +557,22 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int row0 = blockIdx.x * kRowsPerBlock;
+  const int r = threadIdx.x % kRowsPerBlock;
+  const int grp = threadIdx.x / kRowsPerBlock;
+  const int row = row0 + r;
+  const int n_part = 2 * n_vt;
+
+  // With up to kAllPart partials per thread (vocab up to 65,536) all of them
+  // are loaded before the target logits' loads: both sets are then in flight
+  // at once instead of one round trip after another.
+  constexpr int kAllPart = 32;
+  const bool all_at_once = n_part <= kAllPart * kRowGroups;
+  MSPair pre[kAllPart];
+  if (all_at_once && row < n_rows) {
+#pragma unroll
+    for (int k = 0; k < kAllPart; ++k)
+      if (grp + k * kRowGroups < n_part) pre[k] = part[(int64_t)(grp + k * kRowGroups) * n_rows + row];
+  }
 
   // target logits of rows row0 + wave * kPerWave + q
   {
@@ -613,14 +629,18 @@ lmhead_ce_rows_kernel(const T* __restrict__ H, const T* __restrict__ W,
     }
   }
 
-  const int r = threadIdx.x % kRowsPerBlock;
-  const int grp = threadIdx.x / kRowsPerBlock;
-  const int row = row0 + r;
   MSPair st{-INFINITY, 0.0f};
   float zs = 0.0f;  // label smoothing: sum of the (capped) logits, fixed order
-  if (row < n_rows) {
+  if (row < n_rows && all_at_once) {
+    // partials grp, grp + kRowGroups, ... merged in that order
+#pragma unroll
+    for (int k = 0; k < kAllPart; ++k)
+      if (grp + k * kRowGroups < n_part) st = ms_merge(st, pre[k]);
+    if (zsum) {
+      for (int v = grp; v < n_part; v += kRowGroups) zs += zsum[(int64_t)v * n_rows + row];
+    }
+  } else if (row < n_rows) {
     // 8 partials in flight per thread, then merged in order
-    const int n_part = 2 * n_vt;
     for (int v0 = grp; v0 < n_part; v0 += 8 * kRowGroups) {
       MSPair buf[8];
 #pragma unroll
@@ -670,6 +690,7 @@ lmhead_ce_mean_kernel(const float* __restrict__ losses, const int64_t* __restric
                       int64_t ignore_index) {
   float sum = 0.0f;
   int cnt = 0;
+#pragma unroll 8
   for (int i = threadIdx.x; i < n_rows; i += 1024) {
     sum += losses[i];
     cnt += targets[i] != ignore_index;
