@@ -30,10 +30,11 @@ def _run(h, W, t, ignore_index=-100, softcap=0.0, ls=0.0):
 # re-reads), vocab % 128 != 0 (element-wise tail mask), vocab % 128 == 0 but
 # not % 256 (shifted tail tile skipping a whole 128-row half), token tails,
 # and 1, 2, 3 and more 64-wide K blocks per tile (the LDS ring then looks
-# up to three tiles ahead).
+# up to three tiles ahead). Vocab 70,000 has more tile partials per row than
+# the row kernel loads at once (its looped merge).
 @pytest.mark.parametrize("n,vocab,d", [(1, 1, 64), (5, 300, 64), (300, 1000, 128), (257, 4097, 768),
                                        (512, 50304, 768), (1000, 256, 192), (300, 1152, 128),
-                                       (700, 640, 64), (260, 384, 64), (2000, 2432, 192)])
+                                       (700, 640, 64), (260, 384, 64), (2000, 2432, 192), (64, 70000, 64)])
 def test_lmhead_ce_matches_oracle(dtype, n, vocab, d):
     need_gpu()
     g = torch.Generator().manual_seed(n * 7 + vocab)

@@ -95,10 +95,12 @@ def test_reference_grid_backward(itype, groups, seqlen):
 @pytest.mark.parametrize("batch,dim,dstate,seqlen,groups,softplus,opts", [
     (1, 1, 1, 1, 1, True, "Dzb"), (3, 3, 5, 63, 1, False, ""), (2, 20, 16, 64, 1, True, "D"),
     (2, 40, 16, 100, 2, True, "zb"), (1, 16, 7, 129, 1, False, "Dz"), (2, 64, 16, 1000, 4, True, "Dzb"),
-    (1, 33, 16, 257, 1, True, "b"), (2, 48, 16, 17, 3, False, "Dzb")])
+    (1, 33, 16, 257, 1, True, "b"), (2, 48, 16, 17, 3, False, "Dzb"), (1, 400, 16, 128, 1, True, "Dzb")])
 def test_backward_shapes_and_options(batch, dim, dstate, seqlen, groups, softplus, opts):
     """Ragged tiles (seqlen and channels not multiples of 64 / 16), dstate
-    below 16, several groups, each optional input present or absent."""
+    below 16, several groups, each optional input present or absent; 400
+    channels give 25 channel tiles, so the dB / dC tile sums take their 16-,
+    8- and 1-partial loops."""
     need_gpu()
     u, delta, A, B, C, D, z, bias, dout = _inputs(batch, dim, dstate, seqlen, groups, torch.float32,
                                                   batch * 7 + dim + seqlen)
