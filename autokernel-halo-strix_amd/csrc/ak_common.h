@@ -145,6 +145,9 @@ __host__ __device__ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// Compute units of the current device (queried once per device; ak_capi.hip).
+int cu_count();
+
 }  // namespace ak
 
 // ---------------------------------------------------------------------------

@@ -64,7 +64,5 @@ __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
                                            voff, 0, 0, 0);
 }
 
-// Compute units of the current device (queried once per device).
-int cu_count();
 
 }  // namespace ak

@@ -173,8 +173,11 @@ int launch_scan_wide_fwd(const ScanParams& p, bool prep, int u_dtype, int delta_
 int launch_scan_wide_bwd(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype,
                          hipStream_t s);
 // The whole-tile reverse pass (selective_scan_bwd_fast.hip): launches it and
-// returns true when the shape and layout qualify, else launches nothing.
-bool launch_scan_bwd_fast(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype,
+// returns true when the shape and layout qualify, else launches nothing. It
+// may take 32 channels per workgroup, and then sets p.tiles_per_group to the
+// number of dB / dC partial rows it wrote per group (the sums that follow
+// read that many).
+bool launch_scan_bwd_fast(ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype,
                           hipStream_t s);
 
 }  // namespace ak

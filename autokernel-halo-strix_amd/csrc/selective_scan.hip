@@ -978,18 +978,80 @@ mamba_scan_bwd_kernel(ScanParams p) {
   }
 }
 
+// Arguments of the final sums (scan_bwd_finalize_kernel, and the tail blocks
+// of scan_bwd_bc_sum4_kernel).
+template <typename TBC>
+struct FinArgs {
+  const float *dB_part, *dC_part, *dA_part, *dBc_part, *dCc_part, *dD_part, *dbias_part;
+  TBC *dB, *dC;
+  float *dA, *dBc, *dCc, *dD, *dbias;
+  int64_t nbc;  // dB / dC elements summed here (0 when the vector pass did them)
+  int tiles, nb, dim, dstate;
+};
+
+// Items i0, i0 + stride, ... of the final sums: dB / dC over channel tiles
+// (the first 2 nbc items), then dA / dB / dC of input-independent B / C and
+// dD / ddelta_bias over the batch, each in increasing order.
+template <typename TBC>
+__device__ void finalize_items(const FinArgs<TBC>& a, int64_t i0, int64_t stride) {
+  const int64_t nA = (int64_t)a.dim * a.dstate;
+  const int64_t total = 2 * a.nbc + 3 * nA + 2 * (int64_t)a.dim;
+  for (int64_t i = i0; i < total; i += stride) {
+    if (i < 2 * a.nbc) {
+      const bool is_c = i >= a.nbc;
+      const int64_t e = is_c ? i - a.nbc : i;
+      TBC* dst = is_c ? a.dC : a.dB;
+      if (!dst) continue;
+      const float* part = is_c ? a.dC_part : a.dB_part;
+      float s = 0.0f;
+      for (int t = 0; t < a.tiles; ++t) s += part[(int64_t)t * a.nbc + e];
+      dst[e] = from_f32<TBC>(s);
+      continue;
+    }
+    int64_t e = i - 2 * a.nbc;
+    if (e < 3 * nA) {
+      const int k = (int)(e / nA);
+      e -= k * nA;
+      float* dst = k == 0 ? a.dA : k == 1 ? a.dBc : a.dCc;
+      if (!dst) continue;
+      const float* part = k == 0 ? a.dA_part : k == 1 ? a.dBc_part : a.dCc_part;
+      float s = 0.0f;
+      for (int bb = 0; bb < a.nb; ++bb) s += part[(int64_t)bb * nA + e];
+      dst[e] = s;
+      continue;
+    }
+    e -= 3 * nA;
+    const bool is_bias = e >= a.dim;
+    const int dd = (int)(is_bias ? e - a.dim : e);
+    float* dst = is_bias ? a.dbias : a.dD;
+    if (!dst) continue;
+    const float* part = is_bias ? a.dbias_part : a.dD_part;
+    float s = 0.0f;
+    for (int bb = 0; bb < a.nb; ++bb) s += part[(int64_t)bb * a.dim + dd];
+    dst[dd] = s;
+  }
+}
+
 // dB / dC = sum over channel tiles of the partial rows, 4 elements per
-// thread (16-byte loads, 8 tiles in flight), tiles in increasing order: the
-// same order, hence the same bits, as scan_bwd_finalize_kernel.
+// thread (16-byte loads, up to 16 tiles in flight), tiles in increasing
+// order: the same order, hence the same bits, as scan_bwd_finalize_kernel.
+// Blocks from sum_blocks on run the remaining final sums (fa, with nbc = 0)
+// in the same launch.
 template <typename TBC>
 __global__ void __launch_bounds__(256)
 scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restrict__ dC_part,
-                        TBC* __restrict__ dB, TBC* __restrict__ dC, int64_t n4, int tiles) {
+                        TBC* __restrict__ dB, TBC* __restrict__ dC, int64_t n4, int tiles,
+                        unsigned sum_blocks, FinArgs<TBC> fa) {
   struct alignas(4 * sizeof(TBC)) Out4 {
     TBC v[4];
   };
+  if (blockIdx.x >= sum_blocks) {
+    finalize_items(fa, (int64_t)(blockIdx.x - sum_blocks) * blockDim.x + threadIdx.x,
+                   (int64_t)(gridDim.x - sum_blocks) * blockDim.x);
+    return;
+  }
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n4;
-       i += (int64_t)gridDim.x * blockDim.x) {
+       i += (int64_t)sum_blocks * blockDim.x) {
     const bool is_c = i >= n4;
     const int64_t e4 = is_c ? i - n4 : i;
     if (!(is_c ? dC : dB)) continue;
@@ -1045,52 +1107,8 @@ scan_bwd_bc_sum4_kernel(const float* __restrict__ dB_part, const float* __restri
 //   dA [d, n], constant dB / dC [d, n], dD [d], dbias [d] = sum over the batch
 // A null destination is skipped; nb = 0 (no steps) writes zeros.
 template <typename TBC>
-__global__ void __launch_bounds__(256)
-scan_bwd_finalize_kernel(const float* __restrict__ dB_part, const float* __restrict__ dC_part,
-                         const float* __restrict__ dA_part, const float* __restrict__ dBc_part,
-                         const float* __restrict__ dCc_part, const float* __restrict__ dD_part,
-                         const float* __restrict__ dbias_part, TBC* __restrict__ dB,
-                         TBC* __restrict__ dC, float* __restrict__ dA, float* __restrict__ dBc,
-                         float* __restrict__ dCc, float* __restrict__ dD,
-                         float* __restrict__ dbias, int64_t nbc, int tiles, int nb, int dim,
-                         int dstate) {
-  const int64_t nA = (int64_t)dim * dstate;
-  const int64_t total = 2 * nbc + 3 * nA + 2 * (int64_t)dim;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    if (i < 2 * nbc) {
-      const bool is_c = i >= nbc;
-      const int64_t e = is_c ? i - nbc : i;
-      TBC* dst = is_c ? dC : dB;
-      if (!dst) continue;
-      const float* part = is_c ? dC_part : dB_part;
-      float s = 0.0f;
-      for (int t = 0; t < tiles; ++t) s += part[(int64_t)t * nbc + e];
-      dst[e] = from_f32<TBC>(s);
-      continue;
-    }
-    int64_t e = i - 2 * nbc;
-    if (e < 3 * nA) {
-      const int k = (int)(e / nA);
-      e -= k * nA;
-      float* dst = k == 0 ? dA : k == 1 ? dBc : dCc;
-      if (!dst) continue;
-      const float* part = k == 0 ? dA_part : k == 1 ? dBc_part : dCc_part;
-      float s = 0.0f;
-      for (int bb = 0; bb < nb; ++bb) s += part[(int64_t)bb * nA + e];
-      dst[e] = s;
-      continue;
-    }
-    e -= 3 * nA;
-    const bool is_bias = e >= dim;
-    const int dd = (int)(is_bias ? e - dim : e);
-    float* dst = is_bias ? dbias : dD;
-    if (!dst) continue;
-    const float* part = is_bias ? dbias_part : dD_part;
-    float s = 0.0f;
-    for (int bb = 0; bb < nb; ++bb) s += part[(int64_t)bb * dim + dd];
-    dst[dd] = s;
-  }
+__global__ void __launch_bounds__(256) scan_bwd_finalize_kernel(FinArgs<TBC> a) {
+  finalize_items(a, (int64_t)blockIdx.x * blockDim.x + threadIdx.x, (int64_t)gridDim.x * blockDim.x);
 }
 
 // Whether the fast kernel's layout assumptions hold: whole 64-step tiles,
@@ -1201,18 +1219,22 @@ void scan_bwd_finish(const ScanParams& p, void* dB, void* dC, float* dA, float* 
   int64_t nbc = (dBv || dCv) ? (int64_t)p.batch * p.ngroups * p.dstate * p.seqlen : 0;
   const size_t out4 = 4 * sizeof(TBC);
   auto al4 = [&](const void* q) { return !q || reinterpret_cast<uintptr_t>(q) % out4 == 0; };
+  FinArgs<TBC> fa{p.dB_part, p.dC_part, p.dA_part, p.dBc_part, p.dCc_part, p.dD_part, p.dbias_part,
+                  dBv, dCv, dA, dBk, dCk, dD, dbias, nbc, p.tiles_per_group, p.batch, p.dim, p.dstate};
   if (nbc > 0 && nbc % 4 == 0 && al4(dBv) && al4(dCv)) {
+    // one launch: the vector dB / dC sums, then blocks for the per-batch sums
     const int64_t n4 = nbc / 4;
     const unsigned blocks4 = (unsigned)std::min<int64_t>((2 * n4 + 255) / 256, 65535);
-    scan_bwd_bc_sum4_kernel<TBC><<<dim3(blocks4), dim3(256), 0, s>>>(
-        p.dB_part, p.dC_part, dBv, dCv, n4, p.tiles_per_group);
-    nbc = 0;  // the scalar pass below then covers the per-batch sums only
+    fa.nbc = 0;
+    const int64_t rest = 3 * (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
+    const unsigned fin_blocks = (unsigned)std::min<int64_t>((rest + 255) / 256, 8192);
+    scan_bwd_bc_sum4_kernel<TBC><<<dim3(blocks4 + fin_blocks), dim3(256), 0, s>>>(
+        p.dB_part, p.dC_part, dBv, dCv, n4, p.tiles_per_group, blocks4, fa);
+    return;
   }
   const int64_t total = 2 * nbc + 3 * (int64_t)p.dim * p.dstate + 2 * (int64_t)p.dim;
   const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-  scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(
-      p.dB_part, p.dC_part, p.dA_part, p.dBc_part, p.dCc_part, p.dD_part, p.dbias_part, dBv, dCv,
-      dA, dBk, dCk, dD, dbias, nbc, p.tiles_per_group, p.batch, p.dim, p.dstate);
+  scan_bwd_finalize_kernel<TBC><<<dim3(blocks), dim3(256), 0, s>>>(fa);
 }
 
 int finish_for(int bc_dtype, const ScanParams& p, void* dB, void* dC, float* dA, float* dD,
@@ -1245,14 +1267,15 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
     else
       mamba_scan_fwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   }
-  if (launch_scan_bwd_fast(p, dtype_code_of<TU>(), dtype_code_of<TD>(), dtype_code_of<TBC>(), s)) {
-    // whole tiles: the buffer-resource reverse pass (same arithmetic, same bits)
+  ScanParams q = p;  // the whole-tile pass may write fewer, wider dB / dC partial rows
+  if (launch_scan_bwd_fast(q, dtype_code_of<TU>(), dtype_code_of<TD>(), dtype_code_of<TBC>(), s)) {
+    // whole tiles: the buffer-resource reverse pass
   } else if (p.softplus) {
     mamba_scan_bwd_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   } else {
     mamba_scan_bwd_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
   }
-  scan_bwd_finish<TBC>(p, dB, dC, dA, dD, dbias, s);
+  scan_bwd_finish<TBC>(q, dB, dC, dA, dD, dbias, s);
 }
 
 template <typename TU>
@@ -1460,10 +1483,11 @@ extern "C" int ak_selective_scan_bwd(
     // nothing; a variable dB / dC, du, ... are empty
     if (p.b_const && !dB) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dB", name);
     if (p.c_const && !dC) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dC", name);
-    ak::scan_bwd_finalize_kernel<float><<<dim3(64), dim3(256), 0, s>>>(
-        nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, dA,
-        p.b_const ? static_cast<float*>(dB) : nullptr, p.c_const ? static_cast<float*>(dC) : nullptr,
-        dD, ddelta_bias, 0, 0, 0, (int)dim, (int)dstate);
+    const ak::FinArgs<float> fa{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                nullptr, dA, p.b_const ? static_cast<float*>(dB) : nullptr,
+                                p.c_const ? static_cast<float*>(dC) : nullptr, dD, ddelta_bias, 0,
+                                0, 0, (int)dim, (int)dstate};
+    ak::scan_bwd_finalize_kernel<float><<<dim3(64), dim3(256), 0, s>>>(fa);
     return ak_check_launch(name);
   }
   if (!u || !delta || !A || !B || !C || !dout || !du || !ddelta || !dB || !dC || (z && !dz))

@@ -1,11 +1,15 @@
 // Reverse pass of the Mamba-1 selective-scan backward for whole-tile shapes
-// (sequence length a multiple of 64, 16-channel workgroups, 4-element
-// aligned rows, every buffer extent below 2 GiB).
+// (sequence length a multiple of 64, channels per group a multiple of 16,
+// 4-element aligned rows, every buffer extent below 2 GiB).
 //
-// The arithmetic, its order and the workspace layout are those of the
-// general reverse pass (mamba_scan_bwd_kernel in selective_scan.hip, which
-// documents the recurrence), so both produce the same bits. What differs is
-// the data movement and the control flow:
+// The arithmetic and its order are those of the general reverse pass
+// (mamba_scan_bwd_kernel in selective_scan.hip, which documents the
+// recurrence), so du, ddelta, dz, dA, dD and ddelta_bias have the same bits.
+// Where the grid still fills the GPU, a workgroup takes 32 channels (8 waves)
+// instead of 16: it then writes one dB / dC partial row per 32 channels, half
+// the partial-sum traffic, and the sums over channels are added in another
+// order (dB / dC equal to rounding, still deterministic). What else differs
+// is the data movement and the control flow:
 // * every global access goes through a wave-uniform buffer resource based at
 //   the workgroup's first channel, with per-lane 32-bit offsets fixed for the
 //   whole pass and the tile offset in the scalar offset: no 64-bit address
@@ -22,27 +26,31 @@
 //   need no bounds tests, so each 16-step block is one basic block the
 //   scheduler can interleave.
 // At the C5 shape (batch 4, dim 2048, seqlen 4096, dstate 16) the pass takes
-// 435 us against 579 us for the general one on the same box.
+// about 435 us with 16-channel workgroups (579 us for the general one on the
+// same box) and 1.5% less with 32-channel ones, whose partial sums then read
+// 134 MB instead of 268 MB.
 #include "scan_buffer.h"
 
 namespace ak {
 namespace {
 
-template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kGate, bool kDz>
-__global__ void __launch_bounds__(256)
+// kWv waves (4 or 8) of 4 channels each per workgroup.
+template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kGate, bool kDz, int kWv>
+__global__ void __launch_bounds__(64 * kWv)
 mamba_scan_bwd_fast_kernel(ScanParams p) {
-  constexpr int kCh = kScanCh;  // channels per workgroup
+  static_assert(kWv == 4 || kWv == 8, "16 or 32 channels per workgroup");
+  constexpr int kCh = 4 * kWv;  // channels per workgroup
   __shared__ float Bs[16 * kBStride];
   __shared__ float Cs[16 * kBStride];
-  __shared__ __align__(16) float tbuf[4][4 * kTC];     // per wave: (g B, A w)[c][j][n]
-  __shared__ float wbuf[4][64 * kWP];                  // per wave: (dB, dC) channel sums [lane][pair]
+  __shared__ __align__(16) float tbuf[kWv][4 * kTC];     // per wave: (g B, A w)[c][j][n]
+  __shared__ float wbuf[kWv][64 * kWP];                  // per wave: (dB, dC) channel sums [lane][pair]
 
   const int tid = threadIdx.x;
   const int wave = tid / 64;
   const int lane = tid % 64;
   const int c = lane / 16;
   const int n = lane % 16;
-  const int tpg = p.tiles_per_group;  // whole 16-channel tiles
+  const int tpg = p.tiles_per_group;  // whole kCh-channel tiles
   const int per_batch = p.ngroups * tpg;
   const int b = blockIdx.x / per_batch;
   const int g = (blockIdx.x % per_batch) / tpg;
@@ -74,7 +82,7 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
   const uint32_t bc_bytes_C = (uint32_t)(((p.dstate - 1) * p.C_ns + L) * sizeof(TBC));
   const Rsrc rs_B = make_rsrc(static_cast<const TBC*>(p.B) + (int64_t)b * p.B_bs + (int64_t)g * p.B_gs, bc_bytes_B);
   const Rsrc rs_C = make_rsrc(static_cast<const TBC*>(p.C) + (int64_t)b * p.C_bs + (int64_t)g * p.C_gs, bc_bytes_C);
-  // saved states [batch, nchunks, dim, dstate]: the workgroup's 16 x dstate block of a chunk
+  // saved states [batch, nchunks, dim, dstate]: the workgroup's kCh x dstate block of a chunk
   const int64_t ck_cs = (int64_t)p.dim * p.dstate;  // floats per chunk
   const Rsrc rs_ck = make_rsrc(p.ck + (int64_t)b * p.nchunks * ck_cs + (int64_t)d0 * p.dstate,
                                (uint32_t)(((int64_t)(p.nchunks - 1) * ck_cs + kCh * p.dstate) * 4));
@@ -85,7 +93,9 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
   const uint32_t vo_z1 = kGate ? (uint32_t)(wc * p.z_ds + n) * sizeof(TU) : vo_u1;
   const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);   // du, dz, y (out_prez)
   const uint32_t vo_dd1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TD);  // ddelta
-  const int sn = tid / 16, q = tid % 16;
+  // B / C staging by waves 0-3: state sn, steps 4 q .. 4 q + 3
+  const bool stager = wave < 4;
+  const int sn = (tid / 16) % 16, q = tid % 16;
   const int sn_c = min(sn, p.dstate - 1);
   const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
   const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
@@ -120,20 +130,23 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
 
   float gs = 0.0f, a_next = 0.0f, dA_acc = 0.0f, dD_acc = 0.0f, dbias_acc = 0.0f;
   const int nt = p.seqlen / kScanT;
-  Raw4<TBC> bv = bload4<TBC>(rs_B, vo_B, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
-  Raw4<TBC> cv = bload4<TBC>(rs_C, vo_C, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
+  Raw4<TBC> bv{}, cv{};
+  if (stager) {
+    bv = bload4<TBC>(rs_B, vo_B, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
+    cv = bload4<TBC>(rs_C, vo_C, (uint32_t)(nt - 1) * kScanT * sizeof(TBC));
+  }
   Blk pb;
   load_blk(nt - 1, 3, pb);
   for (int t = nt - 1; t >= 0; --t) {
     const int l0 = t * kScanT;
     __syncthreads();
+    if (stager) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool ok = sn < p.dstate;
-      Bs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(bv, k) : 0.0f;
-      Cs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(cv, k) : 0.0f;
-    }
-    {
+      for (int k = 0; k < 4; ++k) {
+        const bool ok = sn < p.dstate;
+        Bs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(bv, k) : 0.0f;
+        Cs[sn * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(cv, k) : 0.0f;
+      }
       const uint32_t ln = (uint32_t)max(t - 1, 0) * kScanT;
       bv = bload4<TBC>(rs_B, vo_B, ln * sizeof(TBC));
       cv = bload4<TBC>(rs_C, vo_C, ln * sizeof(TBC));
@@ -256,17 +269,21 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
 
     __syncthreads();
     {
+      // step l0 + tt, states kPer ng .. kPer ng + kPer - 1: the waves' channel
+      // sums added in wave order
+      constexpr int kPer = 16 / kWv;
       const int tt = tid % 64, ng = tid / 64;
       const int l = l0 + tt;
 #pragma unroll
       for (int v = 0; v < 2; ++v) {
         float* part = v ? p.dC_part : p.dB_part;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n2 = 4 * ng + i;
+        for (int i = 0; i < kPer; ++i) {
+          const int n2 = kPer * ng + i;
           const int Lr = 16 * (2 * v + (tt & 1)) + n2;
-          const float sum = ((wbuf[0][Lr * kWP + tt / 2] + wbuf[1][Lr * kWP + tt / 2]) +
-                             wbuf[2][Lr * kWP + tt / 2]) + wbuf[3][Lr * kWP + tt / 2];
+          float sum = wbuf[0][Lr * kWP + tt / 2];
+#pragma unroll
+          for (int w = 1; w < kWv; ++w) sum += wbuf[w][Lr * kWP + tt / 2];
           if (n2 < p.dstate)
             part[((((int64_t)tile * p.batch + b) * p.ngroups + g) * p.dstate + n2) * p.seqlen + l] = sum;
         }
@@ -283,14 +300,14 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
 }
 
 template <typename TU, typename TD, typename TBC>
-bool scan_bwd_fast_ok(const ScanParams& p) {
+bool scan_bwd_fast_ok(const ScanParams& p, int wgc) {
   auto al4 = [](const void* ptr, int64_t s0, int64_t s1, size_t esz) {
     return (reinterpret_cast<uintptr_t>(ptr) % (4 * esz)) == 0 && s0 % 4 == 0 && s1 % 4 == 0;
   };
   auto fits = [&](int64_t rows, int64_t pitch, size_t esz) {
     return pitch >= 0 && ((rows - 1) * pitch + p.seqlen) * (int64_t)esz < ((int64_t)1 << 31);
   };
-  if (p.seqlen % kScanT != 0 || p.ch_per_group % kScanCh != 0 || p.dstate > 16) return false;
+  if (p.seqlen % kScanT != 0 || p.ch_per_group % wgc != 0 || p.dstate > 16) return false;
   if (p.b_const || p.c_const) return false;
   if (!al4(p.u, p.u_bs, p.u_ds, sizeof(TU)) || !al4(p.delta, p.d_bs, p.d_ds, sizeof(TD)) ||
       !al4(p.dout, p.go_bs, p.go_ds, sizeof(TU)))
@@ -302,22 +319,29 @@ bool scan_bwd_fast_ok(const ScanParams& p) {
   if (p.u_bs < 0 || p.d_bs < 0 || p.go_bs < 0 || p.z_bs < 0 || p.o_bs < 0 || p.B_bs < 0 ||
       p.C_bs < 0 || p.B_gs < 0 || p.C_gs < 0)
     return false;
-  const int64_t ck_bytes = ((int64_t)(p.nchunks - 1) * p.dim * p.dstate + kScanCh * p.dstate) * 4;
+  const int64_t ck_bytes = ((int64_t)(p.nchunks - 1) * p.dim * p.dstate + wgc * p.dstate) * 4;
   if (ck_bytes >= ((int64_t)1 << 31)) return false;
-  return fits(kScanCh, p.u_ds, sizeof(TU)) && fits(kScanCh, p.d_ds, sizeof(TD)) &&
-         fits(kScanCh, p.go_ds, sizeof(TU)) && fits(kScanCh, p.o_ds, sizeof(TD)) &&
-         (!p.z || fits(kScanCh, p.z_ds, sizeof(TU))) && fits(p.dstate, p.B_ns, sizeof(TBC)) &&
+  return fits(wgc, p.u_ds, sizeof(TU)) && fits(wgc, p.d_ds, sizeof(TD)) &&
+         fits(wgc, p.go_ds, sizeof(TU)) && fits(wgc, p.o_ds, sizeof(TD)) &&
+         (!p.z || fits(wgc, p.z_ds, sizeof(TU))) && fits(p.dstate, p.B_ns, sizeof(TBC)) &&
          fits(p.dstate, p.C_ns, sizeof(TBC));
 }
 
 template <typename TU, typename TD, typename TBC>
-bool launch_fast(const ScanParams& p, hipStream_t s) {
-  if (!scan_bwd_fast_ok<TU, TD, TBC>(p)) return false;
+bool launch_fast(ScanParams& p, hipStream_t s) {
+  // 32-channel workgroups when that still gives every CU one
+  const bool wide = p.ch_per_group % 32 == 0 && scan_bwd_fast_ok<TU, TD, TBC>(p, 32) &&
+                    (int64_t)p.batch * p.ngroups * (p.ch_per_group / 32) >= cu_count();
+  if (!wide && !scan_bwd_fast_ok<TU, TD, TBC>(p, kScanCh)) return false;
+  if (wide) p.tiles_per_group = p.ch_per_group / 32;
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
   const bool gate = p.z != nullptr, dz = gate && p.out_prez != nullptr;
   auto go = [&](auto sp, auto gt, auto dzt) {
-    mamba_scan_bwd_fast_kernel<TU, TD, TBC, decltype(sp)::value, decltype(gt)::value, decltype(dzt)::value>
-        <<<dim3(grid), dim3(256), 0, s>>>(p);
+    constexpr bool kSp = decltype(sp)::value, kGt = decltype(gt)::value, kDzt = decltype(dzt)::value;
+    if (wide)
+      mamba_scan_bwd_fast_kernel<TU, TD, TBC, kSp, kGt, kDzt, 8><<<dim3(grid), dim3(512), 0, s>>>(p);
+    else
+      mamba_scan_bwd_fast_kernel<TU, TD, TBC, kSp, kGt, kDzt, 4><<<dim3(grid), dim3(256), 0, s>>>(p);
   };
   using T = std::true_type;
   using F = std::false_type;
@@ -334,7 +358,7 @@ bool launch_fast(const ScanParams& p, hipStream_t s) {
 }
 
 template <typename TU>
-bool dispatch_fast(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, hipStream_t s) {
+bool dispatch_fast(ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype, hipStream_t s) {
   const bool d32 = delta_dtype == AK_DTYPE_F32, bc32 = bc_dtype == AK_DTYPE_F32;
   if (!d32 && delta_dtype != u_dtype) return false;
   if (!bc32 && bc_dtype != u_dtype) return false;
@@ -346,7 +370,7 @@ bool dispatch_fast(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dty
 
 }  // namespace
 
-bool launch_scan_bwd_fast(const ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype,
+bool launch_scan_bwd_fast(ScanParams& p, int u_dtype, int delta_dtype, int bc_dtype,
                           hipStream_t s) {
   switch (u_dtype) {
     case AK_DTYPE_F32: return dispatch_fast<float>(p, u_dtype, delta_dtype, bc_dtype, s);

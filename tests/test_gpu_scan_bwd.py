@@ -113,6 +113,25 @@ def test_backward_shapes_and_options(batch, dim, dstate, seqlen, groups, softplu
     _check(got, ref, _tols("float32", z is not None), (u, delta, A, B, C, D, z, bias))
 
 
+@pytest.mark.parametrize("itype,groups,softplus,opts", [("float32", 2, True, "Dzb"), ("bfloat16", 1, False, "D")])
+def test_backward_wide_workgroups(itype, groups, softplus, opts):
+    """Shapes whose reverse pass takes 32-channel workgroups (8 waves; batch x
+    groups x channels / 32 = 256 workgroups, one per CU): every gradient
+    against the oracle, and bitwise reproducible."""
+    need_gpu()
+    u, delta, A, B, C, D, z, bias, dout = _inputs(8, 1024, 16, 128, groups, ITYPES[itype], 77 + groups)
+    D = D if "D" in opts else None
+    z = z if "z" in opts else None
+    bias = bias if "b" in opts else None
+    say("mamba bwd 32-channel workgroups", itype, groups, softplus, opts)
+    got = _gpu_grads(u, delta, A, B, C, D, z, bias, dout, softplus)
+    again = _gpu_grads(u, delta, A, B, C, D, z, bias, dout, softplus)
+    for a, b in zip(got, again):
+        assert (a is None and b is None) or torch.equal(a, b)
+    ref = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, bias, softplus)
+    _check(got, ref, _tols(itype, z is not None), (u, delta, A, B, C, D, z, bias))
+
+
 @pytest.mark.parametrize("itype", ["float16", "bfloat16"])
 def test_backward_fp32_delta_and_bc(itype):
     """delta and B / C in fp32 with u in half precision (the forward's mixed
