@@ -364,6 +364,12 @@ mamba_scan_fast_kernel(ScanParams p) {
   const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);       // u, step 16 blk + n
   const uint32_t vo_z1 = (uint32_t)(wc * zds + n) * sizeof(TU);
   const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);
+  // checkpoints [batch, nchunks, dim, dstate]: this batch's slab, the lane's
+  // (channel, state) offset fixed, the chunk in the scalar offset
+  const Rsrc rs_ck = make_rsrc(has_ck ? ck_out + (int64_t)b * p.nchunks * p.dim * p.dstate : p.A,
+                               has_ck ? (uint32_t)((int64_t)p.nchunks * p.dim * p.dstate * 4) : 0u);
+  const uint32_t vo_ck = (uint32_t)(d * p.dstate + ns) * 4u;
+  const uint32_t ck_chunk_bytes = (uint32_t)(p.dim * p.dstate * 4);
   // staging: state sn, steps 4q..4q+3; the 16 lanes of a row take 16
   // different states, so the transposed Cs writes of a wave hit 64 distinct
   // banks (with 16 lanes per state they conflicted 8-way)
@@ -449,6 +455,7 @@ mamba_scan_fast_kernel(ScanParams p) {
 
   auto compute = [&](int t, const Regs& cur) {
     const int buf = t & 1;
+    float hck[kScanT / 16];  // the states before the tile's 16-step blocks (checkpoints)
     float dl[4], du[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -468,10 +475,7 @@ mamba_scan_fast_kernel(ScanParams p) {
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
-      if (has_ck) {
-        if (n_ok)
-          ck_out[(((int64_t)b * p.nchunks + (t * kScanT + 16 * blk) / kCk) * p.dim + d) * p.dstate + ns] = h;
-      }
+      hck[blk] = h;
       float hv[16], av[16], xv[16];
       auto steps4 = [&](auto src_c, int j4) {
         constexpr int kSrc = decltype(src_c)::value;
@@ -523,6 +527,14 @@ mamba_scan_fast_kernel(ScanParams p) {
       if constexpr (kPrep) p_go = raw_f32<TU>(cur.go[blk]);
       p_off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
       pending = true;
+    }
+    // the tile's checkpoints in one burst after its last block (stored before
+    // each block they cost about 6 us more at the C5 shape)
+    if (has_ck && n_ok) {
+#pragma unroll
+      for (int blk = 0; blk < kScanT / 16; ++blk)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hck[blk]), rs_ck, (int)vo_ck,
+                                              (int)((uint32_t)((t * kScanT + 16 * blk) / kCk) * ck_chunk_bytes), 0);
     }
     if (!kPrep && xs_out) {
       dsum += row16_sum((dl[0] + dl[1]) + (dl[2] + dl[3]));
@@ -1133,6 +1145,7 @@ bool scan_fast_ok(const ScanParams& p, bool prep = false, int wgc = kScanCh) {
       p.B_gs < 0 || p.C_gs < 0)
     return false;
   if (prep && (p.go_bs < 0 || !fits(wgc, p.go_ds, sizeof(TU)))) return false;
+  if (p.ck && (int64_t)p.nchunks * p.dim * p.dstate * 4 >= ((int64_t)1 << 31)) return false;
   return fits(wgc, p.u_ds, sizeof(TU)) && fits(wgc, p.d_ds, sizeof(TD)) &&
          fits(wgc, p.o_ds, sizeof(TU)) && (!p.z || fits(wgc, p.z_ds, sizeof(TU))) &&
          fits(p.dstate, p.B_ns, sizeof(TBC)) && fits(p.dstate, p.C_ns, sizeof(TBC));
