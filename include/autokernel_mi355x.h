@@ -402,7 +402,10 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  *               output, as the reference's backward does with its `out`.
  * workspace: ak_selective_scan_bwd_workspace_bytes(...) bytes (saved states
  * every 16 steps and the partial sums of dB / dC / dA / dD / ddelta_bias,
- * reduced in a fixed order: results are bitwise reproducible).
+ * reduced in a fixed order: results are bitwise reproducible on a given
+ * device; large whole-tile shapes group 32 channels per partial dB / dC row
+ * when the grid still gives every compute unit a workgroup, so dB / dC can
+ * differ by rounding between devices with different CU counts).
  */
 size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
                                              int64_t dstate, int64_t ngroups, int bc_flags);
