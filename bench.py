@@ -309,7 +309,7 @@ def make_case(name):
             s["ddelta"], s["dA"], s["dB"], s["dC"], s["dD"], s["dz"], None, False)
         return Case(name, "C5-shape Mamba-1 selective scan backward B4 L4096 D2048 N16", "hbm",
                     C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel + scan_bwd_finalize_kernel")
+                    "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
     if name == "c5t":
         # one training step of the scan: the forward keeps its states every 16
         # steps and its pre-gate output, the backward restarts from them
@@ -334,7 +334,7 @@ def make_case(name):
                                     s["dz"], None, False, checkpoints=s["ck"], out_prez=s["prez"])
         return Case(name, "C5-shape Mamba-1 training step (forward keeping its states + backward from them)",
                     "hbm", C5_BYTES + C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel (training variant) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel + scan_bwd_finalize_kernel")
+                    "mamba_scan_fast_kernel (training variant) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
     raise ValueError(name)
 
 
