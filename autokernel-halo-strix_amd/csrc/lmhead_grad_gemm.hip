@@ -537,6 +537,10 @@ int check_gemm(const char* name, int64_t n_rows, int64_t vocab, int64_t d, const
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: d=%lld must be a multiple of %d", name, (long long)d, kKB);
   if (n_rows > (1 << 30) || vocab > (1 << 30) || d > (1 << 20))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
+  // the launch plan counts tiles, and up to 16 K ranges of each, in int
+  const int64_t m_tiles = (std::max(n_rows, vocab) + kGT - 1) / kGT, n_tiles = (d + kGT - 1) / kGT;
+  if (m_tiles * n_tiles * 16 >= (int64_t(1) << 31))
+    return ak_set_error(AK_ERR_INVALID_ARG, "%s: too many 256 x 256 output tiles", name);
   const int64_t vpad = (vocab + kKB - 1) / kKB * kKB;
   if (ld_dl < vpad || ld_dl % 8 || ld_dl >= (1 << 23))
     return ak_set_error(AK_ERR_INVALID_ARG,

@@ -329,9 +329,14 @@ bool scan_bwd_fast_ok(const ScanParams& p, int wgc) {
 
 template <typename TU, typename TD, typename TBC>
 bool launch_fast(ScanParams& p, hipStream_t s) {
-  // 32-channel workgroups when that still gives every CU one
+  // 32-channel workgroups when there are at least kWideMinGroups of them
+  // (one per CU on MI355X). The threshold is a constant, not the live CU
+  // count: the choice fixes the order in which dB / dC are summed over
+  // channels, so it depends on the shape alone and the bits of every
+  // gradient are the same on any device or partition.
+  constexpr int64_t kWideMinGroups = 256;
   const bool wide = p.ch_per_group % 32 == 0 && scan_bwd_fast_ok<TU, TD, TBC>(p, 32) &&
-                    (int64_t)p.batch * p.ngroups * (p.ch_per_group / 32) >= cu_count();
+                    (int64_t)p.batch * p.ngroups * (p.ch_per_group / 32) >= kWideMinGroups;
   if (!wide && !scan_bwd_fast_ok<TU, TD, TBC>(p, kScanCh)) return false;
   if (wide) p.tiles_per_group = p.ch_per_group / 32;
   const int grid = p.batch * p.ngroups * p.tiles_per_group;

@@ -179,11 +179,10 @@ class _CrossEntropyHIP(torch.autograd.Function):
         softcap, ign, ls, zw = ctx.params
         if ctx.keep_grad:
             (grad,) = ctx.saved_tensors
-            # The saved gradient already carries 1 / #counted rows. An upstream
-            # gradient of exactly 1 (loss.backward()) needs no further pass.
-            up = float(grad_loss)
-            if up != 1.0:
-                grad = grad * up
+            # The saved gradient already carries 1 / #counted rows; the
+            # upstream gradient is applied on the device (a product with 1.0
+            # returns the saved bits), so the backward never waits for the GPU.
+            grad = grad * grad_loss.detach().to(grad.dtype)
         else:
             rows2d, tg, row_max, row_sum, denom = ctx.saved_tensors
             # upstream gradient / #counted rows, kept on the device

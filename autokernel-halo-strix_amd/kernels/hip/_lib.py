@@ -466,8 +466,20 @@ def lmhead_grad_workspace_bytes(n_rows: int, vocab: int, d: int) -> int:
 def _grad_gemm(entry: str, grad_logits: torch.Tensor, operand: torch.Tensor,
                out: torch.Tensor, out_mode: int, workspace: Optional[torch.Tensor]) -> None:
     require_device(grad_logits, operand, out, workspace)
+    if grad_logits.dim() != 2 or operand.dim() != 2 or out.dim() != 2:
+        raise ValueError(f"{entry}: grad_logits, operand and out must be 2-D")
     n_rows, vocab = grad_logits.shape
     d = operand.shape[1]
+    if operand.dtype != grad_logits.dtype:
+        raise ValueError(f"{entry}: operand dtype {operand.dtype} != grad_logits dtype {grad_logits.dtype}")
+    want_out = grad_logits.dtype if out_mode == GEMM_OUT_DTYPE else torch.float32
+    if out_mode not in (GEMM_OUT_DTYPE, GEMM_OUT_F32, GEMM_OUT_F32_ADD) or out.dtype != want_out:
+        raise ValueError(f"{entry}: out_mode {out_mode} needs a {want_out} output, got {out.dtype}")
+    # grad_hidden: operand [vocab, d], out [n_rows, d]; grad_weight: operand [n_rows, d], out [vocab, d]
+    rows_op, rows_out = (vocab, n_rows) if entry == "ak_lmhead_grad_hidden" else (n_rows, vocab)
+    if operand.shape[0] != rows_op or tuple(out.shape) != (rows_out, d):
+        raise ValueError(f"{entry}: shapes grad_logits {tuple(grad_logits.shape)}, operand "
+                         f"{tuple(operand.shape)}, out {tuple(out.shape)} do not fit")
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     with _on_device(grad_logits):
         rc = getattr(load(), entry)(
@@ -477,15 +489,37 @@ def _grad_gemm(entry: str, grad_logits: torch.Tensor, operand: torch.Tensor,
     _check(rc, entry)
 
 
+def _zero_k_padding(grad_logits: torch.Tensor) -> None:
+    """Zero columns ``[vocab, vocab rounded up to 64)`` behind a ``[n_rows,
+    vocab]`` dlogits view. ak_lmhead_grad_hidden reads whole 64-column K
+    blocks and multiplies the padding by weight rows that load as zeros, so
+    any finite padding adds nothing, but a NaN or Inf left in fresh memory
+    would turn 0 x NaN into NaN. Also checks that the storage holds
+    ``n_rows`` whole row pitches, the extent the kernel reads."""
+    n_rows, vocab = grad_logits.shape
+    pitch = grad_logits.stride(0)
+    vpad = -(-vocab // 64) * 64
+    if pitch < vpad:
+        raise ValueError(f"grad_logits row pitch {pitch} must cover vocab rounded up to 64 ({vpad})")
+    size = grad_logits.untyped_storage().nbytes() // grad_logits.element_size()
+    if grad_logits.storage_offset() + n_rows * pitch > size:
+        raise ValueError("grad_logits storage must hold n_rows whole row pitches")
+    if vpad > vocab and n_rows:
+        torch.as_strided(grad_logits, (n_rows, vpad - vocab), (pitch, 1),
+                         grad_logits.storage_offset() + vocab).zero_()
+
+
 def lmhead_grad_hidden(grad_logits: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
                        out_mode: int, workspace: Optional[torch.Tensor]) -> None:
     """out (=, or += with GEMM_OUT_F32_ADD) grad_logits @ weight.
 
     ``grad_logits`` is a ``[n_rows, vocab]`` view whose row pitch covers
-    vocab rounded up to 64 with zeros in the padding columns; ``weight`` is
-    ``[vocab, d]``; ``out`` is ``[n_rows, d]``."""
+    vocab rounded up to 64 (the padding columns are zeroed here, and the
+    storage must hold ``n_rows`` whole pitches); ``weight`` is ``[vocab, d]``;
+    ``out`` is ``[n_rows, d]``."""
     if grad_logits.stride(1) != 1:
         raise ValueError("grad_logits must have a contiguous last dimension")
+    _zero_k_padding(grad_logits)
     _grad_gemm("ak_lmhead_grad_hidden", grad_logits, weight, out, out_mode, workspace)
 
 

@@ -5,8 +5,8 @@ Drop-in for the reference module ``kernels/hip/chunked_linear_cross_entropy.py``
 :50-175): same constructor arguments, same ``forward(hidden, weight,
 targets)`` contract, autograd for ``hidden`` and ``weight``.
 
-Forward (bf16/fp16, ``d % 64 == 0``; any softcap and label smoothing):
-one fused kernel,
+Forward (bf16/fp16, any hidden size ``d``; any softcap and label
+smoothing): one fused kernel,
 ``ak_lmhead_ce_fwd`` (``csrc/lmhead_ce.hip``), computes ``hidden @ weight^T``
 tile by tile on the matrix cores and folds each tile into an online
 logsumexp, so the ``[N, V]`` logits never exist in memory and there is no
@@ -18,9 +18,13 @@ partials use ``softcap`` as their offset (no max pass). With
 ``label_smoothing`` a the loss is ``lse - (1 - a) z_t - a mean(z)``; the
 tile epilogue then also sums the (capped) logits of each token.
 
-For fp32 or unaligned inputs the forward runs the reference's row-chunked
-algorithm: per ``chunk_size`` rows a GEMM (``torch.nn.functional.linear``)
-feeds the gfx950 CE row kernel.
+The kernels take ``d`` in 64-wide blocks: a ``d`` that is not a multiple
+of 64 is zero-extended on the way in (exact: the extra columns add zeros to
+every dot product) and the gradients are cut back to ``d`` columns.
+
+For fp32 inputs the forward runs the reference's row-chunked algorithm: per
+``chunk_size`` rows a GEMM (``torch.nn.functional.linear``) feeds the gfx950
+CE row kernel.
 
 Backward (the fused forward's conditions): ``ak_lmhead_ce_bwd``
 recomputes the logits tile by tile on the matrix cores from the saved
@@ -41,11 +45,13 @@ fp32 buffer (the GEMM's add-into-fp32 output) and rounded once at the end.
 The default budget (4 GiB) keeps the C4 shape in one range (8192 x 50304
 bf16 = 824 MB, 0.3% of the 288 GB of HBM); lower it where memory matters
 more than time.
-Otherwise (fp32 or unaligned inputs) per row chunk
-the logits are recomputed with a GEMM and turned into ``dL/dlogits`` by the
-CE row kernel from the saved logsumexp, then ``grad_hidden = dlogits @ W``
-and ``grad_W += dlogits^T @ h`` (fp32 accumulation), as in the reference
-(``:97-132``, ``:150-175``). As in the reference, the z-loss term
+For fp32 inputs, per row chunk the logits are recomputed with a GEMM and
+turned into ``dL/dlogits`` by the CE row kernel from the saved logsumexp
+(the upstream gradient over the counted rows as a device scalar: no host
+sync, where the reference read both with ``.item()``), then
+``grad_hidden = dlogits @ W`` and ``grad_W += dlogits^T @ h`` (fp32
+accumulation), as in the reference (``:97-132``, ``:150-175``). An empty
+batch gives a zero loss and empty / zero gradients. As in the reference, the z-loss term
 contributes to the returned loss only, not to the gradient.
 
 ``chunk_size`` is the row-chunk of the GEMM paths; the fused forward tiles
@@ -64,10 +70,37 @@ from kernels.hip import _lib
 
 def _fused_ok(hidden: torch.Tensor, weight: torch.Tensor, softcap: float,
               label_smoothing: float) -> bool:
+    """Whether the matrix-core kernels take the call: half-precision inputs of
+    one dtype and a finite softcap / smoothing in range. Any hidden size and
+    alignment qualify (``_kernel_operands`` pads and realigns)."""
     return (0.0 <= softcap < float("inf") and 0.0 <= label_smoothing <= 1.0
-            and hidden.dtype in (torch.bfloat16, torch.float16) and weight.dtype == hidden.dtype
-            and hidden.shape[1] % 64 == 0
-            and hidden.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+            and hidden.dtype in (torch.bfloat16, torch.float16) and weight.dtype == hidden.dtype)
+
+
+# The tile kernels consume the hidden dimension in 64-wide blocks.
+_K_BLOCK = 64
+
+
+def _kernel_operands(hidden: torch.Tensor, weight: torch.Tensor):
+    """``(hidden, weight)`` as the fused kernels need them: contiguous,
+    16-byte aligned, hidden size a multiple of 64. A hidden size that is not
+    is zero-extended (both operands get the same zero columns), which adds
+    exact zeros to every logit's dot product, so the logits and both
+    gradients' first ``d`` columns are those of the unpadded problem."""
+    d = hidden.shape[1]
+    dk = -(-d // _K_BLOCK) * _K_BLOCK
+    if dk != d:
+        hp = hidden.new_zeros((hidden.shape[0], dk))
+        hp[:, :d] = hidden
+        wp = weight.new_zeros((weight.shape[0], dk))
+        wp[:, :d] = weight
+        return hp, wp
+    hidden, weight = hidden.contiguous(), weight.contiguous()
+    if hidden.data_ptr() % 16:
+        hidden = hidden.clone()
+    if weight.data_ptr() % 16:
+        weight = weight.clone()
+    return hidden, weight
 
 
 def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
@@ -79,8 +112,7 @@ def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch
     ``[N]``, ``n_valid`` a 1-element int64 tensor. No host synchronisation.
     """
     _lib.require_device(hidden, weight, targets)
-    hidden = hidden.contiguous()
-    weight = weight.contiguous()
+    hidden, weight = _kernel_operands(hidden, weight)
     targets = targets.contiguous().to(torch.int64)
     n = hidden.shape[0]
     dev = hidden.device
@@ -88,6 +120,10 @@ def lmhead_ce_forward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch
     lse = torch.empty(n, dtype=torch.float32, device=dev)
     n_valid = torch.empty(1, dtype=torch.int64, device=dev)
     losses = torch.empty(n, dtype=torch.float32, device=dev) if return_losses else None
+    if n == 0:  # an empty batch: no counted rows, loss 0 (the mean over max(1, 0) rows)
+        loss.zero_()
+        n_valid.zero_()
+        return (loss, lse, n_valid, losses) if return_losses else (loss, lse, n_valid)
     ws = torch.empty(_lib.lmhead_ce_workspace_bytes(n, weight.shape[0]), dtype=torch.uint8, device=dev)
     _lib.lmhead_ce(hidden, weight, targets, loss, lse, losses, n_valid, ws, ignore_index, softcap,
                    label_smoothing)
@@ -120,11 +156,14 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     not requested).
     """
     _lib.require_device(hidden, weight, targets, lse, denom, grad_loss)
-    hidden = hidden.contiguous()
-    weight = weight.contiguous()
+    d_in = hidden.shape[1]
+    hidden, weight = _kernel_operands(hidden, weight)
     targets = targets.contiguous().to(torch.int64)
     n, d = hidden.shape
     vocab = weight.shape[0]
+    if n == 0:
+        return (torch.empty((0, d_in), dtype=hidden.dtype, device=hidden.device) if need_hidden else None,
+                torch.zeros((vocab, d_in), dtype=weight.dtype, device=weight.device) if need_weight else None)
     g1 = grad_loss.reshape(1).to(torch.float32).contiguous()
     den1 = denom.reshape(1).to(torch.float32).contiguous()
     lse = lse.contiguous()
@@ -133,9 +172,9 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     width = min(width, vocab)
     ranges = [(v0, min(v0 + width, vocab)) for v0 in range(0, vocab, width)]
     # each range's dlogits slice lives in a buffer whose pitch covers the
-    # slice rounded up to 64 columns, the padding zeroed (the gradient GEMMs
-    # read whole 64-column K blocks); a pitch off powers of two keeps the rows
-    # from all starting in the same memory channels
+    # slice rounded up to 64 columns (the gradient GEMMs read whole 64-column
+    # K blocks); a pitch off powers of two keeps the rows from all starting
+    # in the same memory channels
     pitch = -(-width // 64) * 64
     if pitch & (pitch - 1) == 0:
         pitch += 64
@@ -150,8 +189,7 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     else:
         grad_hidden = None
     for v0, v1 in ranges:
-        gp[:, v1 - v0:].zero_()
-        g = gp[:, :v1 - v0]
+        g = gp[:, :v1 - v0]  # lmhead_grad_hidden zeroes its K padding
         _lib.lmhead_ce_bwd_range(hidden, weight, targets, lse, g1, den1, g, v0, ignore_index,
                                  softcap, label_smoothing)
         if need_weight:
@@ -161,6 +199,9 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
                                     _lib.GEMM_OUT_DTYPE if single else _lib.GEMM_OUT_F32_ADD, ws)
     if need_hidden and not single:
         grad_hidden = grad_hidden.to(hidden.dtype)
+    if d != d_in:  # drop the zero extension of the hidden size
+        grad_hidden = grad_hidden[:, :d_in].contiguous() if need_hidden else None
+        grad_weight = grad_weight[:, :d_in].contiguous() if need_weight else None
     return grad_hidden, grad_weight
 
 
@@ -210,7 +251,6 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        from kernels.ce_fused import _get_bwd_module
         hidden, weight, targets, lse, n_valid = ctx.saved_tensors
         need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if ctx.fused and (need_h or need_w):
@@ -221,20 +261,20 @@ class _ChunkedLinearCrossEntropy(torch.autograd.Function):
         grad_hidden = torch.empty_like(hidden) if need_h else None
         grad_weight = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device) if need_w else None
         if need_h or need_w:
-            # one host sync for the scalar scale, as in the reference (:160)
-            scale = float(grad_output.item()) / float(n_valid.item())
+            # upstream gradient / #counted rows, on the device (no host sync)
+            scale = (grad_output.detach().to(torch.float32).reshape(1) / n_valid.reshape(1)).contiguous()
             ones = torch.ones_like(lse)
-            bwd = _get_bwd_module()
             w = weight.contiguous()
             h = hidden.contiguous()
             n = h.shape[0]
             for start in range(0, n, ctx.chunk_size):
                 end = min(start + ctx.chunk_size, n)
                 logits = F.linear(h[start:end], w)
-                # softmax = exp(x - lse) / 1: pass lse as the row max and 1 as the row sum
-                glog = bwd.cross_entropy_bwd_tiny_hip(
-                    logits, targets[start:end], lse[start:end], ones[start:end], ctx.softcap,
-                    ctx.ignore_index, ctx.label_smoothing, scale)
+                # softmax = exp(x - lse) / 1: lse as the row max and 1 as the row sum
+                glog = torch.empty_like(logits)
+                _lib.ce_bwd_tiny(logits, targets[start:end], lse[start:end], ones[start:end], glog,
+                                 ctx.softcap, ctx.ignore_index, ctx.label_smoothing, 1.0,
+                                 scale_dev=scale)
                 if need_h:
                     grad_hidden[start:end] = glog @ w
                 if need_w:
@@ -248,8 +288,8 @@ class ChunkedLinearCrossEntropyLoss(nn.Module):
     """Drop-in for ``nn.Linear`` + ``nn.CrossEntropyLoss`` without materialised logits.
 
     Args:
-        chunk_size: rows per chunk for the GEMM-based paths (backward, and the
-            forward when label smoothing is on).
+        chunk_size: rows per chunk of the fp32 path's GEMMs (the half-precision
+            kernels tile the problem themselves).
         softcap: logit softcap (0 = off).
         ignore_index: target value to mask (default -100).
         label_smoothing: alpha (0 = off).

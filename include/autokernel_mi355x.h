@@ -402,10 +402,10 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  *               output, as the reference's backward does with its `out`.
  * workspace: ak_selective_scan_bwd_workspace_bytes(...) bytes (saved states
  * every 16 steps and the partial sums of dB / dC / dA / dD / ddelta_bias,
- * reduced in a fixed order: results are bitwise reproducible on a given
- * device; large whole-tile shapes group 32 channels per partial dB / dC row
- * when the grid still gives every compute unit a workgroup, so dB / dC can
- * differ by rounding between devices with different CU counts).
+ * reduced in a fixed order: results are bitwise reproducible; large
+ * whole-tile shapes, with batch x ngroups x channels-per-group / 32 >= 256,
+ * group 32 channels per partial dB / dC row, a choice fixed by the shape
+ * alone, so the bits do not depend on the device's compute-unit count).
  */
 size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
                                              int64_t dstate, int64_t ngroups, int bc_flags);

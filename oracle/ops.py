@@ -105,7 +105,7 @@ def softmax_ref(x: torch.Tensor) -> torch.Tensor:
 
 
 def _capped(logits: torch.Tensor, softcap: float) -> torch.Tensor:
-    x = logits.float()
+    x = logits if logits.dtype == torch.float64 else logits.float()
     if softcap > 0:
         x = softcap * torch.tanh(x / softcap)
     return x
@@ -169,17 +169,19 @@ def ce_mean_ref(losses: torch.Tensor, targets: torch.Tensor, ignore_index: int =
     """Mean over non-ignored rows, denominator clamped to 1 (``ce_fused.py:594-622``),
     plus ``z_loss_weight * sum(lse^2)`` over the same rows and denominator
     (``:611-626``)."""
-    valid = (targets != ignore_index).float()
+    ct = losses.dtype if losses.dtype == torch.float64 else torch.float32
+    valid = (targets != ignore_index).to(ct)
     total = (losses * valid).sum()
     if z_loss_weight > 0:
-        total = total + z_loss_weight * (lse.float() ** 2 * valid).sum()
+        total = total + z_loss_weight * (lse.to(ct) ** 2 * valid).sum()
     return total / valid.sum().clamp(min=1.0)
 
 
 def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                   ignore_index: int = -100, vocab_chunk: int = 4096, softcap: float = 0.0,
-                  label_smoothing: float = 0.0):
-    """Linear + CE without materialising all logits (fp32 arithmetic).
+                  label_smoothing: float = 0.0, dtype: torch.dtype = torch.float32):
+    """Linear + CE without materialising all logits (``dtype`` arithmetic,
+    fp32 by default, float64 for the full-size checks).
 
     Follows ``kernels/hip/chunked_linear_cross_entropy.py:72-75`` (n_valid),
     ``:135-140`` (loss = sum / n_valid) and ``kernels/ce_fused.py:236-260``
@@ -188,17 +190,17 @@ def lmhead_ce_ref(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Ten
     ``:250-256``), streaming the vocabulary in ``vocab_chunk`` columns with
     an online (max, sum) merge. Returns ``(loss, lse, losses)``.
     """
-    h = hidden.float()
+    h = hidden.to(dtype)
     V = weight.shape[0]
     n = h.shape[0]
-    m = torch.full((n,), -math.inf)
-    s = torch.zeros(n)
+    m = torch.full((n,), -math.inf, dtype=dtype)
+    s = torch.zeros(n, dtype=dtype)
     t = targets.long()
-    xt = torch.zeros(n)
-    zsum = torch.zeros(n)
+    xt = torch.zeros(n, dtype=dtype)
+    zsum = torch.zeros(n, dtype=dtype)
     for v0 in range(0, V, vocab_chunk):
         v1 = min(V, v0 + vocab_chunk)
-        logits = _capped(h @ weight[v0:v1].float().t(), softcap)
+        logits = _capped(h @ weight[v0:v1].to(dtype).t(), softcap)
         cm = logits.max(dim=-1).values
         nm = torch.maximum(m, cm)
         s = s * torch.exp(m - nm) + torch.exp(logits - nm[:, None]).sum(-1)

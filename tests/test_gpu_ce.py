@@ -166,3 +166,36 @@ def test_ce_count_and_mean_many_rows():
     all_ignored = torch.full((10,), -7, device=DEV)
     assert float(_lib.ce_count_valid(all_ignored, -7)[0]) == 1.0
     assert float(_lib.ce_mean(torch.ones(10, device=DEV), None, all_ignored, -7)) == 0.0
+
+
+@pytest.mark.parametrize("up", [1.0, 0.7])
+def test_ce_fused_backward_scales_on_device(up):
+    """Fused mode: the backward applies the upstream gradient on the device
+    (torch's sync debug mode set to error around it). An upstream gradient
+    of 1 returns the gradient the forward wrote, bit for bit; 0.7 the same
+    gradient times bf16(0.7), rounded once."""
+    need_gpu()
+    from kernels.ce_fused import ce_full
+    g = torch.Generator().manual_seed(33)
+    base = (2 * torch.randn(64, 3001, generator=g)).bfloat16()
+    t = torch.randint(0, 3001, (64,), generator=g)
+    t[5] = -100
+    say("ce fused backward on device", up)
+    x = base.to(DEV).requires_grad_()
+    loss = ce_full(x, t.to(DEV), mode="fused")
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        (up * loss).backward()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    # the forward's own gradient: the same kernel call the fused forward makes
+    from kernels.hip import _lib
+    td = t.to(DEV)
+    denom = _lib.ce_count_valid(td, -100)
+    gref = torch.empty_like(x)
+    f32 = dict(dtype=torch.float32, device=DEV)
+    _lib.ce_fwd(base.to(DEV), td, torch.empty(64, **f32), torch.empty(64, **f32), None, None, gref,
+                0.0, -100, 0.0, 1.0, scale_dev=denom[1:])
+    want = gref if up == 1.0 else gref * torch.tensor(up, device=DEV).bfloat16()
+    assert torch.equal(x.grad, want)

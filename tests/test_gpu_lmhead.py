@@ -118,7 +118,24 @@ def test_lmhead_all_ignored_and_bad_targets():
     assert abs(float(loss) - math.log(500)) < 1e-5
 
 
+_C4_ORACLE = {}
+# bf16 round to nearest: within 2^-8 of the value (8 significant bits), with
+# 1% room for the fp32 arithmetic before the rounding
+_U8 = 1.01 * 2.0 ** -8
+
+
+def _c4_oracle(c):
+    """float64 oracle (loss, lse, per-row losses) of the whole C4 problem,
+    computed once per process (about 630 GFLOP on the host)."""
+    if not _C4_ORACLE:
+        loss, lse, losses = ops.lmhead_ce_ref(c["h"], c["W"], c["t"], dtype=torch.float64)
+        _C4_ORACLE.update(loss=loss, lse=lse, losses=losses)
+    return _C4_ORACLE["loss"], _C4_ORACLE["lse"], _C4_ORACLE["losses"]
+
+
 def test_c4_full_size():
+    """C4 against the float64 oracle on all 8,192 rows: logsumexp, per-row
+    losses (zero on ignored rows), the mean, and the count of valid rows."""
     need_gpu()
     import bench
     c = bench.gen_c4()
@@ -127,23 +144,12 @@ def test_c4_full_size():
     t = c["t"]
     valid = t != -100
     assert int(nv) == int(valid.sum()) == 8192 - 409
-    # logsumexp of a row subset against the oracle
-    idx = torch.randperm(8192, generator=torch.Generator().manual_seed(2))[:384].sort().values
-    _, rlse, rl = ops.lmhead_ce_ref(c["h"][idx], c["W"], t[idx])
-    assert torch.allclose(lse.cpu()[idx].double(), rlse.double(), rtol=1e-4)
-    assert torch.allclose(losses.cpu()[idx].double(), rl.double(), rtol=1e-3, atol=1e-3)
-    # every row's logsumexp against an fp32 GPU reference (fp32 GEMM of the
-    # bf16 operands in 1024-row chunks, then logsumexp): the oracle above
-    # covers a subset in float64, this one all 8192 rows
-    hd, Wd = c["h"].to(DEV).float(), c["W"].to(DEV).float().contiguous()
-    ref_all = torch.cat([torch.logsumexp(hd[i:i + 1024] @ Wd.t(), dim=-1) for i in range(0, 8192, 1024)])
-    assert torch.allclose(lse.double(), ref_all.double(), rtol=1e-4, atol=0.0)
-    del hd, Wd
-    # the mean over all rows: GPU lse with exact target logits from the CPU
-    tv = t.clamp(min=0)
-    xt = (c["h"].float() * c["W"][tv].float()).sum(-1)
-    ref_loss = ((lse.cpu().double() - xt.double()) * valid.double()).sum() / valid.sum()
-    assert abs(float(loss) - float(ref_loss)) <= 1e-3 * abs(float(ref_loss))
+    rloss, rlse, rl = _c4_oracle(c)
+    lse_c, losses_c = lse.cpu().double(), losses.cpu().double()
+    assert torch.allclose(lse_c, rlse, rtol=2e-5, atol=0.0), float((lse_c - rlse).abs().max())
+    assert torch.allclose(losses_c, rl, rtol=2e-5, atol=2e-5), float((losses_c - rl).abs().max())
+    assert bool((losses.cpu()[~valid] == 0).all())
+    assert abs(float(loss) - float(rloss)) <= 1e-5 * abs(float(rloss)), (float(loss), float(rloss))
     # deterministic: same bits on a second call
     loss2, lse2, _, _ = _run(c["h"], c["W"], c["t"])
     assert torch.equal(lse2, lse) and torch.equal(loss2, loss)
@@ -451,8 +457,18 @@ def test_lmhead_ce_backward_vocab_ranges(monkeypatch, softcap, ls):
 
 
 def test_c4_full_size_backward():
-    """C4: dlogits rows against float64, grad_hidden rows against float64,
-    grad_weight against an fp32 torch reference on the GPU; deterministic."""
+    """C4 backward, elementwise against the float64 oracle:
+    * dlogits (the kernel's bf16) on 128 token rows x every vocab column and
+      on every token x 768 vocab columns (a vocab-tile boundary, the middle
+      and the ragged tail 50,176-50,303): within bf16 rounding of the oracle;
+    * grad_weight on those 768 vocab rows and grad_hidden on the 128 token
+      rows: tightly against the float64 GEMM of the kernel's own dlogits
+      (the GEMMs' fp32 accumulation and bf16 output rounding), and against
+      the oracle gradient within the bound that dlogits' bf16 rounding
+      allows (2^-8 of the sum of |terms| per element);
+    bf16 rounding (round to nearest, 8 significant bits) is within 2^-8 of
+    the value; the bars take 1.01 times that for the fp32 arithmetic before it.
+    deterministic across two calls."""
     need_gpu()
     import bench
     from kernels.hip import _lib
@@ -466,27 +482,51 @@ def test_c4_full_size_backward():
     gh, gw = lmhead_ce_backward(h, W, t, lse, denom, one)
     gh2, gw2 = lmhead_ce_backward(h, W, t, lse, denom, one)
     assert torch.equal(gh, gh2) and torch.equal(gw, gw2)
-    scale = 1.0 / float(denom)
-    idx = torch.randperm(8192, generator=torch.Generator().manual_seed(5))[:128].sort().values
     dz = torch.empty(8192, 50304, dtype=torch.bfloat16, device=DEV)
     _lib.lmhead_ce_bwd(h, W, t, lse, one.reshape(1), denom.reshape(1), dz, -100)
-    ref = _dz_ref(c["h"][idx], c["W"], c["t"][idx], lse.cpu()[idx], scale)
-    got = dz[idx.to(DEV)].double().cpu()
-    assert bool(((got - ref).abs() <= 2.0 ** -8 * ref.abs() + 1e-6 * scale).all())
-    ghr = ref @ c["W"].double()
-    rel = float((gh.cpu()[idx].double() - ghr).norm() / ghr.norm())
-    assert rel < 5e-3, rel
-    # grad_weight: fp32 torch reference (logits materialised in fp32 on the GPU)
-    z = h.float() @ W.float().t()
-    p = torch.softmax(z, dim=-1)
-    del z
-    valid = t != -100
-    p[torch.arange(8192, device=DEV)[valid], t[valid]] -= 1.0
+    _, rlse, _ = _c4_oracle(c)
+    tc = c["t"]
+    valid = tc != -100
+    scale = 1.0 / float(valid.sum())
+    h64, W64 = c["h"].double(), c["W"].double()
+
+    # vocab rows: the first tile, a tile boundary in the middle, the last tile
+    # (50,176-50,303 is the ragged tail of 256-row vocab tiles) and the one before
+    vsel = torch.cat([torch.arange(0, 256), torch.arange(25472, 25728), torch.arange(50048, 50304)])
+    p = torch.exp(h64 @ W64[vsel].t() - rlse[:, None])             # [8192, 768]
+    hit = (tc[:, None] == vsel[None, :]) & valid[:, None]
+    p = (p - hit.double()) * scale
     p[~valid] = 0.0
-    gwr = (p.t().contiguous() @ h.float()) * scale
-    del p
-    rel = float((gw.float() - gwr).norm() / gwr.norm())
-    assert rel < 5e-3, rel
+    dzv = dz[:, vsel.to(DEV)].double().cpu()
+    assert bool(((dzv - p).abs() <= _U8 * p.abs() + 1e-6 * scale).all())
+    gw_sel = gw[vsel.to(DEV)].double().cpu()
+    tight = dzv.t() @ h64
+    terms = dzv.abs().t() @ h64.abs()
+    assert bool(((gw_sel - tight).abs() <= _U8 * tight.abs() + 1e-5 * terms).all())
+    ref = p.t() @ h64
+    bound = (_U8 * ref.abs() + (_U8 + 2e-5) * (p.abs().t() @ h64.abs())
+             + 1e-6 * scale * h64.abs().sum(0)[None, :])
+    assert bool(((gw_sel - ref).abs() <= bound).all())
+    del p, dzv, hit
+
+    # token rows: 128 random rows, every vocab column
+    idx = torch.randperm(8192, generator=torch.Generator().manual_seed(5))[:128].sort().values
+    p = torch.exp(h64[idx] @ W64.t() - rlse[idx][:, None])           # [128, 50304]
+    tv = tc[idx]
+    rows = torch.arange(128)[valid[idx]]
+    p[rows, tv[valid[idx]]] -= 1.0
+    p *= scale
+    p[~valid[idx]] = 0.0
+    dzr = dz[idx.to(DEV)].double().cpu()
+    assert bool(((dzr - p).abs() <= _U8 * p.abs() + 1e-6 * scale).all())
+    gh_sel = gh[idx.to(DEV)].double().cpu()
+    tight = dzr @ W64
+    terms = dzr.abs() @ W64.abs()
+    assert bool(((gh_sel - tight).abs() <= _U8 * tight.abs() + 1e-5 * terms).all())
+    ref = p @ W64
+    bound = (_U8 * ref.abs() + (_U8 + 2e-5) * (p.abs() @ W64.abs())
+             + 1e-6 * scale * W64.abs().sum(0)[None, :])
+    assert bool(((gh_sel - ref).abs() <= bound).all())
 
 
 def test_c4_backward_homogeneous_in_grad_loss_bitwise():
@@ -531,3 +571,64 @@ def test_fused_and_row_chunked_softcap_paths_agree(ls):
     assert abs(l1 - l2) <= 1e-3 * abs(l2)
     assert float((gh1 - gh2).norm() / gh2.norm()) < 1e-2
     assert float((gw1 - gw2).norm() / gw2.norm()) < 1e-2
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 100), (torch.float16, 200), (torch.bfloat16, 40),
+                                     (torch.bfloat16, 256), (torch.float32, 100)])
+def test_chunked_linear_ce_any_hidden_size_no_host_sync(monkeypatch, dtype, d):
+    """Half-precision inputs take the matrix-core kernels at every hidden size
+    (a size that is not a multiple of 64 is zero-extended; the row-chunked
+    GEMM path is made to raise here), fp32 inputs the row-chunked path; the
+    forward and backward of both run with torch's sync debug mode set to
+    error, so neither reads a device value on the host. Loss and gradients
+    against float64 autograd at the chunked-CE bars."""
+    need_gpu()
+    from kernels.hip import chunked_linear_cross_entropy as clce
+    if dtype != torch.float32:
+        def _no_fallback(*a, **k):
+            raise AssertionError("half-precision input took the row-chunked GEMM path")
+        monkeypatch.setattr(clce, "_chunked_forward", _no_fallback)
+    g = torch.Generator().manual_seed(d)
+    n, V = 333, 2100
+    h0 = torch.randn(n, d, generator=g)
+    W0 = 0.05 * torch.randn(V, d, generator=g)
+    t = torch.randint(0, V, (n,), generator=g)
+    t[::11] = -100
+    say("chunked linear ce any d, no sync", dtype, d)
+    h = h0.to(dtype).to(DEV).requires_grad_()
+    W = W0.to(dtype).to(DEV).requires_grad_()
+    td = t.to(DEV)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        loss = clce.ChunkedLinearCrossEntropyLoss(chunk_size=128, softcap=15.0)(h, W, td)
+        (0.8 * loss).backward()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    hr = h0.to(dtype).double().requires_grad_()
+    Wr = W0.to(dtype).double().requires_grad_()
+    ref = F.cross_entropy(15.0 * torch.tanh((hr @ Wr.t()) / 15.0), t)
+    (0.8 * ref).backward()
+    assert abs(float(loss) - float(ref)) <= 1e-3 * abs(float(ref))
+    assert h.grad.shape == (n, d) and W.grad.shape == (V, d)
+    for got, want in ((h.grad, hr.grad), (W.grad, Wr.grad)):
+        rel = float((got.double().cpu() - want).norm() / want.norm())
+        assert rel < 1e-2, rel
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_chunked_linear_ce_empty_batch(dtype):
+    """No rows: loss 0 (the mean over max(1, 0) counted rows, as the
+    reference's chunk loop gives), an empty hidden gradient and a zero weight
+    gradient."""
+    need_gpu()
+    from kernels.hip.chunked_linear_cross_entropy import ChunkedLinearCrossEntropyLoss
+    h = torch.zeros(0, 128, dtype=dtype, device=DEV, requires_grad=True)
+    W = (0.05 * torch.randn(500, 128)).to(dtype).to(DEV).requires_grad_()
+    t = torch.zeros(0, dtype=torch.int64, device=DEV)
+    say("chunked linear ce empty batch", dtype)
+    loss = ChunkedLinearCrossEntropyLoss()(h, W, t)
+    loss.backward()
+    assert float(loss) == 0.0
+    assert h.grad.shape == (0, 128)
+    assert W.grad is not None and bool((W.grad == 0).all())

@@ -144,3 +144,61 @@ def test_grad_gemm_workspace_too_small_is_an_error():
     small = torch.empty(need - 256, dtype=torch.uint8, device=DEV)
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.lmhead_grad_hidden(dl, W, out, 0, small)
+
+
+def test_grad_hidden_nan_in_k_padding_is_zeroed():
+    """The dlogits padding columns [vocab, vocab rounded up to 64) filled with
+    NaN: the wrapper zeroes them before the kernel reads its last K block, so
+    grad_hidden equals the result from zero padding bit for bit (and is
+    finite); a view whose storage ends inside the last row pitch is refused."""
+    need_gpu()
+    from kernels.hip import _lib
+    gen = torch.Generator().manual_seed(41)
+    n, vocab, d = 300, 1000, 128
+    say("grad_hidden NaN K padding")
+    dl0 = _dl(n, vocab, torch.bfloat16, gen)
+    pitch = dl0.stride(0)
+    buf = torch.full((n, pitch), float("nan"), dtype=torch.bfloat16, device=DEV)
+    buf[:, :vocab] = dl0
+    W = (0.02 * torch.randn(vocab, d, generator=gen)).bfloat16().to(DEV)
+    ws = torch.empty(max(_lib.lmhead_grad_workspace_bytes(n, vocab, d), 1), dtype=torch.uint8, device=DEV)
+    want = torch.empty(n, d, dtype=torch.bfloat16, device=DEV)
+    got = torch.empty_like(want)
+    _lib.lmhead_grad_hidden(dl0, W, want, _lib.GEMM_OUT_DTYPE, ws)
+    _lib.lmhead_grad_hidden(buf[:, :vocab], W, got, _lib.GEMM_OUT_DTYPE, ws)
+    assert bool(torch.isfinite(got).all()) and torch.equal(got, want)
+    short = torch.zeros(n * pitch - 32, dtype=torch.bfloat16, device=DEV)
+    view = torch.as_strided(short, (n, vocab), (pitch, 1))
+    with pytest.raises(ValueError):
+        _lib.lmhead_grad_hidden(view, W, got, _lib.GEMM_OUT_DTYPE, ws)
+
+
+def test_grad_gemm_wrapper_rejects_mismatched_outputs():
+    """Output dtype against out_mode, operand dtype and shapes are checked in
+    the wrapper before the C-ABI is called (an fp32 out_mode with a bf16
+    output would otherwise store fp32 elements at a bf16 pitch)."""
+    need_gpu()
+    from kernels.hip import _lib
+    gen = torch.Generator().manual_seed(43)
+    n, vocab, d = 64, 256, 64
+    dl = _dl(n, vocab, torch.bfloat16, gen)
+    W = torch.zeros(vocab, d, dtype=torch.bfloat16, device=DEV)
+    h = torch.zeros(n, d, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(max(_lib.lmhead_grad_workspace_bytes(n, vocab, d), 1), dtype=torch.uint8, device=DEV)
+    bad = [
+        lambda: _lib.lmhead_grad_hidden(dl, W, torch.empty(n, d, dtype=torch.bfloat16, device=DEV),
+                                        _lib.GEMM_OUT_F32, ws),
+        lambda: _lib.lmhead_grad_hidden(dl, W, torch.empty(n, d, dtype=torch.float32, device=DEV),
+                                        _lib.GEMM_OUT_DTYPE, ws),
+        lambda: _lib.lmhead_grad_hidden(dl, W.half(), torch.empty(n, d, dtype=torch.bfloat16, device=DEV),
+                                        _lib.GEMM_OUT_DTYPE, ws),
+        lambda: _lib.lmhead_grad_hidden(dl, W, torch.empty(n + 1, d, dtype=torch.bfloat16, device=DEV),
+                                        _lib.GEMM_OUT_DTYPE, ws),
+        lambda: _lib.lmhead_grad_weight(dl, h, torch.empty(vocab, d + 64, dtype=torch.bfloat16, device=DEV),
+                                        _lib.GEMM_OUT_DTYPE, ws),
+        lambda: _lib.lmhead_grad_weight(dl, W, torch.empty(vocab, d, dtype=torch.bfloat16, device=DEV),
+                                        _lib.GEMM_OUT_DTYPE, ws),
+    ]
+    for call in bad:
+        with pytest.raises(ValueError):
+            call()

@@ -270,6 +270,31 @@ def test_lmhead_ce_ref_matches_materialised():
         assert torch.allclose(s2, lse, rtol=1e-6) and torch.allclose(l2, loss, rtol=1e-6)
 
 
+@pytest.mark.parametrize("softcap,ls", [(0.0, 0.0), (5.0, 0.0), (0.0, 0.2), (5.0, 0.2)])
+def test_lmhead_ce_ref_float64_matches_torch(softcap, ls):
+    """The float64 mode (used for the full-size C4 checks) against
+    F.cross_entropy / logsumexp of the float64 logits, to float64 rounding,
+    for every vocab chunking; a wrong merge of the chunk partials, a dropped
+    smoothing or softcap term, or a float32 step inside would miss 1e-12."""
+    g = torch.Generator().manual_seed(29)
+    h = torch.randn(64, 48, generator=g)
+    W = 0.5 * torch.randn(700, 48, generator=g)
+    t = torch.randint(0, 700, (64,), generator=g)
+    t[[1, 40]] = -100
+    z = h.double() @ W.double().t()
+    if softcap > 0:
+        z = softcap * torch.tanh(z / softcap)
+    ref = F.cross_entropy(z, t, label_smoothing=ls)
+    ref_per = F.cross_entropy(z, t, label_smoothing=ls, reduction="none")
+    for chunk in (64, 333, 4096):
+        loss, lse, per = ops.lmhead_ce_ref(h, W, t, vocab_chunk=chunk, softcap=softcap,
+                                           label_smoothing=ls, dtype=torch.float64)
+        assert lse.dtype == per.dtype == loss.dtype == torch.float64
+        assert torch.allclose(lse, torch.logsumexp(z, -1), rtol=1e-12, atol=0)
+        assert torch.allclose(per, ref_per, rtol=1e-12, atol=1e-12)
+        assert abs(float(loss) - float(ref)) <= 1e-12 * abs(float(ref))
+
+
 # ---------------------------------------------------------------------------
 # Scans
 # ---------------------------------------------------------------------------
