@@ -350,7 +350,8 @@ def time_case(case, steps, warmup, pairs=ROOFLINE_PAIRS):
     event pair around the K back-to-back launches on the launch stream,
     median ms per launch over ``pairs`` (>= 100) launches each bracketed by
     its own event pair and queued behind a held stream, host us per
-    launcher call)."""
+    launcher call, mean ms per launch over about SUSTAIN_S seconds of
+    back-to-back launches, and that run's launch count)."""
     nset = len(case.sets)
     for i in range(warmup):
         case.launch(case.sets[i % nset])
@@ -367,7 +368,32 @@ def time_case(case, steps, warmup, pairs=ROOFLINE_PAIRS):
     mean_ms = ev0.elapsed_time(ev1) / steps
     n = max(pairs, ROOFLINE_PAIRS)
     durations, host_us = held_event_pairs(case, n)
-    return wall, mean_ms, statistics.median(durations), host_us
+    med_ms = statistics.median(durations)
+    sus_ms, sus_n = sustained_run(case, med_ms)
+    return wall, mean_ms, med_ms, host_us, sus_ms, sus_n
+
+
+# Seconds of back-to-back launches behind the sustained figure (at least 20
+# and at most 5000 launches). A kernel launched after an idle or lighter
+# phase runs its first few milliseconds in a power-management transient
+# (the clock overshoots, then throttles back); a run this long reports the
+# rate the kernel settles at.
+SUSTAIN_S = 0.25
+
+
+def sustained_run(case, med_ms):
+    """Mean ms per launch over about SUSTAIN_S seconds of back-to-back
+    launches (one event pair around them), and the launch count."""
+    nset = len(case.sets)
+    n = int(min(5000, max(20, SUSTAIN_S / (med_ms * 1e-3))))
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(n):
+        case.launch(case.sets[i % nset])
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / n, n
 
 
 # GPU cycles of the spin kernel that holds the stream before each batch of
@@ -580,7 +606,7 @@ def main(argv=None):
     head = None
     for name in names:
         case = make_case(name)
-        wall, mean_ms, med_ms, host_us = time_case(case, args.steps, args.warmup, args.steps)
+        wall, mean_ms, med_ms, host_us, sus_ms, sus_n = time_case(case, args.steps, args.warmup, args.steps)
         # rooflines from the median of the per-launch event pairs
         if case.bound == "hbm":
             achieved = case.work / (med_ms * 1e-3) / 1e9
@@ -588,16 +614,25 @@ def main(argv=None):
         else:
             achieved = case.work / (med_ms * 1e-3) / 1e12
             peak, unit = BF16_PEAK_TFLOPS, "TFLOP/s"
+        sustained = achieved * med_ms / sus_ms
         rec = {
             "workload": case.workload,
             "kernel": case.kernel_name,
             "us_per_launch_median_event_pairs": round(med_ms * 1e3, 2),
             "event_pairs": max(ROOFLINE_PAIRS, args.steps),
-            "us_per_launch_mean": round(mean_ms * 1e3, 2),
             "achieved": round(achieved, 1),
             "unit": unit,
             "peak": peak,
             "frac": round(achieved / peak, 4),
+            # the K timed back-to-back launches (one event pair around them),
+            # which start in the power-management transient
+            "us_per_launch_mean": round(mean_ms * 1e3, 2),
+            "frac_mean": round(achieved * med_ms / mean_ms / peak, 4),
+            # about SUSTAIN_S seconds of back-to-back launches: the settled rate
+            "us_per_launch_sustained": round(sus_ms * 1e3, 2),
+            "sustained_launches": sus_n,
+            "achieved_sustained": round(sustained, 1),
+            "frac_sustained": round(sustained / peak, 4),
             "tokens_per_s": round(case.tokens / (med_ms * 1e-3), 1),
             "input_sets": len(case.sets),
             "wall_ms_per_step": round(wall / args.steps * 1e3, 4),
@@ -609,6 +644,7 @@ def main(argv=None):
             floor_us = case.valu_cycles / 1024 / 2.4e3
             rec["valu_roofline"] = {"floor_us": round(floor_us, 1),
                                     "frac": round(floor_us / (med_ms * 1e3), 4),
+                                    "frac_sustained": round(floor_us / (sus_ms * 1e3), 4),
                                     "model": case.valu_model}
         if name.startswith("c5") or name == "n64":
             rec["Mtok_per_s"] = round(case.tokens / (med_ms * 1e-3) / 1e6, 2)
