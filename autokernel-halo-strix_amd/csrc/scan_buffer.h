@@ -69,6 +69,21 @@ __device__ __forceinline__ void bstore1(Rsrc r, uint32_t voff, float v) {
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, from_f32<T>(v)), r, (int)voff, 0, 0);
 }
 
+// Four consecutive elements of T from a float4 (one 16- or 8-byte store),
+// the tile offset in the scalar offset.
+template <typename T>
+__device__ __forceinline__ void bstore4_at(Rsrc r, uint32_t voff, uint32_t soff, float4 v) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4 w = {__builtin_bit_cast(uint32_t, v.x), __builtin_bit_cast(uint32_t, v.y),
+                     __builtin_bit_cast(uint32_t, v.z), __builtin_bit_cast(uint32_t, v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, (int)voff, (int)soff, 0);
+  } else {
+    auto bits = [](float f) { return (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(f)); };
+    const u32x2 w = {bits(v.x) | (bits(v.y) << 16), bits(v.z) | (bits(v.w) << 16)};
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, (int)voff, (int)soff, 0);
+  }
+}
+
 // bstore1 with the tile offset in the scalar offset.
 template <typename T>
 __device__ __forceinline__ void bstore1_at(Rsrc r, uint32_t voff, uint32_t soff, float v) {

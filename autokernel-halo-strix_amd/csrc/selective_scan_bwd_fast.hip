@@ -24,7 +24,9 @@
 // * the gate and the saved-states dz (kDz: the forward's pre-gate output is
 //   given, so dz is formed here) are compile-time choices, and whole tiles
 //   need no bounds tests, so each 16-step block is one basic block the
-//   scheduler can interleave.
+//   scheduler can interleave;
+// * du, ddelta and dz are kept for a whole tile and stored as whole row
+//   segments (four steps per lane) after its last block.
 // At the C5 shape (batch 4, dim 2048, seqlen 4096, dstate 16) the pass takes
 // about 435 us with 16-channel workgroups (579 us for the general one on the
 // same box) and 1.5% less with 32-channel ones, whose partial sums then read
@@ -91,8 +93,7 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
   const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);
   const uint32_t vo_g1 = (uint32_t)(wc * p.go_ds + n) * sizeof(TU);
   const uint32_t vo_z1 = kGate ? (uint32_t)(wc * p.z_ds + n) * sizeof(TU) : vo_u1;
-  const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);   // du, dz, y (out_prez)
-  const uint32_t vo_dd1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TD);  // ddelta
+  const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);   // y (out_prez)
   // B / C staging by waves 0-3: state sn, steps 4 q .. 4 q + 3
   const bool stager = wave < 4;
   const int sn = (tid / 16) % 16, q = tid % 16;
@@ -137,6 +138,16 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
   }
   Blk pb;
   load_blk(nt - 1, 3, pb);
+  // A tile's du / ddelta / dz, one value per 16-step block (step 16 blk + n
+  // of channel wc), stored once the tile is done as whole row segments: four
+  // consecutive steps per lane, so each channel row of the tile is one
+  // 128-byte (2-byte types) or 256-byte (fp32) store. Stored per block, each
+  // row went out as 32- or 64-byte segments a block apart, and the partially
+  // written lines left L2 between them: at the C5 shape that cost about 47 MB
+  // of extra fetch and 61 MB of extra writes per pass.
+  float st_du[4], st_dd[4], st_dz[4];
+  const uint32_t vo_o4 = (uint32_t)(wc * p.o_ds + 4 * n) * sizeof(TU);
+  const uint32_t vo_dd4 = (uint32_t)(wc * p.o_ds + 4 * n) * sizeof(TD);
   for (int t = nt - 1; t >= 0; --t) {
     const int l0 = t * kScanT;
     __syncthreads();
@@ -250,15 +261,13 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
         saw += v.y + v.w;
       }
       __builtin_amdgcn_wave_barrier();
-      const uint32_t lo = (uint32_t)(l0 + 16 * BLK);
-      if constexpr (kGate && kDz)
-        bstore1_at<TU>(rs_dz, vo_o1, lo * sizeof(TU), go * raw_f32<TU>(cb.yr) * sg * fmaf(zv, 1.0f - sg, 1.0f));
+      if constexpr (kGate && kDz) st_dz[BLK] = go * raw_f32<TU>(cb.yr) * sg * fmaf(zv, 1.0f - sg, 1.0f);
       float ddl = fmaf(uv, sgb, saw);
       if constexpr (kSoftplus) {
         if (x <= 20.0f) ddl *= sigmoid_f32(x);
       }
-      bstore1_at<TU>(rs_du, vo_o1, lo * sizeof(TU), fmaf(dskip, dyv, dlt * sgb));
-      bstore1_at<TD>(rs_dd, vo_dd1, lo * sizeof(TD), ddl);
+      st_du[BLK] = fmaf(dskip, dyv, dlt * sgb);
+      st_dd[BLK] = ddl;
       dD_acc = fmaf(dyv, uv, dD_acc);
       dbias_acc += ddl;
     };
@@ -266,6 +275,28 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
     block(std::integral_constant<int, 2>{});
     block(std::integral_constant<int, 1>{});
     block(std::integral_constant<int, 0>{});
+    {
+      // the tile's outputs through the wave's transpose buffer (free between
+      // tiles): [stream][channel c, pitch 80 floats][step], conflict-free for
+      // the b32 writes and the b128 reads
+      constexpr int kSP = 80, kSS = 4 * kSP;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        tb[c * kSP + 16 * blk + n] = st_du[blk];
+        tb[kSS + c * kSP + 16 * blk + n] = st_dd[blk];
+        if constexpr (kGate && kDz) tb[2 * kSS + c * kSP + 16 * blk + n] = st_dz[blk];
+      }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+      bstore4_at<TU>(rs_du, vo_o4, (uint32_t)l0 * sizeof(TU), *reinterpret_cast<const float4*>(&tb[c * kSP + 4 * n]));
+      bstore4_at<TD>(rs_dd, vo_dd4, (uint32_t)l0 * sizeof(TD),
+                     *reinterpret_cast<const float4*>(&tb[kSS + c * kSP + 4 * n]));
+      if constexpr (kGate && kDz)
+        bstore4_at<TU>(rs_dz, vo_o4, (uint32_t)l0 * sizeof(TU),
+                       *reinterpret_cast<const float4*>(&tb[2 * kSS + c * kSP + 4 * n]));
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+    }
 
     __syncthreads();
     {
