@@ -24,6 +24,7 @@
 // rows per column in a fixed order: dw is deterministic (the reference
 // accumulated it with fp32 atomics).
 #include <atomic>
+#include <mutex>
 
 #include "ak_common.h"
 
@@ -394,21 +395,35 @@ int bwd_entry(const char* name, const void* x, const void* w, const void* dy, co
 // ---------------------------------------------------------------------------
 // Scratch of the no-allocation entry point: the partial weight-gradient rows
 // live in this file-scope device array (one copy per GPU, held until the
-// process ends) instead of a caller workspace. In host code the array's name
-// is only a stand-in; its device address is queried once per device with
-// hipGetSymbolAddress (with that device current) and kept in
-// g_scratch_addr. Calls on one GPU share the array: concurrent calls on one
-// device race on it.
+// process ends) instead of a caller workspace. The array is cut into
+// kNoAllocSlots slots of kNoAllocSlotBytes, and each stream that calls the
+// entry point on a device gets a slot of its own (the first kNoAllocSlots
+// streams, for the life of the process): work queued on different streams,
+// such as a captured graph replayed beside eager calls, never shares partial
+// rows, and calls on one stream are ordered by the stream. In host code the
+// array's name is only a stand-in; its device address is queried once per
+// device with hipGetSymbolAddress (with that device current) and kept in
+// g_scratch_addr.
 // ---------------------------------------------------------------------------
-constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;  // 16 MiB
+constexpr size_t kNoAllocSlotBytes = (size_t)16 << 20;  // 16 MiB per stream
+constexpr int kNoAllocSlots = 4;
 constexpr int kMaxDevices = 64;
 
-__device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+__device__ __align__(256) float scratch[kNoAllocSlots * kNoAllocSlotBytes / sizeof(float)];
 
 std::atomic<float*> g_scratch_addr[kMaxDevices];
 
-// Device address of `scratch` on the current device (queried on first use).
-int scratch_addr(const char* name, float** out) {
+// Per device: the streams that own the slots, in slot order.
+struct SlotTable {
+  std::mutex m;
+  hipStream_t owner[kNoAllocSlots];
+  int used = 0;
+};
+SlotTable g_slots[kMaxDevices];
+
+// Device address of `scratch` on the current device (queried on first use),
+// and the device's index.
+int scratch_addr(const char* name, float** out, int* dev_out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0)
     return ak_set_error(AK_ERR_LAUNCH, "%s: no current HIP device", name);
@@ -425,6 +440,28 @@ int scratch_addr(const char* name, float** out) {
     g_scratch_addr[dev].store(p, std::memory_order_release);
   }
   *out = p;
+  *dev_out = dev;
+  return AK_OK;
+}
+
+// The slot of `stream` on device `dev`, assigning a free one on the stream's
+// first call; more than kNoAllocSlots streams on one device are refused.
+int scratch_slot(const char* name, int dev, hipStream_t stream, int* slot) {
+  SlotTable& t = g_slots[dev];
+  std::lock_guard<std::mutex> lock(t.m);
+  for (int i = 0; i < t.used; ++i)
+    if (t.owner[i] == stream) {
+      *slot = i;
+      return AK_OK;
+    }
+  if (t.used == kNoAllocSlots)
+    return ak_set_error(AK_ERR_UNSUPPORTED,
+                        "%s: the fixed scratch has %d per-stream slots on device %d and %d "
+                        "streams already own them; call from one of those streams or use "
+                        "ak_fused_add_rmsnorm_bwd with a workspace",
+                        name, kNoAllocSlots, dev, kNoAllocSlots);
+  t.owner[t.used] = stream;
+  *slot = t.used++;
   return AK_OK;
 }
 
@@ -468,19 +505,24 @@ extern "C" int ak_fused_add_rmsnorm_bwd_noalloc(const void* hidden, const void* 
   const ak::BwdPlan plan = ak::plan_for(hidden, weight, grad_normed, grad_hidden, grad_x,
                                               rows, cols, ld_h, ld_gn, ld_gh, ld_gx, dtype);
   const size_t need = grad_weight && rows > 0 ? ak::plan_ws_bytes(plan, cols) : 0;
-  if (need > ak::kNoAllocScratchBytes)
+  if (need > ak::kNoAllocSlotBytes)
     return ak_set_error(AK_ERR_WORKSPACE,
                         "%s: %zu bytes of scratch needed (%d partial rows x %lld cols x 4), "
-                        "the fixed scratch holds %zu; use ak_fused_add_rmsnorm_bwd with a workspace",
-                        name, need, plan.nparts, (long long)cols, ak::kNoAllocScratchBytes);
+                        "a stream's slot of the fixed scratch holds %zu; use "
+                        "ak_fused_add_rmsnorm_bwd with a workspace",
+                        name, need, plan.nparts, (long long)cols, ak::kNoAllocSlotBytes);
   if (rows > 0 && (!hidden || !weight || !grad_normed || !grad_x))
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  const hipStream_t s = ak_stream(stream);
   float* part = nullptr;
   if (need > 0) {
-    rc = ak::scratch_addr(name, &part);
+    int dev = -1, slot = -1;
+    rc = ak::scratch_addr(name, &part, &dev);
     if (rc) return rc;
+    rc = ak::scratch_slot(name, dev, s, &slot);
+    if (rc) return rc;
+    part += (size_t)slot * (ak::kNoAllocSlotBytes / sizeof(float));
   }
   return ak::enqueue_bwd(name, plan, hidden, weight, grad_normed, grad_hidden, grad_x,
-                         grad_weight, part, rows, cols, ld_h, ld_gn, ld_gh, ld_gx, eps, dtype,
-                         ak_stream(stream));
+                         grad_weight, part, rows, cols, ld_h, ld_gn, ld_gh, ld_gx, eps, dtype, s);
 }

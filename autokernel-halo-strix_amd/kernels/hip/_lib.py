@@ -301,8 +301,10 @@ def fused_add_rmsnorm_bwd(hidden: torch.Tensor, weight: torch.Tensor,
     _check(rc, "ak_fused_add_rmsnorm_bwd")
 
 
-# Bytes of the fixed scratch behind ak_fused_add_rmsnorm_bwd_noalloc.
+# Bytes of one stream's slot of the fixed scratch behind
+# ak_fused_add_rmsnorm_bwd_noalloc (four slots per GPU, one per calling stream).
 NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_STREAM_SLOTS = 4
 
 
 def fused_add_rmsnorm_bwd_noalloc(hidden: torch.Tensor, weight: torch.Tensor,
@@ -310,8 +312,9 @@ def fused_add_rmsnorm_bwd_noalloc(hidden: torch.Tensor, weight: torch.Tensor,
                                   grad_x: torch.Tensor, grad_weight: Optional[torch.Tensor],
                                   eps: float) -> None:
     """:func:`fused_add_rmsnorm_bwd` through the entry point that allocates
-    nothing (the library's fixed scratch holds the partial weight-gradient
-    rows); shapes beyond that scratch raise."""
+    nothing (a slot of the library's fixed scratch, owned by the current
+    stream, holds the partial weight-gradient rows); shapes beyond a slot, and
+    a fifth calling stream on one GPU, raise."""
     require_device(hidden, weight, grad_hidden, grad_normed, grad_x, grad_weight)
     rows, cols = hidden.shape
     ld_gh = _rows_view(grad_hidden, "grad_hidden") if grad_hidden is not None else cols

@@ -117,7 +117,7 @@ int ak_fused_add_rmsnorm_bwd(const void* hidden, const void* weight,
 
 /*
  * ak_fused_add_rmsnorm_bwd without a workspace: the same kernels and results
- * (bitwise), with the partial weight-gradient rows in a fixed 16 MiB device
+ * (bitwise), with the partial weight-gradient rows in a fixed 64 MiB device
  * array inside the library (one per GPU, held until the process ends) instead
  * of a caller buffer. No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
@@ -127,9 +127,16 @@ int ak_fused_add_rmsnorm_bwd(const void* hidden, const void* weight,
  * (at most 256 workgroup slots, 1024 for rows of <= 512 bf16 / fp16 elements)
  * times cols x 4 bytes exceed 16 MiB -- cols > 16384 for a full grid -- are
  * rejected with AK_ERR_WORKSPACE; use ak_fused_add_rmsnorm_bwd for those. The
- * array is shared by every call on a GPU and keeps the last call's contents:
- * calls that overlap on one GPU (different streams, or host threads) race.
- * The first call on each device looks up the array's address on it.
+ * array holds four 16 MiB slots per GPU; each stream that calls this on a
+ * device gets a slot of its own on its first call (for the life of the
+ * process), so calls queued on different streams -- a captured graph
+ * replayed beside eager calls, say -- never share partial rows, and calls on
+ * one stream are ordered by it. A fifth stream on one device is refused with
+ * AK_ERR_UNSUPPORTED. A slot keeps its last call's contents. A graph captured
+ * on one stream and replayed on another keeps the capture stream's slot, so it
+ * must not overlap eager calls on the capture stream. The per-thread default
+ * stream counts as one stream. The first call on each device looks up the
+ * array's address on it.
  */
 int ak_fused_add_rmsnorm_bwd_noalloc(const void* hidden, const void* weight,
                                      const void* grad_hidden, const void* grad_normed,

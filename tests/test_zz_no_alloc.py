@@ -76,3 +76,30 @@ def test_no_alloc_rejects_shapes_beyond_the_scratch():
     ref = torch.empty_like(h)
     _lib.fused_add_rmsnorm_bwd(h, w, None, gn, ref, None, None, 1e-6)
     assert torch.equal(gx, ref)
+
+
+def test_no_alloc_two_streams_queued_together():
+    """Calls queued on two streams without waiting for each other (their
+    kernels may run at the same time): each stream owns its own slot of the
+    fixed scratch, so both results equal the workspace entry point's bit for
+    bit. Repeated with the streams' roles swapped and with a second round of
+    calls, so each slot's leftover contents are reused."""
+    need_gpu()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    shapes = [(6000, 4096, 11), (3000, 4096, 12)]
+    cases = []
+    for rows, cols, seed in shapes:
+        h, w, gh, gn = _inputs(rows, cols, torch.bfloat16, seed)
+        cases.append(((h, w, gh, gn), _with_workspace(h, w, gh, gn, 1e-5)))
+    torch.cuda.synchronize()
+    for rnd in range(2):
+        say("no-alloc two streams, round", rnd)
+        outs = []
+        order = [0, 1] if rnd == 0 else [1, 0]
+        for si, ci in zip(order, [0, 1]):
+            with torch.cuda.stream(streams[si]):
+                outs.append(_no_alloc(*cases[ci][0], 1e-5))
+        torch.cuda.synchronize()
+        for (got_x, got_w), (_, (ref_x, ref_w)) in zip(outs, cases):
+            assert torch.equal(got_x, ref_x)
+            assert torch.equal(got_w, ref_w)
