@@ -120,7 +120,11 @@ mamba_scan_bwd_fast_kernel(ScanParams p) {
     uint32_t ck;
   };
   auto load_blk = [&](int t, int blk, Blk& r) {
-    const uint32_t l = (uint32_t)(t * kScanT + 16 * blk);
+    // wave-uniform, and pinned to an SGPR: for block 0 the compiler shares
+    // max(t - 1, 0) with the divergent B / C staging branch, and as a VGPR
+    // value the scalar offsets below became one waterfall loop per load
+    // (about 1.7% of the pass at the C5 shape)
+    const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane(t * kScanT + 16 * blk);
     r.dr = bload1<TD>(rs_d, vo_d1, l * sizeof(TD));
     r.ur = bload1<TU>(rs_u, vo_u1, l * sizeof(TU));
     r.gr = bload1<TU>(rs_go, vo_g1, l * sizeof(TU));
