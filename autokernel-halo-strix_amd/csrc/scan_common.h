@@ -157,6 +157,29 @@ inline ScanBwdWs scan_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t
   return w;
 }
 
+// Complex-A scan (selective_scan_complex.hip). Workspace of its backward,
+// each region 256-byte aligned: the complex states every 16 steps and the
+// pre-gate output (used when the caller gives no saved states), the
+// per-4-channel-tile partial rows of a variable dB / dC, the per-batch
+// partials of dA / dD / ddelta_bias and of a constant dB / dC.
+struct ZWs {
+  size_t ck, prez, partB, partC, dA, dD, dBc, dCc, total;
+};
+ZWs scan_complex_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t dstate, int64_t ngroups,
+                        int bc_flags);
+// The forward writes out / out_prez / last_state / chunk_states / checkpoints
+// (complex where the real forward writes fp32). The backward restarts from
+// p.ck / p.out_prez when saved, else re-runs the forward into the workspace,
+// and writes every gradient. Both return nonzero for unsupported dtypes.
+int launch_scan_complex_fwd(ScanParams p, int u_dtype, int delta_dtype, int bc_dtype, hipStream_t s);
+int launch_scan_complex_bwd(ScanParams p, const ZWs& ws, void* workspace, bool saved, int u_dtype,
+                            int delta_dtype, int bc_dtype, void* dB, void* dC, float* dA, float* dD,
+                            float* ddelta_bias, hipStream_t s);
+// Zero-step complex backward: dA, dD, ddelta_bias and a constant dB / dC are
+// sums over nothing.
+void launch_scan_complex_zero(int dim, int dstate, float* dA, float* dD, float* ddelta_bias,
+                              float* dBc, float* dCc, hipStream_t s);
+
 // Whether the general kernels (selective_scan_wide.hip) take the call:
 // more than 16 states, or an input-independent B or C.
 inline bool scan_needs_wide(const ScanParams& p) {

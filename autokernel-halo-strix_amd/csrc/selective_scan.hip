@@ -1313,11 +1313,8 @@ int scan_common_args(const char* name, ScanParams& p, int64_t batch, int64_t dim
                      int bc_dtype, int a_dtype, int* bc_dtype_eff) {
   if (batch < 0 || dim <= 0 || seqlen < 0 || dstate <= 0 || ngroups <= 0)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: bad shape", name);
-  if (a_dtype == AK_DTYPE_C64)
-    return ak_set_error(AK_ERR_UNSUPPORTED,
-                        "%s: complex A (complex64 weights) is not supported; A must be real fp32",
-                        name);
-  if (a_dtype != AK_DTYPE_F32) return ak_set_error(AK_ERR_UNSUPPORTED, "%s: A must be fp32", name);
+  if (a_dtype != AK_DTYPE_F32 && a_dtype != AK_DTYPE_C64)
+    return ak_set_error(AK_ERR_UNSUPPORTED, "%s: A must be fp32 or complex64", name);
   if (dstate > 256)
     return ak_set_error(AK_ERR_UNSUPPORTED, "%s: dstate=%lld > 256 is not supported", name,
                         (long long)dstate);
@@ -1386,6 +1383,11 @@ extern "C" int ak_selective_scan_fwd(
   p.z_bs = z_batch_stride; p.z_ds = z_dim_stride; p.o_bs = out_batch_stride; p.o_ds = out_dim_stride;
   p.softplus = delta_softplus ? 1 : 0;
   hipStream_t s = ak_stream(stream);
+  if (a_dtype == AK_DTYPE_C64) {
+    if (ak::launch_scan_complex_fwd(p, u_dtype, delta_dtype, bc_eff, s))
+      return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and a variable B/C must be fp32 or the dtype of u", name);
+    return ak_check_launch(name);
+  }
   bool rows = false;  // dstate in (16, 64]: the specialised kernel with 2 / 4 rows per channel
   if (p.dstate > 16 && p.dstate <= 64) {
     switch (u_dtype) {
@@ -1465,6 +1467,8 @@ extern "C" size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t d
                                                        int64_t dstate, int64_t ngroups,
                                                        int bc_flags) {
   if (batch <= 0 || dim <= 0 || seqlen <= 0 || dstate <= 0 || ngroups <= 0 || dim % ngroups) return 0;
+  if (bc_flags & AK_SCAN_A_COMPLEX)
+    return ak::scan_complex_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags).total;
   return ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags).total;
 }
 
@@ -1491,11 +1495,18 @@ extern "C" int ak_selective_scan_bwd(
   if (D && !dD) return ak_set_error(AK_ERR_INVALID_ARG, "%s: D given without dD", name);
   if (delta_bias && !ddelta_bias) return ak_set_error(AK_ERR_INVALID_ARG, "%s: delta_bias given without ddelta_bias", name);
   hipStream_t s = ak_stream(stream);
+  const bool cplx = a_dtype == AK_DTYPE_C64;
   if (batch == 0 || seqlen == 0) {
     // no steps: dA, dD, ddelta_bias and a constant dB / dC are sums over
     // nothing; a variable dB / dC, du, ... are empty
     if (p.b_const && !dB) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dB", name);
     if (p.c_const && !dC) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null dC", name);
+    if (cplx) {
+      ak::launch_scan_complex_zero((int)dim, (int)dstate, dA, dD, ddelta_bias,
+                                   p.b_const ? static_cast<float*>(dB) : nullptr,
+                                   p.c_const ? static_cast<float*>(dC) : nullptr, s);
+      return ak_check_launch(name);
+    }
     const ak::FinArgs<float> fa{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                 nullptr, dA, p.b_const ? static_cast<float*>(dB) : nullptr,
                                 p.c_const ? static_cast<float*>(dC) : nullptr, dD, ddelta_bias, 0,
@@ -1508,9 +1519,11 @@ extern "C" int ak_selective_scan_bwd(
   if (checkpoints && z && !out_prez)
     return ak_set_error(AK_ERR_INVALID_ARG, "%s: checkpoints with a gate z need out_prez", name);
   const ak::ScanBwdWs ws = ak::scan_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags);
-  if (!workspace || workspace_bytes < ws.total)
+  const ak::ZWs zws = ak::scan_complex_bwd_ws(batch, dim, seqlen, dstate, ngroups, bc_flags);
+  const size_t need = cplx ? zws.total : ws.total;
+  if (!workspace || workspace_bytes < need)
     return ak_set_error(AK_ERR_WORKSPACE, "%s: workspace %zu bytes < required %zu", name,
-                        workspace_bytes, ws.total);
+                        workspace_bytes, need);
   p.u = u; p.delta = delta; p.A = A; p.B = B; p.C = C; p.D = D; p.z = z;
   p.delta_bias = delta_bias; p.out = nullptr; p.last_state = nullptr;
   p.u_bs = u_batch_stride; p.u_ds = u_dim_stride; p.d_bs = delta_batch_stride; p.d_ds = delta_dim_stride;
@@ -1522,6 +1535,14 @@ extern "C" int ak_selective_scan_bwd(
   p.go_bs = dout_batch_stride; p.go_ds = dout_dim_stride;
   p.softplus = delta_softplus ? 1 : 0;
   p.dout = dout; p.dz = dz; p.du = du; p.ddelta = ddelta;
+  if (cplx) {
+    p.ck = const_cast<float*>(checkpoints);
+    p.out_prez = const_cast<void*>(out_prez);
+    if (ak::launch_scan_complex_bwd(p, zws, workspace, checkpoints != nullptr, u_dtype, delta_dtype,
+                                    bc_eff, dB, dC, dA, dD, ddelta_bias, s))
+      return ak_set_error(AK_ERR_UNSUPPORTED, "%s: delta and a variable B/C must be fp32 or the dtype of u", name);
+    return ak_check_launch(name);
+  }
   char* w = static_cast<char*>(workspace);
   size_t off = 0;
   auto take = [&](size_t bytes) { float* q = bytes ? reinterpret_cast<float*>(w + off) : nullptr; off += bytes; return q; };

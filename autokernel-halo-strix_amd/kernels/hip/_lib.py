@@ -32,7 +32,7 @@ CSRC_DIR = os.path.normpath(os.path.join(os.path.dirname(os.path.abspath(__file_
 
 AK_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 FLOAT_DTYPES = tuple(AK_DTYPE)
-# complex64: named only so that the selective scan's C-ABI can reject a complex A
+# complex64 (interleaved fp32 re, im): the selective scan's complex A
 AK_DTYPE_C64 = 3
 
 _c_void_p = ctypes.c_void_p
@@ -538,6 +538,7 @@ def lmhead_grad_weight(grad_logits: torch.Tensor, hidden: torch.Tensor, out: tor
 # bc_flags of the selective-scan entry points: B / C input-independent ([dim, dstate] fp32)
 SCAN_B_CONST = 1
 SCAN_C_CONST = 2
+SCAN_A_COMPLEX = 4  # workspace query only
 
 
 def _scan_bc(B: torch.Tensor, C: torch.Tensor):
@@ -570,7 +571,9 @@ def selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_s
     """Mamba-1 forward. u/delta/z/out [b, d, l]; B/C [b, g, n, l] or input-independent
     [d, n] fp32; A [d, n] fp32; optional out_prez (pre-gate output, strides of out),
     chunk_states [b, d, ceil(l/2048), n, 2] and checkpoints [b, ceil(l/16), d, n]
-    (the states the backward restarts from)."""
+    (the states the backward restarts from). With a complex64 A: a variable B/C is
+    real [b, g, n, 2l] of (re, im) pairs, a constant one complex64 [d, n], and
+    last_state / chunk_states / checkpoints are complex64."""
     require_device(u, delta, A, B, C, D, z, delta_bias, out, last_state, out_prez, chunk_states,
                    checkpoints)
     if out_prez is not None and out_prez.stride() != out.stride():
@@ -598,7 +601,8 @@ def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA
     contiguous [b, d, l], dB/dC contiguous in B's / C's layout (a variable one in
     its dtype, an input-independent one fp32), dA [d, n] / dD [d] / ddelta_bias [d]
     fp32. With the forward's ``checkpoints`` (and, with z, its contiguous
-    ``out_prez``) the states are not recomputed."""
+    ``out_prez``) the states are not recomputed. With a complex64 A, dA and an
+    input-independent dB / dC are complex64 (layouts as in :func:`selective_scan`)."""
     require_device(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz,
                    ddelta_bias, checkpoints, out_prez)
     if out_prez is not None and not out_prez.is_contiguous():
@@ -608,8 +612,9 @@ def selective_scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA
     flags, bs, cs, ngroups, bc_dtype = _scan_bc(B, C)
     zs = (z.stride(0), z.stride(1)) if z is not None else (0, 0)
     lib = load()
+    wflags = flags | (SCAN_A_COMPLEX if A.is_complex() else 0)
     ws = torch.empty(int(lib.ak_selective_scan_bwd_workspace_bytes(batch, dim, seqlen, dstate,
-                                                                   ngroups, flags)),
+                                                                   ngroups, wflags)),
                      dtype=torch.uint8, device=u.device)
     with _on_device(u):
         rc = lib.ak_selective_scan_bwd(

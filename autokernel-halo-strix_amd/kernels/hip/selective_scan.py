@@ -26,8 +26,13 @@ Two entry points, both drop-ins:
   ``!is_variable_B`` path, ``selective_scan_interface.py:138-160``).
   ``delta`` may be fp32 or ``u``'s dtype. dstate <= 16 with input-dependent
   B / C runs the specialised kernels; everything else the general ones.
-  Complex ``A`` raises ``NotImplementedError`` (the C-ABI rejects complex
-  weights). The backward (``ak_selective_scan_bwd``) returns every input
+  Complex ``A`` (complex64 ``[dim, dstate]``, the reference binding's
+  complex weights, ``selective_scan.cpp:236-240``) runs the complex kernels:
+  an input-dependent ``B`` / ``C`` is then real ``[batch, (ngroups,) dstate,
+  2 * seqlen]`` of (re, im) pairs per step, an input-independent one complex
+  ``[dim, dstate]``; the state, ``last_state`` and ``dA`` are complex and
+  ``out`` is ``2 Re(sum_n h C) + D u`` (``selective_scan_interface.py:
+  140-145, :173-174``). The backward (``ak_selective_scan_bwd``) returns every input
   gradient of the reference's ``selective_scan_cuda.bwd``: ``du``,
   ``ddelta``, ``dA``, ``dB``, ``dC``, ``dD``, ``dz``, ``ddelta_bias``, each
   computed deterministically (fixed summation order); an input-dependent
@@ -81,7 +86,8 @@ def set_save_states(enabled: bool, max_bytes=None) -> None:
 
 def _checkpoint_bytes(u: torch.Tensor, A: torch.Tensor) -> int:
     batch, dim, seqlen = u.shape
-    return 4 * batch * dim * A.shape[1] * ((seqlen + CHECKPOINT_STEPS - 1) // CHECKPOINT_STEPS)
+    per = 8 if A.is_complex() else 4
+    return per * batch * dim * A.shape[1] * ((seqlen + CHECKPOINT_STEPS - 1) // CHECKPOINT_STEPS)
 
 
 def kernel_fn(dA: torch.Tensor, dBx: torch.Tensor, C: torch.Tensor, D: torch.Tensor,
@@ -112,10 +118,6 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
     ``[dim, dstate]`` fp32, A / D / delta_bias fp32, z in u's dtype, delta in
     fp32 or u's dtype."""
     _lib.require_device(u, delta, A, B, C, D, z, delta_bias)
-    if A.is_complex():
-        raise NotImplementedError(
-            "complex A is not supported by the gfx950 selective scan (real fp32 A only; "
-            "the C-ABI rejects complex weights)")
     if u.dim() != 3:
         raise ValueError("u must be [batch, dim, seqlen]")
     batch, dim, seqlen = u.shape
@@ -128,8 +130,11 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
     if A.dim() != 2 or A.shape[0] != dim:
         raise ValueError("A must be [dim, dstate]")
     dstate = A.shape[1]
+    cplx = A.is_complex()
 
     def bc(t, name):
+        if cplx:
+            return _bc_complex(t, name)
         if t.dim() == 2:  # input-independent
             if tuple(t.shape) != (dim, dstate):
                 raise ValueError(f"input-independent {name} must be [dim, dstate], got {tuple(t.shape)}")
@@ -144,13 +149,33 @@ def _normalise(u, delta, A, B, C, D, z, delta_bias):
             t = t.float()
         return t if t.stride(-1) == 1 else t.contiguous()
 
+    def _bc_complex(t, name):
+        """Complex A: input-independent complex [dim, dstate], or input-dependent
+        real [batch, (ngroups,) dstate, 2 seqlen] of (re, im) pairs."""
+        if t.dim() == 2:
+            if tuple(t.shape) != (dim, dstate):
+                raise ValueError(f"input-independent {name} must be [dim, dstate], got {tuple(t.shape)}")
+            return t.to(torch.complex64)
+        if t.is_complex():
+            raise ValueError(f"with a complex A an input-dependent {name} is real "
+                             f"[batch, ngroups, dstate, 2 * seqlen] of (re, im) pairs")
+        if t.dim() == 3:
+            t = t.unsqueeze(1)
+        if t.dim() != 4 or t.shape[0] != batch or t.shape[2] != dstate \
+                or t.shape[3] != 2 * seqlen or dim % t.shape[1]:
+            raise ValueError(f"{name} must be [batch, ngroups, dstate, 2 * seqlen] or [dim, dstate] "
+                             f"with a complex A, got {tuple(t.shape)}")
+        if t.dtype not in (torch.float32, u.dtype):
+            t = t.float()
+        return t if t.stride(-1) == 1 else t.contiguous()
+
     B, C = bc(B, "B"), bc(C, "C")
     if B.dim() == 4 and C.dim() == 4:
         if C.shape != B.shape:
             raise ValueError(f"B / C must have one shape, got {tuple(B.shape)}, {tuple(C.shape)}")
         if C.dtype != B.dtype:
             C = C.to(B.dtype)
-    A = A.float()
+    A = A.to(torch.complex64) if cplx else A.float()
     if A.stride(1) != 1:
         A = A.contiguous()
     if D is not None:
@@ -178,14 +203,15 @@ def _scan_forward(u, delta, A, B, C, D, z, delta_bias, delta_softplus, want_last
     u, delta, A, B, C, D, z, delta_bias = _normalise(u, delta, A, B, C, D, z, delta_bias)
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
+    sdt = torch.complex64 if A.is_complex() else torch.float32  # state type
     out = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=u.device)
-    last_state = (torch.empty((batch, dim, dstate), dtype=torch.float32, device=u.device)
+    last_state = (torch.empty((batch, dim, dstate), dtype=sdt, device=u.device)
                   if want_last_state else None)
     prez = torch.empty_like(out) if want_prez or (want_checkpoints and z is not None) else None
-    chunks = (torch.empty((batch, dim, (seqlen + CHUNK - 1) // CHUNK, dstate, 2), dtype=torch.float32,
+    chunks = (torch.empty((batch, dim, (seqlen + CHUNK - 1) // CHUNK, dstate, 2), dtype=sdt,
                           device=u.device) if want_chunk_states else None)
     ckpt = (torch.empty((batch, (seqlen + CHECKPOINT_STEPS - 1) // CHECKPOINT_STEPS, dim, dstate),
-                        dtype=torch.float32, device=u.device) if want_checkpoints else None)
+                        dtype=sdt, device=u.device) if want_checkpoints else None)
     _lib.selective_scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus,
                         out_prez=prez, chunk_states=chunks, checkpoints=ckpt)
     saved = (u, delta, A, B, C, D, z, delta_bias)
@@ -210,7 +236,7 @@ def _scan_backward(dout, u, delta, A, B, C, D, z, delta_bias, delta_softplus, ch
     dev = u.device
     du = torch.empty((batch, dim, seqlen), dtype=u.dtype, device=dev)
     ddelta = torch.empty((batch, dim, seqlen), dtype=delta.dtype, device=dev)
-    dA = torch.empty(A.shape, dtype=torch.float32, device=dev)
+    dA = torch.empty(A.shape, dtype=A.dtype, device=dev)
     dB = torch.empty(B.shape, dtype=B.dtype, device=dev)
     dC = torch.empty(C.shape, dtype=C.dtype, device=dev)
     dD = torch.empty(dim, dtype=torch.float32, device=dev) if D is not None else None

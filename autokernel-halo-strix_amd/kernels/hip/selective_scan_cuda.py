@@ -15,12 +15,15 @@ The binding's contract is kept: ``dstate <= 256``
 dstate, seqlen]`` or ``[batch, ngroups, dstate, seqlen]``) or
 input-independent ones (``[dim, dstate]`` fp32, ``:115-121``), and the
 gradients of input-dependent ``B`` / ``C`` summed in fp32 and returned in
-their dtype (``:461``, ``:488``; an input-independent one is fp32).
+their dtype (``:461``, ``:488``; an input-independent one is fp32). Complex
+weights (``A`` complex64, ``:236-240``) take input-dependent ``B`` / ``C`` as
+real ``[batch, (ngroups,) dstate, 2 * seqlen]`` (``:270-276``) or
+input-independent complex ones; ``x``, ``dA`` and a constant ``dB`` / ``dC``
+are then complex64.
 
 Differences, by design: the backward recomputes the states itself, so the
 chunk-state tensor ``x`` and the forward output ``out`` passed to ``bwd`` are
-accepted and not read; ``delta`` may be fp32 with half-precision ``u``;
-complex ``A`` raises ``NotImplementedError`` (real weights only).
+accepted and not read; ``delta`` may be fp32 with half-precision ``u``.
 """
 
 from kernels.hip.selective_scan import _normalise, _scan_backward, _scan_forward
@@ -29,9 +32,10 @@ from kernels.hip.selective_scan import _normalise, _scan_backward, _scan_forward
 def fwd(u, delta, A, B, C, D_=None, z_=None, delta_bias_=None, delta_softplus=False):
     """``[out, x]``, or ``[out, x, out_z]`` with a gate ``z``.
 
-    ``out``: y + D u in u's dtype (before the gate); ``x``: fp32
-    ``[batch, dim, n_chunks, 2 * dstate]``, per 2048-step chunk the running
-    prefix (prod exp(delta' A), state) of each state, interleaved;
+    ``out``: y + D u in u's dtype (before the gate); ``x``: fp32 (complex64
+    with a complex ``A``) ``[batch, dim, n_chunks, 2 * dstate]``, per
+    2048-step chunk the running prefix (prod exp(delta' A), state) of each
+    state, interleaved;
     ``out_z``: ``out * silu(z)``.
     """
     gated = z_ is not None

@@ -33,12 +33,15 @@ extern "C" {
 #define AK_DTYPE_F32 0
 #define AK_DTYPE_F16 1
 #define AK_DTYPE_BF16 2
-/* complex64; only named so that the selective scan can reject a complex A */
+/* complex64 (interleaved fp32 re, im): the selective scan's complex A */
 #define AK_DTYPE_C64 3
 
-/* Selective-scan bc_flags: B / C input-independent, [dim, dstate] fp32 */
+/* Selective-scan bc_flags: B / C input-independent, [dim, dstate] fp32
+ * (complex64 with a complex A) */
 #define AK_SCAN_B_CONST 1
 #define AK_SCAN_C_CONST 2
+/* ak_selective_scan_bwd_workspace_bytes only: the size for a complex A */
+#define AK_SCAN_A_COMPLEX 4
 
 #define AK_OK 0
 #define AK_ERR_INVALID_ARG (-1)
@@ -339,9 +342,12 @@ int ak_lmhead_grad_weight(const void* grad_logits, int64_t ld_gl, const void* hi
  * state.
  *   u, z, out : [batch, dim, seqlen], element type u_dtype, last dim contiguous
  *   delta     : [batch, dim, seqlen], element type delta_dtype
- *   A         : [dim, dstate] fp32 (real): a_dtype must be AK_DTYPE_F32;
- *               AK_DTYPE_C64 (the reference's complex weights,
- *               selective_scan_interface.py:140-145) returns AK_ERR_UNSUPPORTED
+ *   A         : [dim, dstate], a_dtype AK_DTYPE_F32 (real) or AK_DTYPE_C64
+ *               (the reference's complex weights, selective_scan.cpp:236-240,
+ *               selective_scan_interface.py:140-145, :173-174: complex state,
+ *               y = 2 Re sum_n h C + D u); with C64 the state stride is 1 and
+ *               A_dim_stride counts complex elements, and everything below
+ *               marked "complex" applies (see the complex notes at the end)
  *   B, C      : variable: [batch, ngroups, dstate, seqlen], element type
  *               bc_dtype (strides batch / group / state);
  *               with AK_SCAN_B_CONST / AK_SCAN_C_CONST in bc_flags:
@@ -365,6 +371,13 @@ int ak_lmhead_grad_weight(const void* grad_logits, int64_t ld_gl, const void* hi
  * (the reference binding's limit, selective_scan.cpp:262). dstate <= 16 with
  * variable B / C runs the specialised kernels, everything else the general
  * ones.
+ * Complex A (AK_DTYPE_C64; complex64 = interleaved fp32 re, im): a variable
+ * B / C is real [batch, ngroups, dstate, 2 seqlen] in bc_dtype with the
+ * (re, im) pair of step l at 2 l, 2 l + 1 (selective_scan.cpp:270-276); a
+ * constant one is complex64 [dim, dstate] (strides in complex elements);
+ * last_state is complex64 [batch, dim, dstate], chunk_states complex64
+ * [batch, dim, ceil(seqlen / 2048), dstate, 2], checkpoints complex64
+ * [batch, ceil(seqlen / 16), dim, dstate].
  */
 int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
                           const void* B, const void* C, const float* D,
@@ -413,6 +426,15 @@ int ak_selective_scan_fwd(const void* u, const void* delta, const float* A,
  * whole-tile shapes, with batch x ngroups x channels-per-group / 32 >= 256,
  * group 32 channels per partial dB / dC row, a choice fixed by the shape
  * alone, so the bits do not depend on the device's compute-unit count).
+ * Complex A: dA is complex64 [dim, dstate]; a variable dB / dC is real
+ * [batch, ngroups, dstate, 2 seqlen] in bc_dtype, a constant one complex64
+ * [dim, dstate]; checkpoints are the forward's complex ones; complex
+ * gradients are packed as dL/dRe + i dL/dIm (torch autograd's convention).
+ * The workspace size is ak_selective_scan_bwd_workspace_bytes(..., bc_flags |
+ * AK_SCAN_A_COMPLEX); without saved states it holds the re-run forward's
+ * states and pre-gate output, and a variable dB / dC takes one fp32 partial
+ * row per 4 channels of a group (4 * 2 seqlen * dstate * ngroups * batch *
+ * dim / ngroups / 4 bytes each).
  */
 size_t ak_selective_scan_bwd_workspace_bytes(int64_t batch, int64_t dim, int64_t seqlen,
                                              int64_t dstate, int64_t ngroups, int bc_flags);

@@ -388,6 +388,165 @@ def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=N
     return du, ddelta, dA, dB, dC, dD, dz, dbias
 
 
+def _bc_complex(t: torch.Tensor, batch: int, dim: int, seqlen: int) -> torch.Tensor:
+    """B or C of a complex-A scan as complex128 ``[batch, dim, dstate, seqlen]``.
+
+    An input-dependent one is a real ``[b, n, 2l]`` or ``[b, g, n, 2l]`` tensor
+    whose last dimension holds (re, im) pairs per step, read with
+    ``view_as_complex`` (``selective_scan_interface.py:140-145``) and repeated
+    over each group's channels; an input-independent one is complex
+    ``[dim, n]``, repeated over batch and steps."""
+    if t.is_complex():
+        return t.to(torch.complex128)[None, :, :, None].expand(batch, dim, t.shape[1], seqlen)
+    t = t.to(torch.float64)
+    if t.dim() == 3:
+        t = t.unsqueeze(1)
+    tc = torch.view_as_complex(t.reshape(*t.shape[:-1], seqlen, 2).contiguous())
+    return tc.repeat_interleave(dim // tc.shape[1], dim=1)
+
+
+def _dl64(delta, delta_bias, delta_softplus):
+    f = torch.float64
+    draw = delta.to(f) + (delta_bias.to(f)[..., None] if delta_bias is not None else 0.0)
+    return draw, (F.softplus(draw) if delta_softplus else draw)
+
+
+def selective_scan_complex_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                               delta_softplus=False, return_last_state=False):
+    """``external/mamba/mamba_ssm/ops/selective_scan_interface.py:115-181`` with
+    complex ``A`` (``:140-145``, ``:173-174``), in complex128 / float64.
+
+    The state is complex; each step's output is twice the real part of
+    sum_n h_n C_n (``y.real * 2``), then ``+ D u`` and the gate ``silu(z)``.
+    Returns float64 ``out`` (and the complex128 last state)."""
+    f, c = torch.float64, torch.complex128
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    u64 = u.to(f)
+    _, dl = _dl64(delta, delta_bias, delta_softplus)
+    Bd = _bc_complex(B, batch, dim, seqlen)
+    Cd = _bc_complex(C, batch, dim, seqlen)
+    A128 = A.to(c)
+    x = torch.zeros(batch, dim, dstate, dtype=c)
+    ys = []
+    for l in range(seqlen):
+        a = torch.exp(dl[:, :, l, None] * A128[None])
+        x = a * x + (dl[:, :, l] * u64[:, :, l])[..., None] * Bd[..., l]
+        ys.append(2.0 * (x * Cd[..., l]).sum(-1).real)
+    y = torch.stack(ys, dim=2) if seqlen else torch.zeros(batch, dim, 0, dtype=f)
+    out = y if D is None else y + u64 * D.to(f)[:, None]
+    if z is not None:
+        out = out * F.silu(z.to(f))
+    return (out, x) if return_last_state else out
+
+
+def selective_scan_complex_chunk_states_ref(u, delta, A, B, delta_bias=None, delta_softplus=False,
+                                            chunk: int = 2048):
+    """The chunk-state output ``x`` of the reference's forward binding for
+    complex ``A`` (``selective_scan.cpp:307-313``: ``[batch, dim, n_chunks,
+    2 * dstate]`` complex): per 2048-step chunk, the running prefix from step
+    0 to the chunk's last step, (prod_s exp(delta'_s A), h) per state.
+    complex128 ``[batch, dim, n_chunks, dstate, 2]``."""
+    f, c = torch.float64, torch.complex128
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    _, dl = _dl64(delta, delta_bias, delta_softplus)
+    Bd = _bc_complex(B, batch, dim, seqlen)
+    nch = (seqlen + chunk - 1) // chunk
+    out = torch.empty(batch, dim, nch, dstate, 2, dtype=c)
+    prod = torch.ones(batch, dim, dstate, dtype=c)
+    h = torch.zeros(batch, dim, dstate, dtype=c)
+    for l in range(seqlen):
+        a = torch.exp(dl[:, :, l, None] * A.to(c)[None])
+        prod = prod * a
+        h = a * h + (dl[:, :, l] * u[:, :, l].to(f))[..., None] * Bd[..., l]
+        if (l + 1) % chunk == 0 or l + 1 == seqlen:
+            out[:, :, l // chunk, :, 0] = prod
+            out[:, :, l // chunk, :, 1] = h
+    return out
+
+
+def selective_scan_complex_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None,
+                                   delta_softplus=False):
+    """Gradients of :func:`selective_scan_complex_ref` by the reverse
+    recurrence in complex128. A complex input's gradient is packed as
+    dL/dRe + i dL/dIm (the convention of torch autograd, which the reference's
+    tests compare the binding's complex ``dA`` with); for a complex z' = w z
+    the packed gradient of z is conj(w) times that of z'. With a_l =
+    exp(delta'_l A), h_l = a_l h_{l-1} + delta'_l u_l B_l and
+    y_l = 2 Re sum_n h_l C_l:
+
+        g_l       = conj(a_{l+1}) g_{l+1} + 2 dy_l conj(C_l)
+        du_l      = D dy_l + sum_n Re(conj(g_l) delta'_l B_l)
+        ddelta'_l = sum_n Re(conj(g_l) u_l B_l) + Re(conj(g_l conj(h_{l-1})) A a_l)
+        dA       += delta'_l conj(a_l) g_l conj(h_{l-1})
+        dB_l      = delta'_l u_l g_l;   dC_l = 2 dy_l conj(h_l)
+
+    Returns ``(du, ddelta, dA, dB, dC, dD, dz, ddelta_bias)``: float64 except
+    dA (complex128) and an input-independent dB / dC (complex128 ``[dim, n]``);
+    an input-dependent dB / dC is float64 in B's / C's real interleaved layout.
+    """
+    f, c = torch.float64, torch.complex128
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    u64, dout64 = u.to(f), dout.to(f)
+    draw, dl = _dl64(delta, delta_bias, delta_softplus)
+    A128 = A.to(c)
+    Bd = _bc_complex(B, batch, dim, seqlen)
+    Cd = _bc_complex(C, batch, dim, seqlen)
+    a = torch.exp(dl[:, :, None, :] * A128[None, :, :, None])  # [b, d, n, l]
+    bx = (dl * u64)[:, :, None, :] * Bd
+    h = torch.empty(batch, dim, dstate, seqlen, dtype=c)
+    s = torch.zeros(batch, dim, dstate, dtype=c)
+    for l in range(seqlen):
+        s = a[..., l] * s + bx[..., l]
+        h[..., l] = s
+    y = 2.0 * (h * Cd).sum(2).real
+    if D is not None:
+        y = y + u64 * D.to(f)[:, None]
+    if z is not None:
+        z64 = z.to(f)
+        sg = torch.sigmoid(z64)
+        dz = dout64 * y * sg * (1 + z64 * (1 - sg))
+        dy = dout64 * z64 * sg
+    else:
+        dz, dy = None, dout64
+    g = torch.zeros(batch, dim, dstate, dtype=c)
+    gh = torch.empty_like(h)
+    for l in range(seqlen - 1, -1, -1):
+        if l + 1 < seqlen:
+            g = g * a[..., l + 1].conj()
+        g = g + 2.0 * dy[:, :, None, l] * Cd[..., l].conj()
+        gh[..., l] = g
+    hprev = torch.cat([torch.zeros_like(h[..., :1]), h[..., :-1]], dim=-1)
+    ga = gh * hprev.conj()                                   # packed gradient of a_l
+    du = (gh.conj() * dl[:, :, None] * Bd).real.sum(2)
+    if D is not None:
+        du = du + dy * D.to(f)[:, None]
+    ddl = ((gh.conj() * u64[:, :, None] * Bd).real
+           + (ga.conj() * A128[None, :, :, None] * a).real).sum(2)
+    dA = (dl[:, :, None] * a.conj() * ga).sum((0, 3))
+    dB_d = gh * (dl * u64)[:, :, None]
+    dC_d = 2.0 * dy[:, :, None] * h.conj()
+
+    def fold(g_d, like):
+        if like.is_complex():  # input-independent [dim, n]
+            return g_d.sum((0, 3))
+        ng = 1 if like.dim() == 3 else like.shape[1]
+        out = g_d.reshape(batch, ng, dim // ng, dstate, seqlen).sum(2)
+        out = torch.view_as_real(out).reshape(batch, ng, dstate, 2 * seqlen)
+        return out.squeeze(1) if like.dim() == 3 else out
+
+    dB, dC = fold(dB_d, B), fold(dC_d, C)
+    if delta_softplus:
+        ddelta = torch.where(draw <= 20.0, ddl * torch.sigmoid(draw), ddl)
+    else:
+        ddelta = ddl
+    dD = (dy * u64).sum((0, 2)) if D is not None else None
+    dbias = ddelta.sum((0, 2)) if delta_bias is not None else None
+    return du, ddelta, dA, dB, dC, dD, dz, dbias
+
+
 def diag_scan_ref(dA, dBx, C, D, x):
     """Diagonal recurrence of ``kernels/hip/selective_scan.py:1-20, :214-241``.
 

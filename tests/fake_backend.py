@@ -163,6 +163,21 @@ def _grad_weight(grad_logits, hidden, out, out_mode, workspace):
 
 def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, out_prez=None,
           chunk_states=None, checkpoints=None):
+    if A.is_complex():
+        o, last = ops.selective_scan_complex_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
+                                                 return_last_state=True)
+        out.copy_(o)
+        if last_state is not None:
+            last_state.copy_(last)
+        if out_prez is not None:
+            out_prez.copy_(ops.selective_scan_complex_ref(u, delta, A, B, C, D, None, delta_bias,
+                                                          delta_softplus))
+        if chunk_states is not None:
+            chunk_states.copy_(ops.selective_scan_complex_chunk_states_ref(u, delta, A, B, delta_bias,
+                                                                           delta_softplus))
+        if checkpoints is not None:
+            checkpoints.zero_()
+        return
     o, last = ops.selective_scan_ref(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
                                      return_last_state=True)
     out.copy_(o)
@@ -178,7 +193,8 @@ def _scan(u, delta, A, B, C, D, z, delta_bias, out, last_state, delta_softplus, 
 
 def _scan_bwd(u, delta, A, B, C, D, z, delta_bias, dout, du, ddelta, dA, dB, dC, dD, dz, dbias,
               delta_softplus, checkpoints=None, out_prez=None):
-    outs = ops.selective_scan_bwd_ref(u, delta, A, B, C, dout, D, z, delta_bias, delta_softplus)
+    bwd = ops.selective_scan_complex_bwd_ref if A.is_complex() else ops.selective_scan_bwd_ref
+    outs = bwd(u, delta, A, B, C, dout, D, z, delta_bias, delta_softplus)
     for dst, src in zip((du, ddelta, dA, dB, dC, dD, dz, dbias), outs):
         if dst is not None:
             dst.copy_(src.to(dst.dtype))

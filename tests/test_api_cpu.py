@@ -209,8 +209,26 @@ def test_selective_scan_fn_api(fake_backend):
     for bb, cc in ((B2, C), (B, C2), (B2, C2)):
         out2 = selective_scan_fn(u, delta, A, bb, cc, torch.ones(4))
         assert torch.allclose(out2, ops.selective_scan_ref(u, delta, A, bb, cc, torch.ones(4)))
-    with pytest.raises(NotImplementedError, match="complex"):
-        selective_scan_fn(u, delta, A.to(torch.complex64), B, C)
+    # complex A: B / C real [b, n, 2l] of (re, im) pairs or complex [dim, n]
+    Ac = torch.complex(A, torch.rand(4, 8, generator=g) * 3.0)
+    with pytest.raises(ValueError, match="2 \\* seqlen"):
+        selective_scan_fn(u, delta, Ac, B, C)
+    with pytest.raises(ValueError, match="real"):
+        selective_scan_fn(u, delta, Ac, torch.complex(B, B), C)
+    Bx, Cx = torch.randn(2, 8, 40, generator=g), torch.randn(2, 8, 40, generator=g)
+    Cc = torch.complex(C2, torch.randn(4, 8, generator=g))
+    outc, lastc = selective_scan_fn(u, delta, Ac, Bx, Cc, torch.ones(4), return_last_state=True)
+    refc, rlc = ops.selective_scan_complex_ref(u, delta, Ac, Bx, Cc, torch.ones(4), return_last_state=True)
+    assert torch.allclose(outc, refc.float(), atol=1e-5) and lastc.dtype == torch.complex64
+    assert torch.allclose(lastc, rlc.to(torch.complex64), atol=1e-5)
+    lc = [t.clone().requires_grad_() for t in (Ac, Bx, Cc)]
+    selective_scan_fn(u, delta, lc[0], lc[1], lc[2], torch.ones(4)).sum().backward()
+    assert lc[0].grad.dtype == torch.complex64 and lc[0].grad.shape == (4, 8)
+    assert lc[1].grad.dtype == torch.float32 and lc[1].grad.shape == (2, 8, 40)
+    assert lc[2].grad.dtype == torch.complex64 and lc[2].grad.shape == (4, 8)
+    gref = ops.selective_scan_complex_bwd_ref(u, delta, Ac, Bx, Cc, torch.ones_like(u), torch.ones(4))
+    assert torch.allclose(lc[0].grad, gref[2].to(torch.complex64), rtol=1e-4, atol=1e-5)
+    assert torch.allclose(lc[1].grad, gref[3].float(), rtol=1e-4, atol=1e-5)
     with pytest.raises(ValueError):
         selective_scan_fn(u, delta, A, torch.randn(5, 8), C)
     Bl = B2.clone().requires_grad_()
@@ -267,6 +285,23 @@ def test_selective_scan_cuda_binding_api(fake_backend):
     assert torch.allclose(res[8], out_z)
     res = selective_scan_cuda.bwd(u, delta, A, B, C, None, None, None, dout, x2, out2, None, False, False)
     assert len(res) == 7 and res[5] is None and res[6] is None
+    # complex weights: x complex64 [batch, dim, n_chunks, 2 * dstate]; dA complex,
+    # a variable dB real [batch, dstate, 2 seqlen], a constant dC complex
+    Ac = torch.complex(A, torch.rand(4, 8, generator=g))
+    Bx = torch.randn(2, 8, 40, generator=g)
+    Cc = torch.complex(torch.randn(4, 8, generator=g), torch.randn(4, 8, generator=g))
+    outc, xc, outc_z = selective_scan_cuda.fwd(u, delta, Ac, Bx, Cc, D, z, bias, True)
+    assert xc.shape == (2, 4, 1, 16) and xc.dtype == torch.complex64
+    xsc = ops.selective_scan_complex_chunk_states_ref(u, delta, Ac, Bx, bias, True)
+    assert torch.allclose(xc, xsc.reshape(2, 4, 1, 16).to(torch.complex64), rtol=1e-5, atol=1e-6)
+    assert torch.allclose(outc, ops.selective_scan_complex_ref(u, delta, Ac, Bx, Cc, D, None, bias, True).float(),
+                          rtol=1e-5, atol=1e-5)
+    res = selective_scan_cuda.bwd(u, delta, Ac, Bx, Cc, D, z, bias, dout, xc, outc, None, True, False)
+    refc = ops.selective_scan_complex_bwd_ref(u, delta, Ac, Bx, Cc, dout, D, z, bias, True)
+    assert res[2].dtype == torch.complex64 and res[3].dtype == torch.float32 and res[4].dtype == torch.complex64
+    for got, want in zip(res[:5], refc[:5]):
+        assert got.shape == want.shape
+        assert torch.allclose(got.to(want.dtype), want, rtol=1e-4, atol=1e-5)
 
 
 # ---------------------------------------------------------------------------

@@ -201,9 +201,12 @@ def test_selective_scan_argument_contract(lib):
     assert f(*_scan_fwd_args(dstate=64, bc_flags=3)) == 0  # input-independent B and C
     rc = f(*_scan_fwd_args(dstate=257))
     assert rc == -2 and b"256" in lib.ak_last_error()
-    rc = f(*_scan_fwd_args(a_dtype=3))
-    assert rc == -2 and b"complex" in lib.ak_last_error()
-    rc = f(*_scan_fwd_args(bc_flags=4))
+    assert f(*_scan_fwd_args(a_dtype=3)) == 0              # complex64 A
+    rc = f(*_scan_fwd_args(a_dtype=1))
+    assert rc == -2 and b"complex64" in lib.ak_last_error()
+    rc = f(*_scan_fwd_args(a_dtype=3, batch=2))           # complex, real shape: null pointers
+    assert rc == -1 and b"null" in lib.ak_last_error()
+    rc = f(*_scan_fwd_args(bc_flags=4))                   # AK_SCAN_A_COMPLEX: workspace query only
     assert rc == -1 and b"bc_flags" in lib.ak_last_error()
     rc = f(*_scan_fwd_args(batch=2))                      # real shape: null pointers
     assert rc == -1 and b"null" in lib.ak_last_error()
@@ -213,3 +216,9 @@ def test_selective_scan_argument_contract(lib):
     # and keeps a [batch, dim, dstate] one instead
     tiles = 2048 // 16
     assert var - kb == tiles * 4 * 64 * 4096 * 4 - 4 * 2048 * 64 * 4
+    # complex A: complex states every 16 steps, the pre-gate output (fp32 slots),
+    # per-4-channel partial rows of (re, im) pairs, complex per-batch partials
+    cw = ws(4, 2048, 4096, 64, 1, 4)
+    a256 = lambda v: (v + 255) // 256 * 256
+    assert cw == (a256(4 * 256 * 2048 * 64 * 8) + a256(4 * 2048 * 4096 * 4)
+                  + 2 * a256(512 * 4 * 64 * 2 * 4096 * 4) + a256(4 * 2048 * 64 * 8) + 2 * a256(4 * 2048 * 4))

@@ -571,6 +571,142 @@ def test_selective_scan_chunk_states_pinned():
         assert torch.allclose(xs[:, :, k, :, 0], prod, rtol=1e-12, atol=1e-300)
 
 
+def _complex_scan_inputs(b=2, d=4, l=24, n=6, g=1, seed=51, const_b=False, const_c=False):
+    """Complex-A inputs in the reference's layouts: A complex [d, n] (S4D-like:
+    negative real part, imaginary part pi * k), a variable B / C real
+    [b, g, n, 2l] of (re, im) pairs, a constant one complex [d, n]."""
+    gen = torch.Generator().manual_seed(seed)
+    u = torch.randn(b, d, l, generator=gen)
+    delta = 0.5 * torch.rand(b, d, l, generator=gen)
+    Ar = -0.5 * torch.rand(d, n, generator=gen) - 0.1
+    Ai = math.pi * torch.arange(n, dtype=torch.float32)[None].expand(d, n) * (0.5 + torch.rand(d, n, generator=gen))
+    A = torch.complex(Ar, Ai)
+    bc = lambda const: (torch.complex(torch.randn(d, n, generator=gen), torch.randn(d, n, generator=gen))
+                        if const else torch.randn(b, g, n, 2 * l, generator=gen))
+    B, C = bc(const_b), bc(const_c)
+    D = torch.randn(d, generator=gen)
+    z = torch.randn(b, d, l, generator=gen)
+    bias = 0.5 * torch.rand(d, generator=gen)
+    return u, delta, A, B, C, D, z, bias
+
+
+def test_complex_scan_real_reduction():
+    """With Im A = 0 and real B / C the complex scan is twice the real one
+    (y = 2 Re sum h C, selective_scan_interface.py:173-174), D u added after
+    the doubling."""
+    u, delta, A, B, C, D, z, bias = _complex_scan_inputs(seed=52)
+    Ar = A.real.contiguous()
+    Bre, Cre = B[..., 0::2], C[..., 0::2]
+    Bc = torch.stack([Bre, torch.zeros_like(Bre)], -1).reshape(B.shape)
+    Cc = torch.stack([Cre, torch.zeros_like(Cre)], -1).reshape(C.shape)
+    got = ops.selective_scan_complex_ref(u, delta, Ar.to(torch.complex64), Bc, Cc, D, z, bias, True)
+    y = ops.selective_scan_ref(u, delta, Ar, Bre, Cre, None, None, bias, True,
+                               compute_dtype=torch.float64)
+    want = (2.0 * y + u.double() * D.double()[:, None]) * F.silu(z.double())
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_complex_scan_brute_force_and_phase_invariance():
+    """Brute force on tiny inputs: h_l = sum_{k<=l} exp(A sum_{j=k+1..l}
+    delta'_j) delta'_k u_k B_k (a double sum with exponentials of summed
+    delta, no recurrence), y_l = 2 Re sum_n h_l C_l + D u. And a phase
+    exp(i phi_n) on B with its conjugate on C leaves the output unchanged."""
+    for const_b, const_c in ((False, False), (True, False), (False, True)):
+        u, delta, A, B, C, D, z, bias = _complex_scan_inputs(b=1, d=2, l=6, n=3, seed=53,
+                                                             const_b=const_b, const_c=const_c)
+        got = ops.selective_scan_complex_ref(u, delta, A, B, C, D, None, bias, True)
+        dl = F.softplus(delta.double() + bias.double()[:, None])
+        Bd = ops._bc_complex(B, 1, 2, 6)
+        Cd = ops._bc_complex(C, 1, 2, 6)
+        A128 = A.to(torch.complex128)
+        cs = torch.cumsum(dl, -1)
+        want = torch.empty(1, 2, 6, dtype=torch.float64)
+        for l in range(6):
+            acc = torch.zeros(1, 2, 3, dtype=torch.complex128)
+            for k in range(l + 1):
+                w = torch.exp(A128[None] * (cs[:, :, l] - cs[:, :, k])[..., None])
+                acc = acc + w * (dl[:, :, k] * u[:, :, k].double())[..., None] * Bd[..., k]
+            want[:, :, l] = 2.0 * (acc * Cd[..., l]).sum(-1).real + u[:, :, l].double() * D.double()
+        assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+    u, delta, A, B, C, D, z, bias = _complex_scan_inputs(g=2, seed=54)
+    phi = torch.rand(6, generator=torch.Generator().manual_seed(3)) * 6.0
+    rot = lambda t, s: torch.view_as_real(
+        torch.view_as_complex(t.reshape(*t.shape[:-1], -1, 2).contiguous())
+        * torch.exp(1j * s * phi.double()).to(torch.complex64)[:, None]).reshape(t.shape)
+    base = ops.selective_scan_complex_ref(u, delta, A, B, C, D, z, bias, True)
+    turned = ops.selective_scan_complex_ref(u, delta, A, rot(B, 1.0), rot(C, -1.0), D, z, bias, True)
+    assert torch.allclose(base, turned, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("const_b,const_c,groups", [(False, False, 1), (False, False, 2),
+                                                    (True, True, 1), (True, False, 1)])
+def test_complex_scan_bwd_matches_autograd(const_b, const_c, groups):
+    """The complex reverse recurrence equals torch autograd of the complex128
+    forward oracle (complex gradients packed as dL/dRe + i dL/dIm), every
+    gradient, with gate, skip, bias and softplus."""
+    u, delta, A, B, C, D, z, bias = _complex_scan_inputs(l=19, g=groups, seed=55 + groups,
+                                                         const_b=const_b, const_c=const_c)
+    delta = delta - 0.5
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(7))
+    up = lambda t: (t.to(torch.complex128) if t.is_complex() else t.double()).requires_grad_()
+    leaves = [up(t) for t in (u, delta, A, B, C, D, z, bias)]
+    out = ops.selective_scan_complex_ref(leaves[0], leaves[1], leaves[2], leaves[3], leaves[4],
+                                         leaves[5], leaves[6], leaves[7], True)
+    out.backward(dout.double())
+    ref = ops.selective_scan_complex_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    for name, r, t in zip("du ddelta dA dB dC dD dz dbias".split(), ref, leaves):
+        assert r.shape == t.grad.shape, name
+        assert torch.allclose(r, t.grad, rtol=1e-10, atol=1e-11), name
+
+
+def test_complex_scan_bwd_finite_differences():
+    """Central differences of the complex128 forward oracle on a few entries
+    of A (real and imaginary parts), of a variable B and C, of delta and u:
+    the packed complex gradient is dL/dRe + i dL/dIm."""
+    u, delta, A, B, C, D, z, bias = _complex_scan_inputs(b=1, d=2, l=7, n=3, seed=58)
+    dout = torch.randn(u.shape, generator=torch.Generator().manual_seed(8))
+    ref = ops.selective_scan_complex_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
+    A128, B64, C64 = A.to(torch.complex128), B.double(), C.double()
+    loss = lambda uu, dd, aa, bb, cc: float((ops.selective_scan_complex_ref(
+        uu, dd, aa, bb, cc, D, z, bias, True) * dout.double()).sum())
+    base = (u.double(), delta.double(), A128, B64, C64)
+    eps = 1e-6
+
+    def fd(which, idx, step):
+        plus = [t.clone() for t in base]
+        minus = [t.clone() for t in base]
+        plus[which][idx] += step
+        minus[which][idx] -= step
+        return (loss(*plus) - loss(*minus)) / (2 * eps)
+
+    for idx in ((0, 0), (1, 2)):
+        assert abs(fd(2, idx, eps) - ref[2][idx].real) < 1e-6
+        assert abs(fd(2, idx, 1j * eps) - ref[2][idx].imag) < 1e-6
+    for idx in ((0, 0, 1, 4), (0, 0, 2, 9)):
+        assert abs(fd(3, idx, eps) - ref[3][idx]) < 1e-6
+        assert abs(fd(4, idx, eps) - ref[4][idx]) < 1e-6
+    for idx in ((0, 0, 3), (0, 1, 6)):
+        assert abs(fd(0, idx, eps) - ref[0][idx]) < 1e-6
+        assert abs(fd(1, idx, eps) - ref[1][idx]) < 1e-6
+
+
+def test_complex_chunk_states_pinned():
+    """Complex chunk states: the state entry is the complex oracle's last state
+    over the prefix; the decay entry is exp(A sum delta') (a product of
+    exponentials is the exponential of the sum)."""
+    u, delta, A, B, C, D, z, bias = _complex_scan_inputs(l=40, g=2, seed=59)
+    xs = ops.selective_scan_complex_chunk_states_ref(u, delta, A, B, bias, True, chunk=16)
+    assert xs.shape == (2, 4, 3, 6, 2)
+    dl = F.softplus(delta.double() + bias.double()[:, None])
+    for k, end in enumerate((16, 32, 40)):
+        _, last = ops.selective_scan_complex_ref(u[..., :end], delta[..., :end], A, B[..., :2 * end],
+                                                 C[..., :2 * end], None, None, bias, True,
+                                                 return_last_state=True)
+        assert torch.allclose(xs[:, :, k, :, 1], last, rtol=1e-12, atol=1e-12)
+        prod = torch.exp(A.to(torch.complex128)[None] * dl[..., :end].sum(-1)[..., None])
+        assert torch.allclose(xs[:, :, k, :, 0], prod, rtol=1e-12, atol=1e-14)
+
+
 def test_lmhead_ce_ref_softcap_matches_materialised_ce():
     """The streamed lm-head oracle with a logit softcap equals the CE row
     oracle (pinned to F.cross_entropy of the capped logits) on materialised
