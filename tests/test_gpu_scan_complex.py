@@ -107,7 +107,7 @@ def _check_all(args, opts, softplus, itype, got):
         _close(name, gv, rv, tol[name], like=leaf.dtype if name in ("du", "ddelta", "dz") else None)
 
 
-@pytest.mark.parametrize("itype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("itype", ["float32", "float16", "bfloat16"])
 @pytest.mark.parametrize("groups", GRID["varBC_groups"])
 @pytest.mark.parametrize("seqlen", GRID["seqlen"])
 def test_complex_reference_grid(itype, groups, seqlen):
@@ -138,6 +138,23 @@ def test_complex_shapes_and_options(batch, dim, dstate, seqlen, groups, softplus
     got = _run(u, delta, A, B, C, D if "D" in opts else None, z if "z" in opts else None,
                bias if "b" in opts else None, dout, softplus)
     _check_all(args, opts, softplus, "float32", got)
+
+
+@pytest.mark.parametrize("itype,delta32,bc32", [("bfloat16", True, False), ("float16", False, True),
+                                                ("bfloat16", True, True)])
+def test_complex_mixed_dtypes(itype, delta32, bc32):
+    """The forward's mixed layouts with complex weights: fp32 delta and / or
+    fp32 B / C with half-precision u (each its own kernel instantiation)."""
+    need_gpu()
+    dt = ITYPES[itype]
+    u, delta, A, B, C, D, z, bias, dout = _inputs(2, 8, 16, 90, 2, dt, 97)
+    if delta32:
+        delta = delta.float()
+    if bc32:
+        B, C = B.float(), C.float()
+    say("complex scan mixed dtypes", itype, delta32, bc32)
+    got = _run(u, delta, A, B, C, D, z, bias, dout, True)
+    _check_all((u, delta, A, B, C, D, z, bias, dout), "Dzb", True, itype, got)
 
 
 def test_complex_chunk_states_checkpoints_and_saved_backward():
