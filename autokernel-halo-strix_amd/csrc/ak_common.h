@@ -31,6 +31,21 @@ template <> __device__ __forceinline__ float from_f32<float>(float v) { return v
 template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
 template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
 
+// Two floats as a packed pair of 16-bit T (a in the low half), rounded to
+// nearest even as from_f32 does, in one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
+// (Two scalar conversions joined by a shift and an or take three instructions:
+// the compiler converts each half separately.)
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef f16 f16x2_t __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2<bf16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+}
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // One 16-byte global access viewed as VE elements of T.

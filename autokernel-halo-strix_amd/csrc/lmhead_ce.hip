@@ -329,6 +329,8 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
 
   using yes = std::true_type;
   using no = std::false_type;
+  // backward: upstream gradient / number of counted tokens, read once
+  const float gs = kGrad ? ga.grad_loss[0] / ga.denom[0] : 0.0f;
   for (int it = 0; it < n_my; ++it) {
     int vt, tt;
     tile_coords(it, n_vt, n_tt, vt, tt);
@@ -338,11 +340,30 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
 
     load_frags(sw, sh, 0, af[0], bf[0]);
     load_frags(sw, sh, 1, af[1], bf[1]);
+    // backward: the tile's logsumexp and targets, loaded before its last K
+    // block. Vector-memory operations complete in issue order, so a load
+    // issued in the epilogue would wait for the ring's DMA and the previous
+    // tile's dlogits stores as well; issued here, only the last block's DMA
+    // is behind it.
+    float pre_lse[4];
+    int64_t pre_tg[4];
+    auto prefetch_rows = [&]() {
+      if constexpr (kGrad) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const int tok_c = min(t_first + wt * 128 + tb * 32 + fr, n_rows - 1);
+          pre_lse[tb] = ga.lse[tok_c];
+          pre_tg[tb] = ga.targets[tok_c];
+        }
+      }
+    };
     if (nb == 1) {
+      prefetch_rows();
       block(yes{}, yes{});
     } else {
       block(yes{}, no{});
       for (int kb = 1; kb < nb - 1; ++kb) block(no{}, no{});
+      prefetch_rows();
       block(no{}, yes{});
     }
     // The epilogue reads the accumulators with explicit v_accvgpr_read
@@ -364,16 +385,15 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
       // v_permlane32_swap pairs groups (0, 2) and (1, 3) across the two half
       // waves, so that every lane then holds 8 consecutive vocab entries of one
       // token row: one 16-byte store (kFineMask: element-wise stores).
-      const float gs = ga.grad_loss[0] / ga.denom[0];
       T* dzp = static_cast<T*>(ga.dz);
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb) {
         const int tok = t_first + wt * 128 + tb * 32 + fr;
         const int tok_c = min(tok, n_rows - 1);
         const bool tok_ok = tok >= t_own && tok < n_rows;
-        const float lse2 = ga.lse[tok_c] * kLog2e;
+        const float lse2 = pre_lse[tb] * kLog2e;
         const float cl2 = kCap ? ga.cap * kLog2e - lse2 : 0.0f;  // log2 of exp(cap - lse)
-        const int64_t tg = ga.targets[tok_c];
+        const int64_t tg = pre_tg[tb];
         const float st = tg == ga.ignore_index ? 0.0f : ((tg < 0 || tg >= ga.vocab_total) ? NAN : gs);
         const float nls = -(ga.ls / (float)ga.vocab_total) * st;  // label smoothing's uniform term
         T* drow = dzp + (int64_t)tok_c * ga.ld_dz + v_first + wv * 128;
@@ -404,9 +424,7 @@ lmhead_ce_tile_kernel(const T* __restrict__ H, const T* __restrict__ W, MSPair* 
                 if (tok_ok && x0 + j >= lo && x0 + j < hi) drow[4 * khalf + x0 + j] = from_f32<T>(e[j]);
             } else {
 #pragma unroll
-              for (int j = 0; j < 2; ++j)
-                pk[g4][j] = (uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(e[2 * j])) |
-                            ((uint32_t)__builtin_bit_cast(uint16_t, from_f32<T>(e[2 * j + 1])) << 16);
+              for (int j = 0; j < 2; ++j) pk[g4][j] = pack2<T>(e[2 * j], e[2 * j + 1]);
             }
           }
           if constexpr (!kFineMask) {
