@@ -238,3 +238,32 @@ def test_complex_binding_fwd_bwd():
     ref = ops.selective_scan_complex_bwd_ref(u, delta, A, B, C, dout, D, z, bias, True)
     for name, i in (("du", 0), ("ddelta", 1), ("dA", 2), ("dB", 3), ("dC", 4)):
         _close(name, res[i].cpu(), ref[i], tol[name], like=u.dtype if i < 2 else None)
+
+
+def test_complex_strided_inputs():
+    """u, delta, z and dout as channel-strided device views (every other
+    channel of a wider tensor, last dim contiguous), through the C-ABI: the
+    kernels take the batch / channel strides as given."""
+    need_gpu()
+    from kernels.hip import _lib
+    u, delta, A, B, C, D, z, bias, dout = _inputs(2, 10, 16, 70, 1, torch.float32, 99)
+
+    def strided(t):
+        w = torch.stack([t, torch.full_like(t, float("nan"))], dim=2).reshape(t.shape[0], -1, t.shape[2])
+        v = w.to(DEV)[:, ::2]
+        assert not v.is_contiguous() and v.stride(1) == 2 * t.shape[2]
+        return v
+
+    us, ds, zs, gs = (strided(t) for t in (u, delta, z, dout))
+    Ad, Bd, Cd, Dd, bd = (t.to(DEV) for t in (A, B, C, D, bias))
+    say("complex scan strided inputs")
+    out = torch.empty(u.shape, device=DEV)
+    last = torch.empty((2, 10, 16), dtype=torch.complex64, device=DEV)
+    _lib.selective_scan(us, ds, Ad, Bd, Cd, Dd, zs, bd, out, last, True)
+    grads = [torch.empty(u.shape, device=DEV), torch.empty(u.shape, device=DEV), torch.empty_like(Ad),
+             torch.empty_like(Bd), torch.empty_like(Cd), torch.empty_like(Dd), torch.empty(u.shape, device=DEV),
+             torch.empty_like(bd)]
+    _lib.selective_scan_bwd(us, ds, Ad, Bd, Cd, Dd, zs, bd, gs, *grads[:6], grads[6], grads[7], True)
+    torch.cuda.synchronize()
+    _check_all((u, delta, A, B, C, D, z, bias, dout), "Dzb", True, "float32",
+               (out.cpu(), last.cpu(), [t.cpu() for t in grads]))
