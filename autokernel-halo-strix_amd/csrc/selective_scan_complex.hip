@@ -18,13 +18,15 @@
 // log2 e), phase sincos(delta' Im A)), h = a h + delta' u B, and the output
 // y = 2 Re sum_n h C + D u, then the gate.
 //
-// Work split: a workgroup holds 4 channels of one group, one wave each; lane
-// s of a wave owns the states s + 64 i, i < KS (dstate <= 64 KS). Steps go in
-// 16-step tiles: lanes 0..15 read the tile's per-channel inputs (one step
-// each) into a per-wave LDS table that every lane reads back, an
-// input-dependent B / C tile is staged in LDS as fp32 for the workgroup, and
-// the per-step sums over the 64 lanes go through a per-wave LDS transpose
-// summed in a fixed order.
+// Work split: LPC lanes per channel, 64 / LPC channels per wave, 4 waves per
+// workgroup, all of one group: LPC = 64 (one channel per wave) for dstate >
+// 16, lane s owning the states s + 64 i, i < KS (dstate <= 64 KS); LPC = 16
+// (four channels per wave) for dstate <= 16, one state per lane. Steps go in
+// 16-step tiles: lanes 0..15 of a channel read the tile's per-channel inputs
+// (one step each) into a per-channel LDS table that the channel's lanes read
+// back, an input-dependent B / C tile is staged in LDS as fp32 for the
+// workgroup, and the per-step sums over a channel's lanes go through a
+// per-wave LDS transpose summed in a fixed order.
 //
 // Backward (reverse over tiles, from the 16-step checkpoints): per state the
 // tile's decays and states are recomputed from the checkpoint, then the
@@ -34,8 +36,8 @@
 //        + Re(conj(g_l conj(h_{l-1})) A a_l);
 //   dA += delta'_l conj(a_l) g_l conj(h_{l-1});  dB_l = delta'_l u_l g_l;
 //   dC_l = 2 dy_l conj(h_l).
-// An input-dependent dB / dC is summed over the workgroup's 4 channels in
-// wave order and written as one partial row per 4-channel tile; dA, dD,
+// An input-dependent dB / dC is summed over the workgroup's channels in a
+// fixed order and written as one partial row per workgroup's channel tile; dA, dD,
 // ddelta_bias and an input-independent dB / dC as per-batch partials. A
 // finish launch adds the partials in a fixed order: every gradient is
 // bitwise reproducible.
@@ -46,7 +48,11 @@ namespace {
 
 constexpr int kZT = 16;    // steps per tile (= kCk, the checkpoint block)
 constexpr int kZP = 34;    // staged B / C: floats per state row (16 steps x (re, im) + 2)
-constexpr int kZW = 4;     // channels (waves) per workgroup
+constexpr int kZW = 4;     // waves per workgroup
+
+// Lanes per channel for a dstate, and channels per workgroup.
+__host__ __device__ inline int zlpc(int dstate) { return dstate <= 16 ? 16 : 64; }
+__host__ __device__ inline int zcpb(int dstate) { return kZW * (64 / zlpc(dstate)); }
 constexpr int kZY = 16 * 64;  // per-wave transpose buffer (floats)
 
 struct ZLayout {
@@ -59,7 +65,7 @@ __host__ __device__ inline ZLayout zlayout(int dstate, bool bvar, bool cvar, boo
   int o = 0;
   L.bs = o; o += a4(bvar ? dstate * kZP : 0);
   L.cs = o; o += a4(cvar ? dstate * kZP : 0);
-  L.tab = o; o += kZW * kZT * 4;
+  L.tab = o; o += zcpb(dstate) * kZT * 4;
   L.y = o; o += kZW * kZY;
   L.gb = o; o += (bwd && bvar) ? kZW * 64 * 32 : 0;
   L.gc = o; o += (bwd && cvar) ? kZW * 64 * 32 : 0;
@@ -93,19 +99,21 @@ __device__ __forceinline__ void zstage(float* dst, const TBC* src, int64_t ns, i
   }
 }
 
-// Sum over the wave's 64 lanes of v[j] (one value per step j < 16): lane j
-// of the wave returns the sum for step j, in a fixed order.
+// Sum over a channel's LPC lanes of v[j] (one value per step j < 16): lane j
+// of the channel returns the sum for step j, in a fixed order.
+template <int LPC>
 __device__ __forceinline__ float zlane_sum(const float (&v)[kZT], float* buf, int lane) {
 #pragma unroll
   for (int j = 0; j < kZT; ++j) buf[j * 64 + lane] = v[j];
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
+  const int cw = lane / LPC, sl = lane % LPC;
   float r = 0.0f;
-  if (lane < kZT) {
+  if (sl < kZT) {
     float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int k = 0; k < 64; k += 4) {
-      const float4 q = *reinterpret_cast<const float4*>(&buf[lane * 64 + k]);
+    for (int k = 0; k < LPC; k += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(&buf[sl * 64 + cw * LPC + k]);
       s4[0] += q.x;
       s4[1] += q.y;
       s4[2] += q.z;
@@ -118,23 +126,25 @@ __device__ __forceinline__ float zlane_sum(const float (&v)[kZT], float* buf, in
   return r;
 }
 
-template <typename TU, typename TD, typename TBC, int KS>
+template <typename TU, typename TD, typename TBC, int KS, int LPC>
 __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams p) {
+  constexpr int CPW = 64 / LPC;  // channels per wave
   extern __shared__ float lds[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int cw = lane / LPC, sl = lane % LPC;  // channel within the wave, state lane
   const int per_batch = p.ngroups * p.tiles_per_group;
   const int b = blockIdx.x / per_batch;
   const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
   const int tile = blockIdx.x % p.tiles_per_group;
-  const int ch_local = tile * kZW + wave;
+  const int ch_local = tile * (kZW * CPW) + wave * CPW + cw;
   const bool ch_ok = ch_local < p.ch_per_group;
   const int d = g * p.ch_per_group + (ch_ok ? ch_local : p.ch_per_group - 1);
   const bool bvar = !p.b_const, cvar = !p.c_const;
   const ZLayout Lo = zlayout(p.dstate, bvar, cvar, false);
   float* Bs = lds + Lo.bs;
   float* Cs = lds + Lo.cs;
-  float* tab = lds + Lo.tab + wave * kZT * 4;
+  float* tab = lds + Lo.tab + (wave * CPW + cw) * kZT * 4;
   float* yb = lds + Lo.y + wave * kZY;
 
   const float* Af = p.A;
@@ -142,7 +152,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
   Cx x[KS], bc[KS], cc[KS];
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
-    const int s = lane + 64 * i;
+    const int s = sl + LPC * i;
     const bool ok = s < p.dstate;
     const int64_t ea = 2 * ((int64_t)d * p.A_ds + (ok ? s : 0));
     ar2[i] = ok ? Af[ea] * kLog2e : 0.0f;
@@ -176,7 +186,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
     if (p.ck && ch_ok) {
 #pragma unroll
       for (int i = 0; i < KS; ++i) {
-        const int s = lane + 64 * i;
+        const int s = sl + LPC * i;
         if (s < p.dstate) {
           float* q = p.ck + 2 * ((((int64_t)b * p.nchunks + t) * p.dim + d) * p.dstate + s);
           q[0] = x[i].r;
@@ -188,16 +198,16 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
     if (bvar) zstage<TBC>(Bs, bsrc, p.B_ns, p.dstate, l0, p.seqlen, tid);
     if (cvar) zstage<TBC>(Cs, csrc, p.C_ns, p.dstate, l0, p.seqlen, tid);
     float u_l = 0.0f, z_l = 0.0f;
-    if (lane < kZT) {
-      const bool ok = lane < nst;
-      const int l = l0 + (ok ? lane : 0);
+    if (sl < kZT) {
+      const bool ok = sl < nst;
+      const int l = l0 + (ok ? sl : 0);
       float dl = to_f32(dp[l]) + dbias;
       if (p.softplus) dl = softplus_f32(dl);
       u_l = to_f32(up[l]);
       z_l = zp ? to_f32(zp[l]) : 0.0f;
       dl = ok ? dl : 0.0f;
-      tab[lane * 4 + 0] = dl;
-      tab[lane * 4 + 1] = dl * u_l;
+      tab[sl * 4 + 0] = dl;
+      tab[sl * 4 + 1] = dl * u_l;
     }
     __syncthreads();
     float yp[kZT];
@@ -208,7 +218,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
       float acc = 0.0f;
 #pragma unroll
       for (int i = 0; i < KS; ++i) {
-        const int s = lane + 64 * i;
+        const int s = sl + LPC * i;
         if (s < p.dstate) {
           const Cx a = cexp_step(dl, ar2[i], ai[i]);
           const Cx bv = bvar ? Cx{Bs[s * kZP + 2 * j], Bs[s * kZP + 2 * j + 1]} : bc[i];
@@ -228,7 +238,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
       const int k = (lend - 1) / kXChunk;
 #pragma unroll
       for (int i = 0; i < KS; ++i) {
-        const int s = lane + 64 * i;
+        const int s = sl + LPC * i;
         if (s < p.dstate) {
           const Cx pr = cexp_step(dsum, ar2[i], ai[i]);
           float* q = p.chunk_states + 4 * ((((int64_t)b * p.dim + d) * p.xchunks + k) * p.dstate + s);
@@ -239,18 +249,18 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
         }
       }
     }
-    const float ysum = zlane_sum(yp, yb, lane);
-    if (lane < nst && ch_ok) {
+    const float ysum = zlane_sum<LPC>(yp, yb, lane);
+    if (sl < nst && ch_ok) {
       float o = fmaf(dskip, u_l, 2.0f * ysum);
-      if (p.out_prez) static_cast<TU*>(p.out_prez)[orow + l0 + lane] = from_f32<TU>(o);
+      if (p.out_prez) static_cast<TU*>(p.out_prez)[orow + l0 + sl] = from_f32<TU>(o);
       if (zp) o *= silu_fast(z_l);
-      if (p.out) static_cast<TU*>(p.out)[orow + l0 + lane] = from_f32<TU>(o);
+      if (p.out) static_cast<TU*>(p.out)[orow + l0 + sl] = from_f32<TU>(o);
     }
   }
   if (p.last_state && ch_ok) {
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
-      const int s = lane + 64 * i;
+      const int s = sl + LPC * i;
       if (s < p.dstate) {
         float* q = p.last_state + 2 * (((int64_t)b * p.dim + d) * p.dstate + s);
         q[0] = x[i].r;
@@ -264,23 +274,25 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
 // host): dA_part complex [batch, dim, dstate]; dD_part / dbias_part
 // [batch, dim]; dBc_part / dCc_part complex [batch, dim, dstate];
 // dB_part / dC_part [tiles, batch, ngroups, dstate, 2 seqlen].
-template <typename TU, typename TD, typename TBC, int KS>
+template <typename TU, typename TD, typename TBC, int KS, int LPC>
 __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams p) {
+  constexpr int CPW = 64 / LPC;  // channels per wave
   extern __shared__ float lds[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int cw = lane / LPC, sl = lane % LPC;  // channel within the wave, state lane
   const int per_batch = p.ngroups * p.tiles_per_group;
   const int b = blockIdx.x / per_batch;
   const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
   const int tile = blockIdx.x % p.tiles_per_group;
-  const int ch_local = tile * kZW + wave;
+  const int ch_local = tile * (kZW * CPW) + wave * CPW + cw;
   const bool ch_ok = ch_local < p.ch_per_group;
   const int d = g * p.ch_per_group + (ch_ok ? ch_local : p.ch_per_group - 1);
   const bool bvar = !p.b_const, cvar = !p.c_const;
   const ZLayout Lo = zlayout(p.dstate, bvar, cvar, true);
   float* Bs = lds + Lo.bs;
   float* Cs = lds + Lo.cs;
-  float* tab = lds + Lo.tab + wave * kZT * 4;
+  float* tab = lds + Lo.tab + (wave * CPW + cw) * kZT * 4;
   float* yb = lds + Lo.y + wave * kZY;
   float* gbB = lds + Lo.gb;
   float* gbC = lds + Lo.gc;
@@ -289,7 +301,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
   Cx gs[KS], an[KS], accA[KS], accB[KS], accC[KS], bc[KS], cc[KS];
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
-    const int s = lane + 64 * i;
+    const int s = sl + LPC * i;
     const bool ok = s < p.dstate;
     const int64_t ea = 2 * ((int64_t)d * p.A_ds + (ok ? s : 0));
     arn[i] = ok ? p.A[ea] : 0.0f;
@@ -331,9 +343,9 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
     if (bvar) zstage<TBC>(Bs, bsrc, p.B_ns, p.dstate, l0, p.seqlen, tid);
     if (cvar) zstage<TBC>(Cs, csrc, p.C_ns, p.dstate, l0, p.seqlen, tid);
     float draw = 0.0f, dy = 0.0f;
-    if (lane < kZT) {
-      const bool ok = lane < nst;
-      const int l = l0 + (ok ? lane : 0);
+    if (sl < kZT) {
+      const bool ok = sl < nst;
+      const int l = l0 + (ok ? sl : 0);
       draw = to_f32(dp[l]) + dbias;
       const float dl = ok ? (p.softplus ? softplus_f32(draw) : draw) : 0.0f;
       const float uu = to_f32(up[l]);
@@ -349,10 +361,10 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
         }
       }
       dD_acc = fmaf(dy, uu, dD_acc);
-      tab[lane * 4 + 0] = dl;
-      tab[lane * 4 + 1] = dl * uu;
-      tab[lane * 4 + 2] = uu;
-      tab[lane * 4 + 3] = dy;
+      tab[sl * 4 + 0] = dl;
+      tab[sl * 4 + 1] = dl * uu;
+      tab[sl * 4 + 2] = uu;
+      tab[sl * 4 + 3] = dy;
     }
     __syncthreads();
     float ddl_p[kZT], du_p[kZT];
@@ -363,7 +375,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
     }
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
-      const int s = lane + 64 * i;
+      const int s = sl + LPC * i;
       const bool ok = s < p.dstate;
       const int sc = ok ? s : 0;
       Cx x0 = {0.0f, 0.0f};
@@ -437,8 +449,8 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
         accC[i] = dCa;
       }
       if (bvar || cvar) {
-        // the 4 channels' rows of this state, added in wave order; channels
-        // past the group's end add 0
+        // the workgroup's channels' rows of this state, added in channel
+        // order; channels past the group's end add 0
         if (bvar) {
 #pragma unroll
           for (int k = 0; k < 2 * kZT; k += 4)
@@ -453,8 +465,9 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
         }
         __syncthreads();
         {
-          const int sl = tid >> 2, q8 = (tid & 3) * 8;  // lane sl's words q8 .. q8 + 7
-          const int st = sl + 64 * i;
+          constexpr int WPT = LPC * 32 / 256;               // words per thread
+          const int rs = tid / (32 / WPT), q8 = (tid % (32 / WPT)) * WPT;  // state lane, first word
+          const int st = rs + LPC * i;
           if (st < p.dstate) {
             const int64_t row = ((((int64_t)tile * p.batch + b) * p.ngroups + g) * p.dstate + st) * (2 * (int64_t)p.seqlen);
             for (int v = 0; v < 2; ++v) {
@@ -462,11 +475,12 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
               const float* gbuf = v == 0 ? gbB : gbC;
               float* part = v == 0 ? p.dB_part : p.dC_part;
 #pragma unroll
-              for (int k = 0; k < 8; ++k) {
+              for (int k = 0; k < WPT; ++k) {
                 const int w = q8 + k;  // (re, im) word of step w / 2
-                float sum = gbuf[(0 * 64 + sl) * 32 + w];
+                float sum = gbuf[rs * 32 + w];
 #pragma unroll
-                for (int wv = 1; wv < kZW; ++wv) sum += gbuf[(wv * 64 + sl) * 32 + w];
+                for (int ch = 1; ch < kZW * CPW; ++ch)
+                  sum += gbuf[((ch / CPW) * 64 + (ch % CPW) * LPC + rs) * 32 + w];
                 if ((w >> 1) < nst) part[row + 2 * (int64_t)l0 + w] = sum;
               }
             }
@@ -476,20 +490,20 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
       }
     }
     // per-step sums over the wave's states
-    const float ddl = zlane_sum(ddl_p, yb, lane);
-    const float dus = zlane_sum(du_p, yb, lane);
-    if (lane < nst && ch_ok) {
+    const float ddl = zlane_sum<LPC>(ddl_p, yb, lane);
+    const float dus = zlane_sum<LPC>(du_p, yb, lane);
+    if (sl < nst && ch_ok) {
       float dd = ddl;
       if (p.softplus && draw <= 20.0f) dd = ddl * sigmoid_f32(draw);
-      static_cast<TU*>(p.du)[orow + l0 + lane] = from_f32<TU>(fmaf(dskip, dy, dus));
-      static_cast<TD*>(p.ddelta)[orow + l0 + lane] = from_f32<TD>(dd);
+      static_cast<TU*>(p.du)[orow + l0 + sl] = from_f32<TU>(fmaf(dskip, dy, dus));
+      static_cast<TD*>(p.ddelta)[orow + l0 + sl] = from_f32<TD>(dd);
       dbias_acc += dd;
     }
   }
   // per-batch partials
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
-    const int s = lane + 64 * i;
+    const int s = sl + LPC * i;
     if (s < p.dstate && ch_ok) {
       const int64_t e = 2 * (((int64_t)b * p.dim + d) * p.dstate + s);
       p.dA_part[e] = accA[i].r;
@@ -504,21 +518,21 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_bwd_kernel(ScanParams 
       }
     }
   }
-  // dD / ddelta_bias: lanes 0..15 hold per-lane sums over their steps; add
-  // them in lane order through the transpose buffer
+  // dD / ddelta_bias: lanes 0..15 of a channel hold per-lane sums over their
+  // steps; add them in lane order through the transpose buffer
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
-  if (lane < kZT) {
-    yb[lane] = dD_acc;
-    yb[kZT + lane] = dbias_acc;
+  if (sl < kZT) {
+    yb[2 * kZT * cw + sl] = dD_acc;
+    yb[2 * kZT * cw + kZT + sl] = dbias_acc;
   }
   __builtin_amdgcn_wave_barrier();
   asm volatile("" ::: "memory");
-  if (lane == 0 && ch_ok) {
+  if (sl == 0 && ch_ok) {
     float sD = 0.0f, sb = 0.0f;
     for (int j = 0; j < kZT; ++j) {
-      sD += yb[j];
-      sb += yb[kZT + j];
+      sD += yb[2 * kZT * cw + j];
+      sb += yb[2 * kZT * cw + kZT + j];
     }
     p.dD_part[(int64_t)b * p.dim + d] = sD;
     p.dbias_part[(int64_t)b * p.dim + d] = sb;
@@ -593,17 +607,17 @@ __global__ void __launch_bounds__(256) scan_complex_bc_sum_kernel(ZFin f) {
 
 int zks(int dstate) { return (dstate + 63) / 64; }
 
-template <typename TU, typename TD, typename TBC, int KS>
+template <typename TU, typename TD, typename TBC, int KS, int LPC = 64>
 void launch_fwd_ks(const ScanParams& p, size_t bytes, int grid, hipStream_t s) {
-  auto kernel = mamba_scan_complex_fwd_kernel<TU, TD, TBC, KS>;
+  auto kernel = mamba_scan_complex_fwd_kernel<TU, TD, TBC, KS, LPC>;
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   kernel<<<dim3(grid), dim3(256), bytes, s>>>(p);
 }
 
-template <typename TU, typename TD, typename TBC, int KS>
+template <typename TU, typename TD, typename TBC, int KS, int LPC = 64>
 void launch_bwd_ks(const ScanParams& p, size_t bytes, int grid, hipStream_t s) {
-  auto kernel = mamba_scan_complex_bwd_kernel<TU, TD, TBC, KS>;
+  auto kernel = mamba_scan_complex_bwd_kernel<TU, TD, TBC, KS, LPC>;
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   kernel<<<dim3(grid), dim3(256), bytes, s>>>(p);
@@ -614,6 +628,10 @@ void zfwd(const ScanParams& p, hipStream_t s) {
   const ZLayout L = zlayout(p.dstate, !p.b_const, !p.c_const, false);
   const size_t bytes = (size_t)L.total * 4;
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
+  if (zlpc(p.dstate) == 16) {
+    launch_fwd_ks<TU, TD, TBC, 1, 16>(p, bytes, grid, s);
+    return;
+  }
   switch (zks(p.dstate)) {
     case 1: launch_fwd_ks<TU, TD, TBC, 1>(p, bytes, grid, s); break;
     case 2: launch_fwd_ks<TU, TD, TBC, 2>(p, bytes, grid, s); break;
@@ -627,6 +645,10 @@ void zbwd(const ScanParams& p, hipStream_t s) {
   const ZLayout L = zlayout(p.dstate, !p.b_const, !p.c_const, true);
   const size_t bytes = (size_t)L.total * 4;
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
+  if (zlpc(p.dstate) == 16) {
+    launch_bwd_ks<TU, TD, TBC, 1, 16>(p, bytes, grid, s);
+    return;
+  }
   switch (zks(p.dstate)) {
     case 1: launch_bwd_ks<TU, TD, TBC, 1>(p, bytes, grid, s); break;
     case 2: launch_bwd_ks<TU, TD, TBC, 2>(p, bytes, grid, s); break;
@@ -675,7 +697,7 @@ ZWs scan_complex_bwd_ws(int64_t batch, int64_t dim, int64_t seqlen, int64_t dsta
                         int bc_flags) {
   ZWs w{};
   const int64_t cpg = dim / ngroups;
-  const int64_t tiles = (cpg + kZW - 1) / kZW;
+  const int64_t tiles = (cpg + zcpb((int)dstate) - 1) / zcpb((int)dstate);
   const int64_t nck = (seqlen + kCk - 1) / kCk;
   w.ck = zalign((size_t)(batch * nck * dim * dstate) * 8);
   w.prez = zalign((size_t)(batch * dim * seqlen) * 4);
@@ -697,7 +719,7 @@ void launch_scan_complex_zero(int dim, int dstate, float* dA, float* dD, float* 
 }
 
 int launch_scan_complex_fwd(ScanParams p, int u_dtype, int delta_dtype, int bc_dtype, hipStream_t s) {
-  p.tiles_per_group = (p.ch_per_group + kZW - 1) / kZW;
+  p.tiles_per_group = (p.ch_per_group + zcpb(p.dstate) - 1) / zcpb(p.dstate);
   if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF) return 1;
   return zdispatch<ZFwd>(u_dtype, delta_dtype, bc_dtype, p, s) ? 0 : 1;
 }
@@ -705,7 +727,7 @@ int launch_scan_complex_fwd(ScanParams p, int u_dtype, int delta_dtype, int bc_d
 int launch_scan_complex_bwd(ScanParams p, const ZWs& ws, void* workspace, bool saved, int u_dtype,
                             int delta_dtype, int bc_dtype, void* dB, void* dC, float* dA, float* dD,
                             float* ddelta_bias, hipStream_t s) {
-  p.tiles_per_group = (p.ch_per_group + kZW - 1) / kZW;
+  p.tiles_per_group = (p.ch_per_group + zcpb(p.dstate) - 1) / zcpb(p.dstate);
   if ((int64_t)p.batch * p.ngroups * p.tiles_per_group > 0x7FFFFFFF) return 1;
   char* w = static_cast<char*>(workspace);
   size_t off = 0;
