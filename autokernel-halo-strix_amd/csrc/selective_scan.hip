@@ -587,6 +587,270 @@ mamba_scan_fast_kernel(ScanParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Producer / consumer split of the whole-tile forward for dstate <= 16
+// (mamba_scan_split_kernel). At the C5 shape the (channel, state) lanes fill
+// only 2 waves per SIMD, and at that occupancy the recurrence's dependent FMA
+// chain and exp2 latency leave the SIMDs idle about a third of the time. This
+// kernel doubles the waves without duplicating any arithmetic: a workgroup of
+// 16 channels has 8 waves. Waves 0-3 (producers) run the recurrence exactly as
+// mamba_scan_fast_kernel does and write each 16-step block's states into a
+// transpose buffer; waves 4-7 (consumers) read block K's states while the
+// producers compute block K + 1, and form the outputs: y = sum_n h C + D u,
+// then the gate, or in the backward's preparation pass dz. The transpose
+// buffer is double-buffered per producer wave and one workgroup barrier per
+// block hands it over (LDS counters between each producer / consumer pair
+// instead measured 9-20% slower: the flag round trips sit on the producers'
+// critical path). Producers run at a raised wave priority (s_setprio 2), so a
+// SIMD issues the recurrence first and fills its gaps with consumer work. The
+// producers stage B, the consumers C, each double-buffered per 64-step tile.
+// The arithmetic and its order are those of mamba_scan_fast_kernel, so every
+// output has the same bits.
+//
+// kMode: kFwdLean / kFwdTrain as for mamba_scan_fast_kernel (a gate z is
+// required), or kPrepGated: the backward's preparation pass with a gate
+// (checkpoints by the producers, dz = dout y sigma(z) (1 + z (1 - sigma(z)))
+// by the consumers).
+enum { kPrepGated = 3 };
+
+template <typename TU, typename TD, typename TBC, bool kSoftplus, int kMode>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
+mamba_scan_split_kernel(ScanParams p) {
+  static_assert(kMode == kFwdLean || kMode == kFwdTrain || kMode == kPrepGated, "split modes");
+  constexpr bool kPrep = kMode == kPrepGated;
+  constexpr bool kPrez = kMode == kFwdTrain;
+  constexpr bool kSaveCk = kMode != kFwdLean;
+  __shared__ float Bs[2][16 * kBStride];
+  __shared__ float Cs[2][kScanT * kCStride];
+  __shared__ float hbuf[2][4][4 * kHC];  // [block parity][producer wave][c][j][n]
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // wave-uniform role
+  const bool producer = wave < 4;
+  const int pw = wave & 3;  // the producer / consumer pair: channels 4 pw .. 4 pw + 3
+  const int lane = tid % 64;
+  const int c = lane / 16;
+  const int n = lane % 16;
+  const int per_batch = p.ngroups * p.tiles_per_group;
+  const int b = blockIdx.x / per_batch;
+  const int g = (blockIdx.x % per_batch) / p.tiles_per_group;
+  const int tile = blockIdx.x % p.tiles_per_group;
+  const int d0 = g * p.ch_per_group + tile * kScanCh;
+  const int wc = pw * 4 + c;
+  const int d = d0 + wc;
+  const bool n_ok = n < p.dstate;
+  const uint32_t L = (uint32_t)p.seqlen;
+  const int nt = p.seqlen / kScanT;
+  auto row_rsrc = [&](const void* base, int64_t bs, int64_t ds, int esz) {
+    const char* q = static_cast<const char*>(base) + ((int64_t)b * bs + (int64_t)d0 * ds) * esz;
+    return make_rsrc(q, (uint32_t)(((kScanCh - 1) * ds + L) * esz));
+  };
+  // staging: thread r of each role loads state sn, steps 4 q .. 4 q + 3 of B
+  // (producers) or C (consumers)
+  const int r = tid & 255;
+  const int sn = r % 16, q = r / 16;
+  const int sn_c = min(sn, p.dstate - 1);
+  const bool s_ok = sn < p.dstate;
+
+  if (producer) {
+    __builtin_amdgcn_s_setprio(2);
+    const float a_scaled = n_ok ? p.A[(int64_t)d * p.A_ds + n] * kLog2e : 0.0f;
+    const float dbias = p.delta_bias ? p.delta_bias[d] : 0.0f;
+    const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
+    const Rsrc rs_d = row_rsrc(p.delta, p.d_bs, p.d_ds, sizeof(TD));
+    const uint32_t bc_bytes_B = (uint32_t)(((p.dstate - 1) * p.B_ns + L) * sizeof(TBC));
+    const Rsrc rs_B = make_rsrc(static_cast<const TBC*>(p.B) + (int64_t)b * p.B_bs + (int64_t)g * p.B_gs, bc_bytes_B);
+    const uint32_t vo_d4 = (uint32_t)(wc * p.d_ds + 4 * n) * sizeof(TD);  // delta, steps 4n..4n+3
+    const uint32_t vo_u4 = (uint32_t)(wc * p.u_ds + 4 * n) * sizeof(TU);
+    const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
+    // checkpoints [batch, nchunks, dim, dstate]: the batch's slab, the chunk in the scalar offset
+    const Rsrc rs_ck = make_rsrc(kSaveCk ? p.ck + (int64_t)b * p.nchunks * p.dim * p.dstate : p.A,
+                                 kSaveCk ? (uint32_t)((int64_t)p.nchunks * p.dim * p.dstate * 4) : 0u);
+    const uint32_t vo_ck = (uint32_t)(d * p.dstate + n) * 4u;
+    const uint32_t ck_chunk_bytes = (uint32_t)(p.dim * p.dstate * 4);
+    struct Regs {
+      Raw4<TD> dv;
+      Raw4<TU> uv;
+    };
+    auto load_regs = [&](int t, Regs& rr) {
+      const uint32_t l0 = (uint32_t)t * kScanT;
+      rr.dv = bload4<TD>(rs_d, vo_d4, l0 * sizeof(TD));
+      rr.uv = bload4<TU>(rs_u, vo_u4, l0 * sizeof(TU));
+    };
+    auto write_B = [&](const Raw4<TBC>& v, int buf) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) Bs[buf][sn * kBStride + 4 * q + k] = s_ok ? raw4_f32<TBC>(v, k) : 0.0f;
+    };
+    Raw4<TBC> sv = bload4<TBC>(rs_B, vo_B, 0u);
+    Regs ra, rb;
+    load_regs(0, ra);
+    write_B(sv, 0);
+    sv = bload4<TBC>(rs_B, vo_B, (uint32_t)min(1, nt - 1) * kScanT * sizeof(TBC));
+    __syncthreads();
+    float h = 0.0f;
+    // Tile t: stage tile t + 1's B (its buffer was last read in tile t - 1,
+    // before the barrier that ended it), issue the loads of tile t + 2's B
+    // and tile t + 1's delta / u (clamped to the last tile), then the four
+    // blocks, each ending with the states written and a barrier.
+    auto tile_body = [&](int t, const Regs& cur, Regs& nxt) {
+      write_B(sv, (t + 1) & 1);
+      sv = bload4<TBC>(rs_B, vo_B, (uint32_t)min(t + 2, nt - 1) * kScanT * sizeof(TBC));
+      load_regs(min(t + 1, nt - 1), nxt);
+      asm volatile("" ::: "memory");
+      const int buf = t & 1;
+      float hck[kScanT / 16];  // the states before the tile's 16-step blocks (checkpoints)
+      float dl[4], du[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float dv = raw4_f32<TD>(cur.dv, k) + dbias;
+        if constexpr (kSoftplus) dv = softplus_f32(dv);
+        dl[k] = dv;
+        du[k] = dv * raw4_f32<TU>(cur.uv, k);
+      }
+      // wait states between the last VALU write of dl / du and their DPP reads
+      asm volatile("s_nop 1"
+                   : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
+                     "+v"(du[2]), "+v"(du[3]));
+#pragma unroll
+      for (int blk = 0; blk < kScanT / 16; ++blk) {
+        hck[blk] = h;
+        float bt[16], hv[16], av[16], xv[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) bt[l] = Bs[buf][n * kBStride + 16 * blk + l];
+        auto steps4 = [&](auto src_c, int j4) {
+          constexpr int kSrc = decltype(src_c)::value;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) av[4 * j4 + k] = mul_bcast<kSrc>(dl[k], a_scaled);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) xv[4 * j4 + k] = mul_bcast<kSrc>(du[k], bt[4 * j4 + k]);
+        };
+        switch (blk) {
+          case 0:
+            steps4(std::integral_constant<int, 0>{}, 0); steps4(std::integral_constant<int, 1>{}, 1);
+            steps4(std::integral_constant<int, 2>{}, 2); steps4(std::integral_constant<int, 3>{}, 3);
+            break;
+          case 1:
+            steps4(std::integral_constant<int, 4>{}, 0); steps4(std::integral_constant<int, 5>{}, 1);
+            steps4(std::integral_constant<int, 6>{}, 2); steps4(std::integral_constant<int, 7>{}, 3);
+            break;
+          case 2:
+            steps4(std::integral_constant<int, 8>{}, 0); steps4(std::integral_constant<int, 9>{}, 1);
+            steps4(std::integral_constant<int, 10>{}, 2); steps4(std::integral_constant<int, 11>{}, 3);
+            break;
+          default:
+            steps4(std::integral_constant<int, 12>{}, 0); steps4(std::integral_constant<int, 13>{}, 1);
+            steps4(std::integral_constant<int, 14>{}, 2); steps4(std::integral_constant<int, 15>{}, 3);
+            break;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) av[j] = __builtin_amdgcn_exp2f(av[j]);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          h = fmaf(av[j], h, xv[j]);
+          hv[j] = h;
+        }
+        // block 4 t + blk's states, [c][j][n]: its buffer was last read (block
+        // 4 t + blk - 2) before the previous barrier
+        float* hb = hbuf[blk & 1][pw];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
+        __syncthreads();
+      }
+      if (kSaveCk && n_ok) {
+#pragma unroll
+        for (int blk = 0; blk < kScanT / 16; ++blk)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hck[blk]), rs_ck, (int)vo_ck,
+                                                (int)((uint32_t)((t * kScanT + 16 * blk) / kCk) * ck_chunk_bytes), 0);
+      }
+    };
+    for (int t = 0; t < nt; t += 2) {
+      tile_body(t, ra, rb);
+      if (t + 1 < nt) tile_body(t + 1, rb, ra);
+    }
+    if (!kPrep && p.last_state && n_ok) p.last_state[((int64_t)b * p.dim + d) * p.dstate + n] = h;
+  } else {
+    const float dskip = p.D ? p.D[d] : 0.0f;
+    const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
+    const Rsrc rs_z = row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU));
+    // the forward's output, or the preparation pass's dz
+    const Rsrc rs_o = row_rsrc(kPrep ? p.dz : p.out, p.o_bs, p.o_ds, sizeof(TU));
+    const Rsrc rs_oz = kPrez ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
+    const Rsrc rs_go = kPrep ? row_rsrc(p.dout, p.go_bs, p.go_ds, sizeof(TU)) : rs_u;
+    const uint32_t bc_bytes_C = (uint32_t)(((p.dstate - 1) * p.C_ns + L) * sizeof(TBC));
+    const Rsrc rs_C = make_rsrc(static_cast<const TBC*>(p.C) + (int64_t)b * p.C_bs + (int64_t)g * p.C_gs, bc_bytes_C);
+    // lane (c, n) forms step 16 blk + n of channel wc
+    const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);
+    const uint32_t vo_z1 = (uint32_t)(wc * p.z_ds + n) * sizeof(TU);
+    const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);
+    const uint32_t vo_go1 = kPrep ? (uint32_t)(wc * p.go_ds + n) * sizeof(TU) : 0u;
+    const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
+    struct Regs {
+      Raw1<TU> uo[4], zo[4];
+      Raw1<TU> go[kPrep ? 4 : 1];
+    };
+    auto load_regs = [&](int t, Regs& rr) {
+      const uint32_t l0 = (uint32_t)t * kScanT;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        rr.uo[blk] = bload1<TU>(rs_u, vo_u1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+        rr.zo[blk] = bload1<TU>(rs_z, vo_z1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+        if constexpr (kPrep) rr.go[blk] = bload1<TU>(rs_go, vo_go1 + 16 * blk * sizeof(TU), l0 * sizeof(TU));
+      }
+    };
+    auto write_C = [&](const Raw4<TBC>& v, int buf) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) Cs[buf][(4 * q + k) * kCStride + sn] = s_ok ? raw4_f32<TBC>(v, k) : 0.0f;
+    };
+    Raw4<TBC> sv = bload4<TBC>(rs_C, vo_C, 0u);
+    Regs ra, rb;
+    load_regs(0, ra);
+    write_C(sv, 0);
+    sv = bload4<TBC>(rs_C, vo_C, (uint32_t)min(1, nt - 1) * kScanT * sizeof(TBC));
+    __syncthreads();
+    // Tile t: after each block's barrier, that block's states are complete;
+    // after the first, stage tile t + 1's C (its buffer was last read for
+    // block 4 t - 1, before that barrier) and issue the next loads.
+    auto tile_body = [&](int t, const Regs& cur, Regs& nxt) {
+      const int buf = t & 1;
+#pragma unroll
+      for (int blk = 0; blk < kScanT / 16; ++blk) {
+        __syncthreads();
+        if (blk == 0) {
+          write_C(sv, (t + 1) & 1);
+          sv = bload4<TBC>(rs_C, vo_C, (uint32_t)min(t + 2, nt - 1) * kScanT * sizeof(TBC));
+          load_regs(min(t + 1, nt - 1), nxt);
+          asm volatile("" ::: "memory");
+        }
+        const float* hb = hbuf[blk & 1][pw];
+        float ph[16], pc[16];
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) {
+          ph[s2] = hb[c * kHC + n * kHJ + s2];
+          pc[s2] = Cs[buf][(16 * blk + n) * kCStride + s2];
+        }
+        float y4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
+        const float ysum = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+        float o = fmaf(dskip, raw_f32<TU>(cur.uo[blk]), ysum);
+        const float zv = raw_f32<TU>(cur.zo[blk]);
+        const uint32_t off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
+        if constexpr (kPrep) {
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-zv * kLog2e));
+          bstore1<TU>(rs_o, off, raw_f32<TU>(cur.go[blk]) * o * sg * fmaf(zv, 1.0f - sg, 1.0f));
+        } else {
+          if constexpr (kPrez) bstore1<TU>(rs_oz, off, o);
+          bstore1<TU>(rs_o, off, o * silu_fast(zv));
+        }
+      }
+    };
+    for (int t = 0; t < nt; t += 2) {
+      tile_body(t, ra, rb);
+      if (t + 1 < nt) tile_body(t + 1, rb, ra);
+    }
+  }
+}
+
 // Diagonal recurrence over [batch, seqlen, d_inner] fp32, one lane per
 // (batch, channel); consecutive lanes read consecutive channels, so every
 // step is a coalesced 256-byte row segment per wave.
@@ -1156,14 +1420,15 @@ void launch_scan(const ScanParams& p, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
   const bool lean = p.z && !p.out_prez && !p.ck && !p.chunk_states;
   const bool train = p.z && p.out_prez && p.ck && !p.chunk_states;
+  // the inference and training forwards: producer / consumer waves
   if (scan_fast_ok<TU, TD, TBC>(p) && lean && p.softplus)
-    mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdLean><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, true, kFwdLean><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && lean)
-    mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdLean><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, false, kFwdLean><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && train && p.softplus)
-    mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdTrain><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, true, kFwdTrain><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && train)
-    mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdTrain><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, false, kFwdTrain><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
     mamba_scan_fast_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p))
@@ -1273,7 +1538,11 @@ void launch_scan_bwd(const ScanParams& p, void* dB, void* dC, float* dA, float* 
                      bool saved_states, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
   if (!saved_states) {  // preparation pass: states every 16 steps and dz
-    if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
+    if (scan_fast_ok<TU, TD, TBC>(p, true) && p.z && p.softplus)
+      mamba_scan_split_kernel<TU, TD, TBC, true, kPrepGated><<<dim3(grid), dim3(512), 0, s>>>(p);
+    else if (scan_fast_ok<TU, TD, TBC>(p, true) && p.z)
+      mamba_scan_split_kernel<TU, TD, TBC, false, kPrepGated><<<dim3(grid), dim3(512), 0, s>>>(p);
+    else if (scan_fast_ok<TU, TD, TBC>(p, true) && p.softplus)
       mamba_scan_fast_kernel<TU, TD, TBC, true, true><<<dim3(grid), dim3(256), 0, s>>>(p);
     else if (scan_fast_ok<TU, TD, TBC>(p, true))
       mamba_scan_fast_kernel<TU, TD, TBC, false, true><<<dim3(grid), dim3(256), 0, s>>>(p);

@@ -275,7 +275,7 @@ def make_case(name):
         launch = lambda s: _lib.selective_scan(s["u"], s["delta"], s["A"], s["B"], s["C"], s["D"],
                                                s["z"], None, s["out"], None, False)
         return Case(name, "C5 Mamba-1 selective scan B4 L4096 D2048 N16", "hbm", C5_BYTES, 4 * 4096,
-                    launch, sets, "mamba_scan_fast_kernel",
+                    launch, sets, "mamba_scan_split_kernel (producer / consumer waves)",
                     valu_cycles=scan_valu_cycles(4, 2048, 16, 4096), valu_model=SCAN_VALU_MODEL)
     if name == "n64":
         # the reference's own mamba-ssm benchmark shape (scripts/bench_external_kernels.py:140)
@@ -311,7 +311,7 @@ def make_case(name):
             s["ddelta"], s["dA"], s["dB"], s["dC"], s["dD"], s["dz"], None, False)
         return Case(name, "C5-shape Mamba-1 selective scan backward B4 L4096 D2048 N16", "hbm",
                     C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel (preparation) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
+                    "mamba_scan_split_kernel (preparation) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
     if name == "c5t":
         # one training step of the scan: the forward keeps its states every 16
         # steps and its pre-gate output, the backward restarts from them
@@ -336,7 +336,7 @@ def make_case(name):
                                     s["dz"], None, False, checkpoints=s["ck"], out_prez=s["prez"])
         return Case(name, "C5-shape Mamba-1 training step (forward keeping its states + backward from them)",
                     "hbm", C5_BYTES + C5B_BYTES, 4 * 4096, launch, sets,
-                    "mamba_scan_fast_kernel (training variant) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
+                    "mamba_scan_split_kernel (training variant) + mamba_scan_bwd_fast_kernel + scan_bwd_bc_sum4_kernel (with the per-batch sums)")
     raise ValueError(name)
 
 
