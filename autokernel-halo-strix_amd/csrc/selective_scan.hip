@@ -832,16 +832,24 @@ mamba_scan_split_kernel(ScanParams p) {
 #pragma unroll
         for (int s = 0; s < 16; ++s) y4[s & 3] = fmaf(ph[s], pc[s], y4[s & 3]);
         const float ysum = (y4[0] + y4[1]) + (y4[2] + y4[3]);
+        // each stored value is rounded to fp32 and then to the storage type, as
+        // the single-role kernel and the reference do: the opaque copies keep
+        // the compiler from fusing the last FMA or product with an fp16
+        // conversion (v_fma_mixlo_f16, one rounding)
         float o = fmaf(dskip, raw_f32<TU>(cur.uo[blk]), ysum);
+        asm("" : "+v"(o));
         const float zv = raw_f32<TU>(cur.zo[blk]);
         const uint32_t off = vo_o1 + ((uint32_t)t * kScanT + 16 * blk) * sizeof(TU);
+        float v;
         if constexpr (kPrep) {
           const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-zv * kLog2e));
-          bstore1<TU>(rs_o, off, raw_f32<TU>(cur.go[blk]) * o * sg * fmaf(zv, 1.0f - sg, 1.0f));
+          v = raw_f32<TU>(cur.go[blk]) * o * sg * fmaf(zv, 1.0f - sg, 1.0f);
         } else {
           if constexpr (kPrez) bstore1<TU>(rs_oz, off, o);
-          bstore1<TU>(rs_o, off, o * silu_fast(zv));
+          v = o * silu_fast(zv);
         }
+        asm("" : "+v"(v));
+        bstore1<TU>(rs_o, off, v);
       }
     };
     for (int t = 0; t < nt; t += 2) {
