@@ -286,6 +286,9 @@ mamba_scan_fwd_kernel(ScanParams p) {
 // checkpoints but no chunk states (the training forward that keeps its
 // states). The run-time tests split the tile loop into basic blocks that the
 // scheduler cannot interleave across (about 8% of the kernel at the C5 shape).
+// For dstate <= 16 the forwards run on mamba_scan_split_kernel (below), which
+// takes the same variants; this kernel is launched with kFwdAny for dstate
+// 17-64 (kRPC > 1) and as the preparation pass without a gate.
 enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 
 // kRPC (forward only): 16-lane rows per channel, for dstate up to 16 * kRPC.
@@ -608,18 +611,21 @@ mamba_scan_fast_kernel(ScanParams p) {
 // output has the same bits.
 //
 // kMode: kFwdLean / kFwdTrain as for mamba_scan_fast_kernel (a gate z is
-// required), or kPrepGated: the backward's preparation pass with a gate
-// (checkpoints by the producers, dz = dout y sigma(z) (1 + z (1 - sigma(z)))
-// by the consumers).
+// required); kFwdAny: any forward, the gate, pre-gate output, checkpoints and
+// chunk states tested at run time (the compiled binding's fwd, which returns
+// the chunk states); or kPrepGated: the backward's preparation pass with a
+// gate (checkpoints by the producers, dz = dout y sigma(z) (1 + z (1 -
+// sigma(z))) by the consumers).
 enum { kPrepGated = 3 };
 
 template <typename TU, typename TD, typename TBC, bool kSoftplus, int kMode>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
 mamba_scan_split_kernel(ScanParams p) {
-  static_assert(kMode == kFwdLean || kMode == kFwdTrain || kMode == kPrepGated, "split modes");
   constexpr bool kPrep = kMode == kPrepGated;
-  constexpr bool kPrez = kMode == kFwdTrain;
-  constexpr bool kSaveCk = kMode != kFwdLean;
+  const bool has_z = kMode != kFwdAny || p.z != nullptr;
+  const bool has_prez = kMode == kFwdTrain || (kMode == kFwdAny && p.out_prez != nullptr);
+  const bool has_ck = kMode == kFwdTrain || kPrep || (kMode == kFwdAny && p.ck != nullptr);
+  float* const xs_out = kMode == kFwdAny ? p.chunk_states : nullptr;
   __shared__ float Bs[2][16 * kBStride];
   __shared__ float Cs[2][kScanT * kCStride];
   __shared__ float hbuf[2][4][4 * kHC];  // [block parity][producer wave][c][j][n]
@@ -664,8 +670,8 @@ mamba_scan_split_kernel(ScanParams p) {
     const uint32_t vo_u4 = (uint32_t)(wc * p.u_ds + 4 * n) * sizeof(TU);
     const uint32_t vo_B = (uint32_t)(sn_c * p.B_ns + 4 * q) * sizeof(TBC);
     // checkpoints [batch, nchunks, dim, dstate]: the batch's slab, the chunk in the scalar offset
-    const Rsrc rs_ck = make_rsrc(kSaveCk ? p.ck + (int64_t)b * p.nchunks * p.dim * p.dstate : p.A,
-                                 kSaveCk ? (uint32_t)((int64_t)p.nchunks * p.dim * p.dstate * 4) : 0u);
+    const Rsrc rs_ck = make_rsrc(has_ck ? p.ck + (int64_t)b * p.nchunks * p.dim * p.dstate : p.A,
+                                 has_ck ? (uint32_t)((int64_t)p.nchunks * p.dim * p.dstate * 4) : 0u);
     const uint32_t vo_ck = (uint32_t)(d * p.dstate + n) * 4u;
     const uint32_t ck_chunk_bytes = (uint32_t)(p.dim * p.dstate * 4);
     struct Regs {
@@ -688,6 +694,7 @@ mamba_scan_split_kernel(ScanParams p) {
     sv = bload4<TBC>(rs_B, vo_B, (uint32_t)min(1, nt - 1) * kScanT * sizeof(TBC));
     __syncthreads();
     float h = 0.0f;
+    float dsum = 0.0f;  // sum of delta' since step 0 (chunk states)
     // Tile t: stage tile t + 1's B (its buffer was last read in tile t - 1,
     // before the barrier that ended it), issue the loads of tile t + 2's B
     // and tile t + 1's delta / u (clamped to the last tile), then the four
@@ -756,11 +763,22 @@ mamba_scan_split_kernel(ScanParams p) {
         for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
         __syncthreads();
       }
-      if (kSaveCk && n_ok) {
+      if (has_ck && n_ok) {
 #pragma unroll
         for (int blk = 0; blk < kScanT / 16; ++blk)
           __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, hck[blk]), rs_ck, (int)vo_ck,
                                                 (int)((uint32_t)((t * kScanT + 16 * blk) / kCk) * ck_chunk_bytes), 0);
+      }
+      if (xs_out) {
+        // the channel's delta' over the tile, then (decay product, state) at
+        // each 2048-step chunk end
+        dsum += row16_sum((dl[0] + dl[1]) + (dl[2] + dl[3]));
+        const int l1 = (t + 1) * kScanT;
+        if ((l1 % kXChunk == 0 || l1 >= p.seqlen) && n_ok) {
+          float* xs = xs_out + ((((int64_t)b * p.dim + d) * p.xchunks + (l1 - 1) / kXChunk) * p.dstate + n) * 2;
+          xs[0] = __builtin_amdgcn_exp2f(a_scaled * dsum);
+          xs[1] = h;
+        }
       }
     };
     for (int t = 0; t < nt; t += 2) {
@@ -771,16 +789,18 @@ mamba_scan_split_kernel(ScanParams p) {
   } else {
     const float dskip = p.D ? p.D[d] : 0.0f;
     const Rsrc rs_u = row_rsrc(p.u, p.u_bs, p.u_ds, sizeof(TU));
-    const Rsrc rs_z = row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU));
+    // without a gate the z loads read u again (valid addresses, unused)
+    const Rsrc rs_z = has_z ? row_rsrc(p.z, p.z_bs, p.z_ds, sizeof(TU)) : rs_u;
+    const int64_t zds = has_z ? p.z_ds : p.u_ds;
     // the forward's output, or the preparation pass's dz
     const Rsrc rs_o = row_rsrc(kPrep ? p.dz : p.out, p.o_bs, p.o_ds, sizeof(TU));
-    const Rsrc rs_oz = kPrez ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
+    const Rsrc rs_oz = has_prez ? row_rsrc(p.out_prez, p.o_bs, p.o_ds, sizeof(TU)) : rs_o;
     const Rsrc rs_go = kPrep ? row_rsrc(p.dout, p.go_bs, p.go_ds, sizeof(TU)) : rs_u;
     const uint32_t bc_bytes_C = (uint32_t)(((p.dstate - 1) * p.C_ns + L) * sizeof(TBC));
     const Rsrc rs_C = make_rsrc(static_cast<const TBC*>(p.C) + (int64_t)b * p.C_bs + (int64_t)g * p.C_gs, bc_bytes_C);
     // lane (c, n) forms step 16 blk + n of channel wc
     const uint32_t vo_u1 = (uint32_t)(wc * p.u_ds + n) * sizeof(TU);
-    const uint32_t vo_z1 = (uint32_t)(wc * p.z_ds + n) * sizeof(TU);
+    const uint32_t vo_z1 = (uint32_t)(wc * zds + n) * sizeof(TU);
     const uint32_t vo_o1 = (uint32_t)(wc * p.o_ds + n) * sizeof(TU);
     const uint32_t vo_go1 = kPrep ? (uint32_t)(wc * p.go_ds + n) * sizeof(TU) : 0u;
     const uint32_t vo_C = (uint32_t)(sn_c * p.C_ns + 4 * q) * sizeof(TBC);
@@ -845,8 +865,8 @@ mamba_scan_split_kernel(ScanParams p) {
           const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-zv * kLog2e));
           v = raw_f32<TU>(cur.go[blk]) * o * sg * fmaf(zv, 1.0f - sg, 1.0f);
         } else {
-          if constexpr (kPrez) bstore1<TU>(rs_oz, off, o);
-          v = o * silu_fast(zv);
+          if (has_prez) bstore1<TU>(rs_oz, off, o);
+          v = has_z ? o * silu_fast(zv) : o;
         }
         asm("" : "+v"(v));
         bstore1<TU>(rs_o, off, v);
@@ -1428,7 +1448,8 @@ void launch_scan(const ScanParams& p, hipStream_t s) {
   const int grid = p.batch * p.ngroups * p.tiles_per_group;
   const bool lean = p.z && !p.out_prez && !p.ck && !p.chunk_states;
   const bool train = p.z && p.out_prez && p.ck && !p.chunk_states;
-  // the inference and training forwards: producer / consumer waves
+  // whole tiles: producer / consumer waves (inference and training variants
+  // fixed at compile time, any other combination of outputs at run time)
   if (scan_fast_ok<TU, TD, TBC>(p) && lean && p.softplus)
     mamba_scan_split_kernel<TU, TD, TBC, true, kFwdLean><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && lean)
@@ -1438,9 +1459,9 @@ void launch_scan(const ScanParams& p, hipStream_t s) {
   else if (scan_fast_ok<TU, TD, TBC>(p) && train)
     mamba_scan_split_kernel<TU, TD, TBC, false, kFwdTrain><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p) && p.softplus)
-    mamba_scan_fast_kernel<TU, TD, TBC, true><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, true, kFwdAny><<<dim3(grid), dim3(512), 0, s>>>(p);
   else if (scan_fast_ok<TU, TD, TBC>(p))
-    mamba_scan_fast_kernel<TU, TD, TBC, false><<<dim3(grid), dim3(256), 0, s>>>(p);
+    mamba_scan_split_kernel<TU, TD, TBC, false, kFwdAny><<<dim3(grid), dim3(512), 0, s>>>(p);
   else
     mamba_scan_fwd_kernel<TU, TD, TBC><<<dim3(grid), dim3(256), 0, s>>>(p);
 }

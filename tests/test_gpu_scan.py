@@ -127,20 +127,22 @@ def test_fast_and_generic_paths_agree():
 
 @pytest.mark.parametrize("itype,softplus,groups", [("bfloat16", False, 1), ("float32", True, 2),
                                                     ("float16", True, 1)])
-def test_split_and_single_role_forwards_agree_bitwise(itype, softplus, groups):
-    """The producer / consumer forward (taken for the inference call, a gate
-    only, and the training call, gate + pre-gate output + checkpoints) and the
-    single-role whole-tile kernel (taken when chunk states are also asked for,
-    or a pre-gate output without checkpoints) run the same arithmetic in the
-    same order: every output has the same bits."""
+def test_forward_variants_agree_bitwise(itype, softplus, groups):
+    """The whole-tile forward is compiled in variants that fix its optional
+    outputs: inference (a gate only), training (gate, pre-gate output and
+    checkpoints), and a general one that tests them at run time (taken when
+    chunk states are asked for, as the compiled binding's fwd does, or for a
+    pre-gate output without checkpoints). They run the same arithmetic in the
+    same order: every output has the same bits, fp16 outputs included (each
+    value is rounded to fp32 before its storage type, as in the reference)."""
     need_gpu()
     from kernels.hip import _lib
     batch, dim, dstate, seqlen = 2, 64, 16, 512
     u, delta, A, B, C, D, z, bias = (t.to(DEV) for t in
                                      _inputs(batch, dim, dstate, seqlen, groups, ITYPES[itype], 41))
-    say("mamba split vs single-role forward", itype, softplus, groups)
+    say("mamba forward variants", itype, softplus, groups)
 
-    def run(prez=False, ck=False, xs=False):
+    def run(prez=False, ck=False, xs=False, gate=True):
         r = {"out": torch.empty_like(u), "last": torch.empty(batch, dim, dstate, device=DEV)}
         if prez:
             r["prez"] = torch.empty_like(u)
@@ -148,23 +150,28 @@ def test_split_and_single_role_forwards_agree_bitwise(itype, softplus, groups):
             r["ck"] = torch.empty(batch, seqlen // 16, dim, dstate, device=DEV)
         if xs:
             r["xs"] = torch.empty(batch, dim, (seqlen + 2047) // 2048, dstate, 2, device=DEV)
-        _lib.selective_scan(u, delta, A, B, C, D, z, bias, r["out"], r["last"], softplus,
+        _lib.selective_scan(u, delta, A, B, C, D, z if gate else None, bias, r["out"], r["last"], softplus,
                             out_prez=r.get("prez"), chunk_states=r.get("xs"), checkpoints=r.get("ck"))
         return r
 
     lean, train = run(), run(prez=True, ck=True)
-    single, single_prez = run(prez=True, ck=True, xs=True), run(prez=True)
+    general, general_prez = run(prez=True, ck=True, xs=True), run(prez=True)
+    ungated = run(prez=True, xs=True, gate=False)
     torch.cuda.synchronize()
     for k in ("out", "last"):
-        assert torch.equal(lean[k], single[k]), k
-        assert torch.equal(train[k], single[k]), k
+        assert torch.equal(lean[k], general[k]), k
+        assert torch.equal(train[k], general[k]), k
     for k in ("prez", "ck"):
-        assert torch.equal(train[k], single[k]), k
-    assert torch.equal(single_prez["prez"], single["prez"])
-    ref, _ = c_oracle.selective_scan(u.cpu(), delta.cpu(), A.cpu(), B.cpu(), C.cpu(), D.cpu(), z.cpu(),
-                                     bias.cpu(), softplus)
+        assert torch.equal(train[k], general[k]), k
+    assert torch.equal(general_prez["prez"], general["prez"])
+    # without a gate the output is the pre-gate output, and the states are the gated call's
+    assert torch.equal(ungated["out"], general["prez"]) and torch.equal(ungated["prez"], general["prez"])
+    assert torch.equal(ungated["xs"], general["xs"]) and torch.equal(ungated["last"], general["last"])
+    ref, rlast = c_oracle.selective_scan(u.cpu(), delta.cpu(), A.cpu(), B.cpu(), C.cpu(), D.cpu(), z.cpu(),
+                                         bias.cpu(), softplus)
     rtol, atol = GRID["tolerances"][itype]
     assert torch.allclose(lean["out"].cpu().float(), ref, rtol=rtol, atol=atol)
+    assert torch.allclose(lean["last"].cpu(), rlast, rtol=1e-4, atol=1e-4)
 
 
 def test_c5_full_size():
