@@ -300,7 +300,7 @@ enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 // still fit in a CU's LDS.
 template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false,
           int kVar = kFwdAny, int kRPC = 1>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRPC == 4 && sizeof(TBC) == 2 ? 3 : 1)))
 mamba_scan_fast_kernel(ScanParams p) {
   static_assert(!(kPrep && kVar != kFwdAny), "the fixed variants are forwards");
   static_assert(kRPC == 1 || kRPC == 2 || kRPC == 4, "1, 2 or 4 rows per channel");
@@ -315,8 +315,19 @@ mamba_scan_fast_kernel(ScanParams p) {
   float* const ck_out = kVar == kFwdLean ? nullptr : p.ck;
   const bool has_ck = kPrep || kVar == kFwdTrain || (kVar == kFwdAny && ck_out != nullptr);
   float* const xs_out = kVar != kFwdAny ? nullptr : p.chunk_states;
-  __shared__ float Bs[kNB][kNS * kBStride];
-  __shared__ float Cs[kNB][kScanT * kCSt];
+  // 4 rows per channel with 16-bit B / C (the reference's N = 64 benchmark
+  // shape): B and C are staged at their storage width and each lane reads its
+  // B values per 16-step block, so the kernel fits 3 waves per SIMD (159
+  // VGPRs, 40 KB of LDS) instead of 2 (209, 56 KB); every value is converted
+  // exactly, so the outputs keep their bits. At 2 rows per channel it costs
+  // more conversion work than the occupancy returns, so it is not used there.
+  constexpr bool kH16 = kRPC == 4 && sizeof(TBC) == 2;
+  constexpr int kB16P = kScanT + 8;  // halves per state row (144 bytes)
+  constexpr int kC16P = kNS + 8;     // halves per step row
+  __shared__ __align__(16) float Bs[kNB][kH16 ? 1 : kNS * kBStride];
+  __shared__ __align__(16) float Cs[kNB][kH16 ? 1 : kScanT * kCSt];
+  __shared__ __align__(16) uint16_t Bh[kH16 ? kNS * kB16P : 8];
+  __shared__ __align__(16) uint16_t Ch[kH16 ? kScanT * kC16P : 8];
   __shared__ float hbuf[4][4 * kHC];
 
   const int tid = threadIdx.x;
@@ -419,10 +430,20 @@ mamba_scan_fast_kernel(ScanParams p) {
     for (int kk = 0; kk < kRPC; ++kk) {
       const int st = sn + 16 * kk;
       const bool ok = st < p.dstate;
+      if constexpr (kH16) {
+        const u32x2 bw = (u32x2)s.bv[kk];
+        *reinterpret_cast<u32x2*>(&Bh[st * kB16P + 4 * q]) = ok ? bw : (u32x2){0u, 0u};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        Bs[buf][st * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(s.bv[kk], k) : 0.0f;
-        Cs[buf][(4 * q + k) * kCSt + st] = ok ? raw4_f32<TBC>(s.cv[kk], k) : 0.0f;
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t w = s.cv[kk][k >> 1];
+          Ch[(4 * q + k) * kC16P + st] = ok ? (uint16_t)((k & 1) ? (w >> 16) : (w & 0xFFFFu)) : (uint16_t)0;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          Bs[buf][st * kBStride + 4 * q + k] = ok ? raw4_f32<TBC>(s.bv[kk], k) : 0.0f;
+          Cs[buf][(4 * q + k) * kCSt + st] = ok ? raw4_f32<TBC>(s.cv[kk], k) : 0.0f;
+        }
       }
     }
   };
@@ -472,13 +493,31 @@ mamba_scan_fast_kernel(ScanParams p) {
                  : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
                    "+v"(du[2]), "+v"(du[3]));
     const int bb = kNB == 2 ? buf : 0;
-    float bt[kScanT];
+    constexpr bool kBBlk = kH16;  // B read per 16-step block
+    float bt[kBBlk ? 16 : kScanT];
+    if constexpr (!kBBlk) {
 #pragma unroll
-    for (int l = 0; l < kScanT; ++l) bt[l] = Bs[bb][ns * kBStride + l];
+      for (int l = 0; l < kScanT; ++l) bt[l] = Bs[bb][ns * kBStride + l];
+    }
 
 #pragma unroll
     for (int blk = 0; blk < kScanT / 16; ++blk) {
       hck[blk] = h;
+      if constexpr (kBBlk) {
+        if constexpr (kH16) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(&Bh[ns * kB16P + 16 * blk]);
+          const u32x4 w0 = src[0], w1 = src[1];
+#pragma unroll
+          for (int l = 0; l < 8; ++l) {
+            const uint32_t w = l < 4 ? w0[l] : w1[l - 4];
+            bt[2 * l] = raw_f32<TBC>((uint16_t)(w & 0xFFFFu));
+            bt[2 * l + 1] = raw_f32<TBC>((uint16_t)(w >> 16));
+          }
+        } else {
+#pragma unroll
+          for (int l = 0; l < 16; ++l) bt[l] = Bs[bb][ns * kBStride + 16 * blk + l];
+        }
+      }
       float hv[16], av[16], xv[16];
       auto steps4 = [&](auto src_c, int j4) {
         constexpr int kSrc = decltype(src_c)::value;
@@ -486,7 +525,7 @@ mamba_scan_fast_kernel(ScanParams p) {
         for (int k = 0; k < 4; ++k) av[4 * j4 + k] = mul_bcast<kSrc>(dl[k], a_scaled);
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          xv[4 * j4 + k] = mul_bcast<kSrc>(du[k], bt[16 * blk + 4 * j4 + k]);
+          xv[4 * j4 + k] = mul_bcast<kSrc>(du[k], bt[(kBBlk ? 0 : 16 * blk) + 4 * j4 + k]);
       };
       switch (blk) {
         case 0:
@@ -520,9 +559,19 @@ mamba_scan_fast_kernel(ScanParams p) {
       for (int j = 0; j < 16; ++j) hb[c * kHC + j * kHJ + n] = hv[j];
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int s2 = 0; s2 < 16; ++s2) {
-        ph[s2] = hb[c * kHC + n * kHJ + s2];
-        pc[s2] = Cs[bb][(16 * blk + n) * kCSt + 16 * sr + s2];
+      for (int s2 = 0; s2 < 16; ++s2) ph[s2] = hb[c * kHC + n * kHJ + s2];
+      if constexpr (kH16) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(&Ch[(16 * blk + n) * kC16P + 16 * sr]);
+        const u32x4 w0 = src[0], w1 = src[1];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const uint32_t w = l < 4 ? w0[l] : w1[l - 4];
+          pc[2 * l] = raw_f32<TBC>((uint16_t)(w & 0xFFFFu));
+          pc[2 * l + 1] = raw_f32<TBC>((uint16_t)(w >> 16));
+        }
+      } else {
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2) pc[s2] = Cs[bb][(16 * blk + n) * kCSt + 16 * sr + s2];
       }
       __builtin_amdgcn_wave_barrier();
       p_uo = raw_f32<TU>(cur.uo[blk]);
