@@ -279,16 +279,20 @@ mamba_scan_fwd_kernel(ScanParams p) {
 // * softplus chosen at compile time (as a run-time branch the compiler
 //   if-converts it and evaluates log1p(exp(x)) on every tile).
 // ---------------------------------------------------------------------------
-// kPrep: the backward's preparation pass (as in mamba_scan_fwd_kernel).
-// kVar (forward only) fixes the optional outputs at compile time: kFwdAny
-// tests the pointers at run time; kFwdLean has a gate z and none of out_prez,
+// kPrep: the backward's preparation pass (as in mamba_scan_fwd_kernel). The
+// forward's optional outputs (gate, pre-gate output, checkpoints, chunk
+// states) are tested at run time. For dstate <= 16 the forwards run on
+// mamba_scan_split_kernel (below), which also has variants with those outputs
+// fixed at compile time (the run-time tests split the tile loop into basic
+// blocks that the scheduler cannot interleave across: about 8% of the kernel
+// at the C5 shape); this kernel is launched for dstate 17-64 (kRPC > 1) and as
+// the preparation pass without a gate.
+//
+// The forward variants of mamba_scan_split_kernel: kFwdAny tests the outputs'
+// pointers at run time; kFwdLean has a gate z and none of out_prez,
 // checkpoints or chunk states (inference); kFwdTrain has a gate, out_prez and
 // checkpoints but no chunk states (the training forward that keeps its
-// states). The run-time tests split the tile loop into basic blocks that the
-// scheduler cannot interleave across (about 8% of the kernel at the C5 shape).
-// For dstate <= 16 the forwards run on mamba_scan_split_kernel (below), which
-// takes the same variants; this kernel is launched with kFwdAny for dstate
-// 17-64 (kRPC > 1) and as the preparation pass without a gate.
+// states).
 enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 
 // kRPC (forward only): 16-lane rows per channel, for dstate up to 16 * kRPC.
@@ -298,11 +302,9 @@ enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 // swaps. A workgroup then holds 16 / kRPC channels, and the larger B / C
 // staging is single-buffered (two barriers per tile) so that two workgroups
 // still fit in a CU's LDS.
-template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false,
-          int kVar = kFwdAny, int kRPC = 1>
+template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false, int kRPC = 1>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRPC == 4 && sizeof(TBC) == 2 ? 3 : 1)))
 mamba_scan_fast_kernel(ScanParams p) {
-  static_assert(!(kPrep && kVar != kFwdAny), "the fixed variants are forwards");
   static_assert(kRPC == 1 || kRPC == 2 || kRPC == 4, "1, 2 or 4 rows per channel");
   static_assert(!(kPrep && kRPC != 1), "the preparation pass has 16 states");
   constexpr int kNS = 16 * kRPC;                         // state slots per channel
@@ -310,11 +312,11 @@ mamba_scan_fast_kernel(ScanParams p) {
   constexpr int kWGC = 16 / kRPC;                        // channels per workgroup
   constexpr int kCSt = kRPC == 1 ? kCStride : kNS + 4;   // Cs step pitch (floats)
   constexpr int kNB = kRPC == 1 ? 2 : 1;                 // staging buffers
-  const bool has_z = kVar != kFwdAny || p.z != nullptr;
-  const bool has_prez = kVar == kFwdTrain || (kVar == kFwdAny && !kPrep && p.out_prez != nullptr);
-  float* const ck_out = kVar == kFwdLean ? nullptr : p.ck;
-  const bool has_ck = kPrep || kVar == kFwdTrain || (kVar == kFwdAny && ck_out != nullptr);
-  float* const xs_out = kVar != kFwdAny ? nullptr : p.chunk_states;
+  const bool has_z = p.z != nullptr;
+  const bool has_prez = !kPrep && p.out_prez != nullptr;
+  float* const ck_out = p.ck;
+  const bool has_ck = kPrep || ck_out != nullptr;
+  float* const xs_out = p.chunk_states;
   // 4 rows per channel with 16-bit B / C (the reference's N = 64 benchmark
   // shape): B and C are staged at their storage width and each lane reads its
   // B values per 16-step block, so the kernel fits 3 waves per SIMD (159
@@ -1528,11 +1530,11 @@ bool launch_scan_rows(const ScanParams& p, hipStream_t s) {
   q.tiles_per_group = p.ch_per_group / wgc;
   const int grid = q.batch * q.ngroups * q.tiles_per_group;
   if (rpc == 2) {
-    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdAny, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
-    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdAny, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
+    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
+    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, 2><<<dim3(grid), dim3(256), 0, s>>>(q);
   } else {
-    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, kFwdAny, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
-    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, kFwdAny, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
+    if (p.softplus) mamba_scan_fast_kernel<TU, TD, TBC, true, false, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
+    else mamba_scan_fast_kernel<TU, TD, TBC, false, false, 4><<<dim3(grid), dim3(256), 0, s>>>(q);
   }
   return true;
 }
