@@ -303,7 +303,7 @@ enum { kFwdAny = 0, kFwdLean = 1, kFwdTrain = 2 };
 // staging is single-buffered (two barriers per tile) so that two workgroups
 // still fit in a CU's LDS.
 template <typename TU, typename TD, typename TBC, bool kSoftplus, bool kPrep = false, int kRPC = 1>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kRPC == 4 && sizeof(TBC) == 2 ? 3 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((kRPC == 4 && sizeof(TBC) == 2) || kRPC == 2 ? 3 : 1)))
 mamba_scan_fast_kernel(ScanParams p) {
   static_assert(kRPC == 1 || kRPC == 2 || kRPC == 4, "1, 2 or 4 rows per channel");
   static_assert(!(kPrep && kRPC != 1), "the preparation pass has 16 states");
@@ -321,8 +321,10 @@ mamba_scan_fast_kernel(ScanParams p) {
   // shape): B and C are staged at their storage width and each lane reads its
   // B values per 16-step block, so the kernel fits 3 waves per SIMD (159
   // VGPRs, 40 KB of LDS) instead of 2 (209, 56 KB); every value is converted
-  // exactly, so the outputs keep their bits. At 2 rows per channel it costs
-  // more conversion work than the occupancy returns, so it is not used there.
+  // exactly, so the outputs keep their bits. At 2 rows per channel the fp32
+  // staging already fits (39 KB) and the per-block B reads alone bring the
+  // kernel to 3 waves per SIMD (150 VGPRs instead of 195); the 16-bit staging
+  // would only add conversion work there.
   constexpr bool kH16 = kRPC == 4 && sizeof(TBC) == 2;
   constexpr int kB16P = kScanT + 8;  // halves per state row (144 bytes)
   constexpr int kC16P = kNS + 8;     // halves per step row
@@ -495,7 +497,7 @@ mamba_scan_fast_kernel(ScanParams p) {
                  : "+v"(dl[0]), "+v"(dl[1]), "+v"(dl[2]), "+v"(dl[3]), "+v"(du[0]), "+v"(du[1]),
                    "+v"(du[2]), "+v"(du[3]));
     const int bb = kNB == 2 ? buf : 0;
-    constexpr bool kBBlk = kH16;  // B read per 16-step block
+    constexpr bool kBBlk = kH16 || kRPC == 2;  // B read per 16-step block
     float bt[kBBlk ? 16 : kScanT];
     if constexpr (!kBBlk) {
 #pragma unroll
