@@ -79,11 +79,34 @@ struct Cx {
 __device__ __forceinline__ Cx cmul(Cx a, Cx b) { return {a.r * b.r - a.i * b.i, a.r * b.i + a.i * b.r}; }
 __device__ __forceinline__ Cx cconj(Cx a) { return {a.r, -a.i}; }
 
-// exp(dl * A) for A = (ar, ai), ar pre-scaled by log2 e
+// sin and cos of x radians on the hardware's transcendental units
+// (v_sin_f32 / v_cos_f32 take revolutions): x / 2 pi is reduced to [-1/2,
+// 1/2] revolutions by subtracting its nearest integer, so the phase error
+// grows with |x| (the rounding of x / 2 pi: about 6e-8 |x| radians). The
+// reference builds its scan with fast math, so its __builtin_sincosf is a
+// hardware approximation as well.
+__device__ __forceinline__ void sincos_hw(float x, float* s, float* c) {
+  float r = x * 0.15915494309189535f;  // 1 / (2 pi)
+  r -= __builtin_rintf(r);
+  *s = __builtin_amdgcn_sinf(r);
+  *c = __builtin_amdgcn_cosf(r);
+}
+
+// exp(dl * A) for A = (ar, ai), ar pre-scaled by log2 e: the per-step decay
+// factor, with the hardware phase
 __device__ __forceinline__ Cx cexp_step(float dl, float ar2, float ai) {
   const float mag = __builtin_amdgcn_exp2f(dl * ar2);
   float sn, cs;
-  sincosf(dl * ai, &sn, &cs);
+  sincos_hw(dl * ai, &sn, &cs);
+  return {mag * cs, mag * sn};
+}
+
+// exp(dsum * A) for a chunk state's decay product: once per 2048-step chunk,
+// where the phase dsum Im A can be large, so the accurate sincosf
+__device__ __forceinline__ Cx cexp_chunk(float dsum, float ar2, float ai) {
+  const float mag = __builtin_amdgcn_exp2f(dsum * ar2);
+  float sn, cs;
+  sincosf(dsum * ai, &sn, &cs);
   return {mag * cs, mag * sn};
 }
 
@@ -240,7 +263,7 @@ __global__ void __launch_bounds__(256) mamba_scan_complex_fwd_kernel(ScanParams 
       for (int i = 0; i < KS; ++i) {
         const int s = sl + LPC * i;
         if (s < p.dstate) {
-          const Cx pr = cexp_step(dsum, ar2[i], ai[i]);
+          const Cx pr = cexp_chunk(dsum, ar2[i], ai[i]);
           float* q = p.chunk_states + 4 * ((((int64_t)b * p.dim + d) * p.xchunks + k) * p.dstate + s);
           q[0] = pr.r;
           q[1] = pr.i;
