@@ -174,6 +174,48 @@ def test_forward_variants_agree_bitwise(itype, softplus, groups):
     assert torch.allclose(lean["last"].cpu(), rlast, rtol=1e-4, atol=1e-4)
 
 
+def test_whole_tile_forward_random_shapes():
+    """Seeded random whole-tile shapes (seqlen a multiple of 64, channels per
+    group a multiple of 16, dstate 1-16) with random dtypes and options,
+    through the C-ABI: out and last_state against the C oracle at the
+    reference grid's tolerances, and the inference / training / general
+    variants of the producer / consumer forward bitwise equal to each other."""
+    need_gpu()
+    from kernels.hip import _lib
+    rng = torch.Generator().manual_seed(2024)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=rng))]
+    for case in range(10):
+        groups = pick([1, 1, 2, 4])
+        batch, dim = pick([1, 2, 3]), 16 * groups * pick([1, 2, 3])
+        dstate, seqlen = pick([1, 3, 8, 13, 16, 16]), 64 * pick([1, 2, 5, 8])
+        itype = pick(["float32", "float16", "bfloat16"])
+        softplus, use_bias, fp32_delta = pick([True, False]), pick([True, False]), pick([True, False])
+        say("mamba random whole-tile forward", case, batch, dim, dstate, seqlen, groups, itype, softplus,
+            use_bias, fp32_delta)
+        u, delta, A, B, C, D, z, bias = _inputs(batch, dim, dstate, seqlen, groups, ITYPES[itype], 100 + case)
+        if fp32_delta:
+            delta = delta.float()
+        bias = bias if use_bias else None
+        dv = [t if t is None else t.to(DEV) for t in (u, delta, A, B, C, D, z, bias)]
+        outs = []
+        for prez, ck, xs in ((False, False, False), (True, True, False), (True, True, True)):
+            out = torch.empty_like(dv[0])
+            last = torch.empty(batch, dim, dstate, device=DEV)
+            pz = torch.empty_like(dv[0]) if prez else None
+            cks = torch.empty(batch, seqlen // 16, dim, dstate, device=DEV) if ck else None
+            xss = torch.empty(batch, dim, (seqlen + 2047) // 2048, dstate, 2, device=DEV) if xs else None
+            _lib.selective_scan(*dv, out, last, softplus, out_prez=pz, chunk_states=xss, checkpoints=cks)
+            outs.append((out, last, pz, cks))
+        torch.cuda.synchronize()
+        for o in outs[1:]:
+            assert torch.equal(o[0], outs[0][0]) and torch.equal(o[1], outs[0][1]), case
+        assert torch.equal(outs[1][2], outs[2][2]) and torch.equal(outs[1][3], outs[2][3]), case
+        ref, rlast = c_oracle.selective_scan(u, delta, A, B, C, D, z, bias, softplus)
+        rtol, atol = GRID["tolerances"][itype]
+        assert torch.allclose(outs[0][0].cpu().float(), ref, rtol=rtol, atol=atol), case
+        assert torch.allclose(outs[0][1].cpu(), rlast, rtol=1e-3, atol=1e-3), case
+
+
 def test_c5_full_size():
     need_gpu()
     import bench
