@@ -953,6 +953,110 @@ diag_scan_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
   }
 }
 
+// The same recurrence in chunks of lc steps, for shapes whose (batch, channel)
+// lanes are too few to keep the GPU busy (AMADEUS: 384 channels; the
+// sequential kernel above then runs at about 6% of HBM bandwidth). Three
+// launches, lanes (batch, chunk, channel) with channels coalesced, and the
+// output buffer as the only scratch:
+//   1. every chunk but the last: its decay product P = prod dA and its state
+//      from zero S, stored in the first two rows of the chunk in y;
+//   2. per (batch, channel), sequentially over the chunks: the state entering
+//      chunk k, s_k = P_{k-1} s_{k-1} + S_{k-1}, stored over P_k (the row a
+//      chunk's own lane reads before writing anything);
+//   3. every chunk from its entering state: s = dA s + dBx, y = C s + D x.
+// 8 bytes per element more than the sequential pass (dA and dBx read twice);
+// the states differ from the sequential ones by rounding only. Chunks: enough
+// for about 2^17 lanes, at most 64, at least 16 steps each.
+__global__ void __launch_bounds__(256)
+diag_scan_chunk_agg_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                           float* __restrict__ y, int batch, int seqlen, int d_inner, int lc,
+                           int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)(nchunks - 1) * d_inner;
+  if (gid >= (int64_t)batch * per_b) return;
+  const int b = (int)(gid / per_b);
+  const int k = (int)((gid % per_b) / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int64_t row0 = (int64_t)b * seqlen + (int64_t)k * lc;
+  int64_t idx = row0 * d_inner + d;
+  float P = 1.0f, S = 0.0f;
+#pragma unroll 8
+  for (int t = 0; t < lc; ++t, idx += d_inner) {
+    const float a = dA[idx];
+    S = fmaf(a, S, dBx[idx]);
+    P *= a;
+  }
+  y[row0 * d_inner + d] = P;
+  y[(row0 + 1) * d_inner + d] = S;
+}
+
+__global__ void __launch_bounds__(256)
+diag_scan_chunk_carry_kernel(float* __restrict__ y, float* __restrict__ also, int batch, int seqlen,
+                             int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)batch * d_inner) return;
+  const int b = (int)(gid / d_inner);
+  const int d = (int)(gid % d_inner);
+  // the aggregates of up to 16 chunks are loaded before any of their rows is
+  // overwritten, so the loads do not wait on the chain
+  constexpr int kG = 16;
+  float s = 0.0f;
+  const int64_t base = (int64_t)b * seqlen * d_inner + d;
+  const int64_t chunk_stride = (int64_t)lc * d_inner;
+  for (int k0 = 0; k0 + 1 < nchunks; k0 += kG) {
+    float P[kG], S[kG];
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      const int k = min(k0 + i, nchunks - 2);
+      P[i] = y[base + k * chunk_stride];
+      S[i] = y[base + k * chunk_stride + d_inner];
+    }
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      if (k0 + i + 1 < nchunks) {
+        y[base + (k0 + i) * chunk_stride] = s;  // the state entering chunk k0 + i
+        if (also) also[base + (k0 + i) * chunk_stride] = s;
+        s = fmaf(P[i], s, S[i]);
+      }
+    }
+  }
+  y[base + (int64_t)(nchunks - 1) * chunk_stride] = s;
+  if (also) also[base + (int64_t)(nchunks - 1) * chunk_stride] = s;
+}
+
+// Chunks for the diagonal scan: enough for about 2^17 lanes in all, at most
+// 64, at least 16 steps each; 1 means the sequential kernels.
+inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner) {
+  const int64_t lanes = batch * d_inner;
+  const int64_t want = ((int64_t)1 << 17);
+  int64_t nchunks = lanes >= want ? 1 : (want + lanes - 1) / lanes;
+  nchunks = std::min<int64_t>(std::min<int64_t>(nchunks, 64), seqlen / 16);
+  return (int)std::max<int64_t>(nchunks, 1);
+}
+
+__global__ void __launch_bounds__(256)
+diag_scan_chunk_out_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                           const float* __restrict__ C, const float* __restrict__ D,
+                           const float* __restrict__ x, float* __restrict__ y, int batch,
+                           int seqlen, int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)nchunks * d_inner;
+  if (gid >= (int64_t)batch * per_b) return;
+  const int b = (int)(gid / per_b);
+  const int k = (int)((gid % per_b) / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int t0 = k * lc;
+  const int n = min(lc, seqlen - t0);
+  int64_t idx = ((int64_t)b * seqlen + t0) * d_inner + d;
+  float s = y[idx];  // the entering state, read before this lane writes its rows
+  const float dd = D[d];
+#pragma unroll 8
+  for (int t = 0; t < n; ++t, idx += d_inner) {
+    s = fmaf(dA[idx], s, dBx[idx]);
+    y[idx] = fmaf(C[idx], s, dd * x[idx]);
+  }
+}
+
 // Backward of the diagonal recurrence (the gradient of the reference's
 // sequential formula, kernels/hip/_torch_ops.py:346-386, and of its HIP
 // kernel kernels/hip/selective_scan_backward.py:72-311), one lane per
@@ -1056,6 +1160,189 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
   float s = 0.0f;
   for (int b = 0; b < batch; ++b) s += gD_part[(int64_t)b * d_inner + d];
   grad_D[d] = s;
+}
+
+// The backward in chunks (the same plan as the chunked forward, lanes
+// (batch, chunk, channel), the gradient buffers as scratch), for shapes whose
+// (batch, channel) lanes are too few for the GPU:
+//   1. forward aggregates (P, S) of every chunk but the last in grad_C;
+//   2. per (batch, channel): the forward state entering each chunk, kept in
+//      the chunk's first grad_dBx row;
+//   3. every chunk: its states, into grad_C;
+//   4. reverse aggregates of every chunk but the first: with the carried
+//      adjoint c (c = g_t dA_t passes step t's gradient to step t - 1, and
+//      g_t = gy_t C_t + c), the chunk's product Q of dA (in grad_dA) and its
+//      carried value G leaving the chunk from c = 0 (in grad_x);
+//   5. per (batch, channel), from the last chunk back: the carried adjoint
+//      entering each chunk, c_k = Q_{k+1} c_{k+1} + G_{k+1}, over Q;
+//   6. every chunk backward in time from its entering adjoint, as the
+//      sequential kernel does, writing every gradient; its first step reads
+//      the previous chunk's last state from the kept entering state, and the
+//      chunk's sum of gy x goes to its first grad_x row;
+//   7. per (batch, channel): the chunks' partials summed in chunk order (into
+//      the grad_D workspace) and grad_x restored in those rows; then grad_D
+//      as the sum over the batch, in order.
+// Every chunk but the last is full, so (P, S) fit its first two rows; each
+// lane reads its chunk's scratch rows before it writes them.
+__global__ void __launch_bounds__(256)
+diag_bwd_fwd_states_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                           const float* __restrict__ s_in, float* __restrict__ st, int batch,
+                           int seqlen, int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)nchunks * d_inner;
+  if (gid >= (int64_t)batch * per_b) return;
+  const int b = (int)(gid / per_b);
+  const int k = (int)((gid % per_b) / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int t0 = k * lc;
+  const int n = min(lc, seqlen - t0);
+  int64_t idx = ((int64_t)b * seqlen + t0) * d_inner + d;
+  float s = s_in[idx];
+#pragma unroll 8
+  for (int t = 0; t < n; ++t, idx += d_inner) {
+    s = fmaf(dA[idx], s, dBx[idx]);
+    st[idx] = s;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+diag_bwd_rev_agg_kernel(const float* __restrict__ dA, const float* __restrict__ C,
+                        const float* __restrict__ gy, float* __restrict__ q_out,
+                        float* __restrict__ g_out, int batch, int seqlen, int d_inner, int lc,
+                        int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)(nchunks - 1) * d_inner;
+  if (gid >= (int64_t)batch * per_b) return;
+  const int b = (int)(gid / per_b);
+  const int k = 1 + (int)((gid % per_b) / d_inner);  // chunks 1 .. nchunks - 1
+  const int d = (int)(gid % d_inner);
+  const int t0 = k * lc;
+  const int n = min(lc, seqlen - t0);
+  const int64_t first = ((int64_t)b * seqlen + t0) * d_inner + d;
+  int64_t idx = first + (int64_t)(n - 1) * d_inner;
+  float c = 0.0f, Q = 1.0f;
+#pragma unroll 8
+  for (int t = n - 1; t >= 0; --t, idx -= d_inner) {
+    const float a = dA[idx];
+    const float g = fmaf(gy[idx], C[idx], c);
+    c = g * a;
+    Q *= a;
+  }
+  q_out[first] = Q;
+  g_out[first] = c;
+}
+
+__global__ void __launch_bounds__(256)
+diag_bwd_rev_carry_kernel(float* __restrict__ q_c, const float* __restrict__ g_agg, int batch,
+                          int seqlen, int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)batch * d_inner) return;
+  const int b = (int)(gid / d_inner);
+  const int d = (int)(gid % d_inner);
+  constexpr int kG = 16;
+  const int64_t base = (int64_t)b * seqlen * d_inner + d;
+  const int64_t chunk_stride = (int64_t)lc * d_inner;
+  float c = 0.0f;  // entering the last chunk
+  // chunks nchunks - 1 down to 1: up to 16 aggregates loaded before their rows are overwritten
+  for (int k0 = nchunks - 1; k0 >= 1; k0 -= kG) {
+    float Q[kG], G[kG];
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      const int k = max(k0 - i, 1);
+      Q[i] = q_c[base + k * chunk_stride];
+      G[i] = g_agg[base + k * chunk_stride];
+    }
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      if (k0 - i >= 1) {
+        q_c[base + (k0 - i) * chunk_stride] = c;  // the adjoint carried into chunk k0 - i
+        c = fmaf(Q[i], c, G[i]);
+      }
+    }
+  }
+  q_c[base] = c;  // into chunk 0
+}
+
+__global__ void __launch_bounds__(256)
+diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ C,
+                      const float* __restrict__ D, const float* __restrict__ x,
+                      const float* __restrict__ gy, float* __restrict__ g_dA,
+                      float* __restrict__ g_dBx, float* g_C, float* __restrict__ g_x, int batch,
+                      int seqlen, int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_b = (int64_t)nchunks * d_inner;
+  if (gid >= (int64_t)batch * per_b) return;
+  const int b = (int)(gid / per_b);
+  const int k = (int)((gid % per_b) / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int t0 = k * lc;
+  const int n = min(lc, seqlen - t0);
+  const int64_t D_ = d_inner;
+  const int64_t first = ((int64_t)b * seqlen + t0) * D_ + d;
+  float c = g_dA[first];               // the adjoint carried into the chunk
+  const float s_prev0 = g_dBx[first];  // the state before the chunk
+  const float dd = D[d];
+  float gd = 0.0f;
+  // steps t .. t - 7 (chunk-relative) loaded before any of their rows is
+  // written: grad_C holds the states and is overwritten with gy * state, so
+  // the loads cannot move past the stores otherwise
+  auto step = [&](int t, float a, float cv, float yv, float xv, float st_t, float st_p) {
+    const int64_t i = first + (int64_t)t * D_;
+    g_C[i] = yv * st_t;
+    const float g = fmaf(yv, cv, c);
+    g_dA[i] = g * st_p;
+    g_dBx[i] = g;
+    c = g * a;
+    if (t > 0) g_x[i] = yv * dd;
+    gd = fmaf(yv, xv, gd);
+  };
+  int t = n - 1;
+  for (; t - kDiagU + 1 >= 0; t -= kDiagU) {
+    float a[kDiagU], cv[kDiagU], yv[kDiagU], xv[kDiagU], st[kDiagU + 1];
+#pragma unroll
+    for (int j = 0; j < kDiagU; ++j) {
+      const int64_t i = first + (int64_t)(t - j) * D_;
+      a[j] = dA[i];
+      cv[j] = C[i];
+      yv[j] = gy[i];
+      xv[j] = x[i];
+      st[j] = g_C[i];
+    }
+    st[kDiagU] = t - kDiagU >= 0 ? g_C[first + (int64_t)(t - kDiagU) * D_] : s_prev0;
+#pragma unroll
+    for (int j = 0; j < kDiagU; ++j) step(t - j, a[j], cv[j], yv[j], xv[j], st[j], st[j + 1]);
+  }
+  for (; t >= 0; --t) {
+    const int64_t i = first + (int64_t)t * D_;
+    const float st_t = g_C[i];
+    const float st_p = t > 0 ? g_C[i - D_] : s_prev0;
+    step(t, dA[i], C[i], gy[i], x[i], st_t, st_p);
+  }
+  g_x[first] = gd;  // the chunk's sum of gy x (the row's gy D is written back by the grad_D pass)
+}
+
+// Per (batch, channel): the sum of the chunks' gy x partials in chunk order
+// (into the grad_D workspace, summed over the batch by diag_scan_gd_kernel),
+// and gy D written back into those grad_x rows.
+__global__ void __launch_bounds__(256)
+diag_bwd_gd_chunks_kernel(const float* __restrict__ gy, const float* __restrict__ D,
+                          float* __restrict__ g_x, float* __restrict__ part, int batch,
+                          int seqlen, int d_inner, int lc, int nchunks) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)batch * d_inner) return;
+  const int b = (int)(gid / d_inner);
+  const int d = (int)(gid % d_inner);
+  const int64_t base = (int64_t)b * seqlen * d_inner + d;
+  const int64_t chunk_stride = (int64_t)lc * d_inner;
+  const float dd = D[d];
+  float s = 0.0f;
+#pragma unroll 8
+  for (int k = 0; k < nchunks; ++k) {
+    const int64_t i = base + k * chunk_stride;
+    s += g_x[i];
+    g_x[i] = gy[i] * dd;
+  }
+  part[gid] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -1770,10 +2057,28 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   if (batch * d_inner > 0x7FFFFFFFll) return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
   if (batch == 0 || seqlen == 0) return AK_OK;
   if (!dA || !dBx || !C || !D || !x || !y) return ak_set_error(AK_ERR_INVALID_ARG, "%s: null pointer", name);
+  if (batch * seqlen * d_inner >= ((int64_t)1 << 62)) return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
   const int64_t lanes = batch * d_inner;
-  const unsigned grid = (unsigned)((lanes + 255) / 256);
-  ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, ak_stream(stream)>>>(dA, dBx, C, D, x, y, (int)batch,
-                                                                      (int)seqlen, (int)d_inner);
+  hipStream_t s = ak_stream(stream);
+  // chunks when (batch, channel) lanes alone leave the GPU idle
+  const int nchunks = ak::diag_chunks(batch, seqlen, d_inner);
+  if (nchunks <= 1) {
+    const unsigned grid = (unsigned)((lanes + 255) / 256);
+    ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch, (int)seqlen,
+                                                         (int)d_inner);
+    return ak_check_launch(name);
+  }
+  const int lc = (int)((seqlen + nchunks - 1) / nchunks);  // >= 16
+  const int nc = (int)((seqlen + lc - 1) / lc);             // every chunk but the last is full
+  const unsigned g1 = (unsigned)((batch * (nc - 1) * d_inner + 255) / 256);
+  const unsigned g2 = (unsigned)((lanes + 255) / 256);
+  const unsigned g3 = (unsigned)((batch * nc * d_inner + 255) / 256);
+  ak::diag_scan_chunk_agg_kernel<<<dim3(g1), dim3(256), 0, s>>>(dA, dBx, y, (int)batch, (int)seqlen,
+                                                               (int)d_inner, lc, nc);
+  ak::diag_scan_chunk_carry_kernel<<<dim3(g2), dim3(256), 0, s>>>(y, nullptr, (int)batch, (int)seqlen,
+                                                                 (int)d_inner, lc, nc);
+  ak::diag_scan_chunk_out_kernel<<<dim3(g3), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch,
+                                                               (int)seqlen, (int)d_inner, lc, nc);
   return ak_check_launch(name);
 }
 
@@ -1806,6 +2111,30 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
                         workspace_bytes, ak_diag_scan_bwd_workspace_bytes(batch, d_inner));
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
+  const int nc = ak::diag_chunks(batch, seqlen, d_inner);
+  if (nc > 1) {
+    const int lc = (int)((seqlen + nc - 1) / nc);
+    const int ncs = (int)((seqlen + lc - 1) / lc);
+    const int B_ = (int)batch, L_ = (int)seqlen, D_ = (int)d_inner;
+    const unsigned g_agg = (unsigned)((batch * (ncs - 1) * d_inner + 255) / 256);
+    const unsigned g_lane = (unsigned)((lanes + 255) / 256);
+    const unsigned g_all = (unsigned)((batch * ncs * d_inner + 255) / 256);
+    ak::diag_scan_chunk_agg_kernel<<<dim3(g_agg), dim3(256), 0, s>>>(dA, dBx, grad_C, B_, L_, D_, lc, ncs);
+    ak::diag_scan_chunk_carry_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_C, grad_dBx, B_, L_, D_, lc,
+                                                                       ncs);
+    ak::diag_bwd_fwd_states_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, grad_dBx, grad_C, B_, L_, D_,
+                                                                    lc, ncs);
+    ak::diag_bwd_rev_agg_kernel<<<dim3(g_agg), dim3(256), 0, s>>>(dA, C, grad_y, grad_dA, grad_x, B_, L_,
+                                                                 D_, lc, ncs);
+    ak::diag_bwd_rev_carry_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_dA, grad_x, B_, L_, D_, lc, ncs);
+    ak::diag_bwd_chunk_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, C, D, x, grad_y, grad_dA, grad_dBx,
+                                                               grad_C, grad_x, B_, L_, D_, lc, ncs);
+    ak::diag_bwd_gd_chunks_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_y, D, grad_x, part, B_, L_, D_,
+                                                                   lc, ncs);
+    ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
+        part, grad_D, B_, D_);
+    return ak_check_launch(name);
+  }
   ak::diag_scan_bwd_kernel<<<dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0, s>>>(
       dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx, grad_C, grad_x, part, (int)batch, (int)seqlen,
       (int)d_inner);
