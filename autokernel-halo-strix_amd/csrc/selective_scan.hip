@@ -965,8 +965,8 @@ diag_scan_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
 //      chunk's own lane reads before writing anything);
 //   3. every chunk from its entering state: s = dA s + dBx, y = C s + D x.
 // 8 bytes per element more than the sequential pass (dA and dBx read twice);
-// the states differ from the sequential ones by rounding only. Chunks: enough
-// for about 2^17 lanes, at most 64, at least 16 steps each.
+// the states differ from the sequential ones by rounding only. Chunks: see
+// diag_chunks.
 __global__ void __launch_bounds__(256)
 diag_scan_chunk_agg_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
                            float* __restrict__ y, int batch, int seqlen, int d_inner, int lc,
@@ -1024,11 +1024,14 @@ diag_scan_chunk_carry_kernel(float* __restrict__ y, float* __restrict__ also, in
   if (also) also[base + (int64_t)(nchunks - 1) * chunk_stride] = s;
 }
 
-// Chunks for the diagonal scan: enough for about 2^17 lanes in all, at most
-// 64, at least 16 steps each; 1 means the sequential kernels.
-inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner) {
+// Chunks for the diagonal scan: enough for about 2^lanes_log2 lanes in all,
+// at most 64, at least 16 steps each; 1 means the sequential kernels. At
+// AMADEUS's shape ([16, 1024, 384]) the forward measured fastest with 2^18
+// lanes (41 against 46 us with 2^17, the same with 2^19) and the backward with
+// 2^17 (124 us, 137 with 2^19).
+inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner, int lanes_log2) {
   const int64_t lanes = batch * d_inner;
-  const int64_t want = ((int64_t)1 << 17);
+  const int64_t want = ((int64_t)1 << lanes_log2);
   int64_t nchunks = lanes >= want ? 1 : (want + lanes - 1) / lanes;
   nchunks = std::min<int64_t>(std::min<int64_t>(nchunks, 64), seqlen / 16);
   return (int)std::max<int64_t>(nchunks, 1);
@@ -2061,7 +2064,7 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const int64_t lanes = batch * d_inner;
   hipStream_t s = ak_stream(stream);
   // chunks when (batch, channel) lanes alone leave the GPU idle
-  const int nchunks = ak::diag_chunks(batch, seqlen, d_inner);
+  const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
   if (nchunks <= 1) {
     const unsigned grid = (unsigned)((lanes + 255) / 256);
     ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch, (int)seqlen,
@@ -2111,7 +2114,7 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
                         workspace_bytes, ak_diag_scan_bwd_workspace_bytes(batch, d_inner));
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
-  const int nc = ak::diag_chunks(batch, seqlen, d_inner);
+  const int nc = ak::diag_chunks(batch, seqlen, d_inner, 17);
   if (nc > 1) {
     const int lc = (int)((seqlen + nc - 1) / nc);
     const int ncs = (int)((seqlen + lc - 1) / lc);

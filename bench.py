@@ -114,6 +114,19 @@ def gen_c5(b=4, d=2048, l=4096, n=16):
     return {"u": u, "delta": delta, "A": A, "B": B, "C": C, "D": D, "z": z}
 
 
+def gen_diag(b=16, l=1024, d=384):
+    """Inputs of the diagonal scan as AMADEUS forms them (models/amadeus.py:98-103):
+    dA = exp(dt A) with softplus-sized dt and A = -(1..64) over 6 heads,
+    dBx = dt B x, C, D = 1, x ~ N(0, 1), and an upstream gradient."""
+    g = torch.Generator().manual_seed(3)
+    dt = F.softplus(torch.randn(b, l, d, generator=g) * 0.5 - 4.0)
+    A = -torch.arange(1, 65, dtype=torch.float32).repeat(d // 64)
+    x = torch.randn(b, l, d, generator=g)
+    return {"dA": torch.exp(dt * A), "dBx": dt * torch.randn(b, l, d, generator=g) * x,
+            "C": torch.randn(b, l, d, generator=g), "D": torch.ones(d), "x": x,
+            "gy": torch.randn(b, l, d, generator=g)}
+
+
 # Algorithmic work per launch (survey 8(d)).
 C1_BYTES = 2048 * 768 * 4 * 2 + 768 * 4
 C2_BYTES = 2 * 8 * 12 * 1024 * 1024 * 2
@@ -130,6 +143,13 @@ C5_BYTES = 3 * 4 * 2048 * 4096 * 2 + 4 * 2048 * 4096 * 4 + 2 * 4 * 16 * 4096 * 2
 # the reference's N=64 mamba-ssm shape: u, delta, out fp16 [8, 384, 512];
 # B, C fp16 [8, 64, 512]; A [384, 64] and D fp32
 N64_BYTES = 3 * 8 * 384 * 512 * 2 + 2 * 8 * 64 * 512 * 2 + 384 * 64 * 4 + 384 * 4
+# the diagonal scan (AMADEUS's SSM path, 384 channels) at batch 16, seqlen 1024:
+# forward reads dA, dBx, C, x and writes y (fp32 per element) plus D; backward
+# reads dA, dBx, C, x, grad_y and writes grad_dA, grad_dBx, grad_C, grad_x,
+# plus D and grad_D
+DIAG_SHAPE = (16, 1024, 384)
+DIAG_BYTES = 5 * 4 * 16 * 1024 * 384 + 384 * 4
+DIAGB_BYTES = 9 * 4 * 16 * 1024 * 384 + 2 * 384 * 4
 # Mamba-1 backward at the C5 shape: read u, z, dout (bf16), delta (fp32), B, C,
 # A, D; write du, dz (bf16), ddelta (fp32), dB, dC (bf16), dA, dD (fp32)
 C5B_BYTES = (4 * 2048 * 4096 * (2 + 2 + 2 + 4 + 2 + 2 + 4) + 4 * 4 * 16 * 4096 * 2
@@ -294,6 +314,23 @@ def make_case(name):
         return Case(name, "Mamba-1 scan at the reference's benchmark shape B8 D384 L512 N64 fp16",
                     "hbm", N64_BYTES, 8 * 512, launch, sets, "mamba_scan_fast_kernel (4 lane rows per channel)",
                     valu_cycles=scan_valu_cycles(8, 384, 64, 512), valu_model=SCAN_VALU_MODEL)
+    if name in ("diag", "diagb"):
+        # the diagonal recurrence at AMADEUS's shape: chunked forward / backward
+        cpu = gen_diag(*DIAG_SHAPE)
+        sets = _replicate(cpu, _sets(DIAGB_BYTES if name == "diagb" else DIAG_BYTES))
+        for st in sets:
+            st["y"] = torch.empty_like(st["x"])
+            st["grads"] = [torch.empty_like(st["x"]) for _ in range(4)] + [torch.empty_like(st["D"])]
+        if name == "diag":
+            launch = lambda st: _lib.diag_scan(st["dA"], st["dBx"], st["C"], st["D"], st["x"], st["y"])
+            return Case(name, "Diagonal scan fp32 [16, 1024, 384] (AMADEUS's SSM width)", "hbm", DIAG_BYTES,
+                        16 * 1024, launch, sets,
+                        "diag_scan_chunk_agg_kernel + diag_scan_chunk_carry_kernel + diag_scan_chunk_out_kernel")
+        launch = lambda st: _lib.diag_scan_bwd(st["dA"], st["dBx"], st["C"], st["D"], st["x"], st["gy"],
+                                               st["grads"][0], st["grads"][1], st["grads"][2], st["grads"][4],
+                                               st["grads"][3])
+        return Case(name, "Diagonal scan backward fp32 [16, 1024, 384]", "hbm", DIAGB_BYTES, 16 * 1024, launch,
+                    sets, "chunked diagonal-scan backward (8 launches)")
     if name == "c5b":
         cpu = gen_c5()
         cpu["dout"] = torch.randn(cpu["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()
@@ -535,6 +572,14 @@ def cpu_baseline(name, budget_s=4.0):
                                                       c["D"], c["z"])), 2)
         return ((32 * 4096) / t / 2048 / 1e6, "Mtok/s",
                 "batch 1, 32 of 2048 channels, full L=4096 (forward oracle + float64 backward oracle)")
+    if name == "diag":
+        c = gen_diag(b=1)
+        t = timed(lambda: ops.diag_scan_ref(c["dA"], c["dBx"], c["C"], c["D"], c["x"]), 3)
+        return DIAG_BYTES / 16 / t / 1e9, "GB/s", "batch 1 of 16 (fp32 oracle)"
+    if name == "diagb":
+        c = gen_diag(b=1)
+        t = timed(lambda: ops.diag_scan_bwd_ref(c["dA"], c["dBx"], c["C"], c["D"], c["x"], c["gy"]), 2)
+        return DIAGB_BYTES / 16 / t / 1e9, "GB/s", "batch 1 of 16 (float64 oracle)"
     if name == "n64":
         g = torch.Generator().manual_seed(0)
         u = torch.randn(1, 48, 512, generator=g).half()
@@ -567,7 +612,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b,c5t,n64")
+    ap.add_argument("--only", default="c1,c2,c3,c3b,c4,c4s,c4b,c5,c5b,c5t,n64,diag,diagb")
     ap.add_argument("--harness", nargs="?", const="", default=None, metavar="KERNEL_TYPE",
                     help="run the staged correctness + timing harness for one kernel type "
                          "(softmax, cross_entropy, rmsnorm, fused_residual_add_rmsnorm, "

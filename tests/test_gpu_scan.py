@@ -312,6 +312,34 @@ def test_diag_scan_backward(shp):
         assert bool(((got - ref).abs() <= bound).all()), float(((got - ref).abs() / bound).max())
 
 
+@pytest.mark.parametrize("shp", [(1, 32, 3), (1, 33, 1), (3, 100, 7), (2, 1000, 33), (1, 5000, 8),
+                                 (16, 1024, 384), (2, 31, 5), (512, 64, 384)])
+def test_diag_scan_chunk_plans(shp):
+    """The diagonal scan's chunk plans at their edges, forward and backward
+    against the float64 oracle: the smallest chunked lengths (32, 33 steps),
+    a short last chunk (1000 = 58 x 17 + 14), the 64-chunk cap (5000 steps),
+    AMADEUS's width, and shapes that stay sequential (31 steps; 2^17 lanes)."""
+    need_gpu()
+    from kernels.hip import selective_scan, selective_scan_backward
+    g = torch.Generator().manual_seed(sum(shp) + 5)
+    dA = torch.sigmoid(torch.randn(*shp, generator=g) + 2.0)
+    dBx = 0.1 * torch.randn(*shp, generator=g)
+    C = torch.randn(*shp, generator=g)
+    D = torch.randn(shp[2], generator=g)
+    x = torch.randn(*shp, generator=g)
+    gy = torch.randn(*shp, generator=g)
+    say("diag scan chunk plan", shp)
+    y = selective_scan.kernel_fn(*(t.to(DEV) for t in (dA, dBx, C, D, x))).cpu().double()
+    ref = ops.diag_scan_ref(dA.double(), dBx.double(), C.double(), D.double(), x.double())
+    assert bool(((y - ref).abs() <= 1e-5 * ref.abs() + 1e-6 * float(ref.abs().max())).all())
+    outs = selective_scan_backward.kernel_fn(*(t.to(DEV) for t in (dA, dBx, C, D, x, gy)))
+    refs = ops.diag_scan_bwd_ref(dA, dBx, C, D, x, gy)
+    for got, r in zip(outs, refs):
+        got = got.double().cpu()
+        bound = 1e-5 * r.abs() + 1e-6 * float(r.abs().max())
+        assert bool(((got - r).abs() <= bound).all()), float(((got - r).abs() / bound).max())
+
+
 def test_diag_scan_op_autograd_on_gpu():
     """torch.ops.autokernel.selective_scan backward on the GPU (the gfx950
     backward kernel) against the float64 sequential backward."""
