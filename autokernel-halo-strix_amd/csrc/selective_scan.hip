@@ -991,8 +991,8 @@ diag_scan_chunk_agg_kernel(const float* __restrict__ dA, const float* __restrict
 }
 
 __global__ void __launch_bounds__(256)
-diag_scan_chunk_carry_kernel(float* __restrict__ y, float* __restrict__ also, int batch, int seqlen,
-                             int d_inner, int lc, int nchunks) {
+diag_scan_chunk_carry_kernel(float* __restrict__ y, int batch, int seqlen, int d_inner, int lc,
+                             int nchunks) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)batch * d_inner) return;
   const int b = (int)(gid / d_inner);
@@ -1015,13 +1015,11 @@ diag_scan_chunk_carry_kernel(float* __restrict__ y, float* __restrict__ also, in
     for (int i = 0; i < kG; ++i) {
       if (k0 + i + 1 < nchunks) {
         y[base + (k0 + i) * chunk_stride] = s;  // the state entering chunk k0 + i
-        if (also) also[base + (k0 + i) * chunk_stride] = s;
         s = fmaf(P[i], s, S[i]);
       }
     }
   }
   y[base + (int64_t)(nchunks - 1) * chunk_stride] = s;
-  if (also) also[base + (int64_t)(nchunks - 1) * chunk_stride] = s;
 }
 
 // Chunks for the diagonal scan: enough for about 2^lanes_log2 lanes in all,
@@ -1165,32 +1163,37 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
   grad_D[d] = s;
 }
 
-// The backward in chunks (the same plan as the chunked forward, lanes
+// The backward in chunks (the chunk plan of the chunked forward, lanes
 // (batch, chunk, channel), the gradient buffers as scratch), for shapes whose
-// (batch, channel) lanes are too few for the GPU:
-//   1. forward aggregates (P, S) of every chunk but the last in grad_C;
-//   2. per (batch, channel): the forward state entering each chunk, kept in
-//      the chunk's first grad_dBx row;
-//   3. every chunk: its states, into grad_C;
-//   4. reverse aggregates of every chunk but the first: with the carried
-//      adjoint c (c = g_t dA_t passes step t's gradient to step t - 1, and
-//      g_t = gy_t C_t + c), the chunk's product Q of dA (in grad_dA) and its
-//      carried value G leaving the chunk from c = 0 (in grad_x);
-//   5. per (batch, channel), from the last chunk back: the carried adjoint
-//      entering each chunk, c_k = Q_{k+1} c_{k+1} + G_{k+1}, over Q;
-//   6. every chunk backward in time from its entering adjoint, as the
-//      sequential kernel does, writing every gradient; its first step reads
-//      the previous chunk's last state from the kept entering state, and the
+// (batch, channel) lanes are too few for the GPU. The adjoint is carried
+// backward in time as c: g_t = gy_t C_t + c, then c = g_t dA_t is what step t
+// passes to step t - 1, affine in c across a chunk. Five launches:
+//   1. every chunk's aggregates in one pass over its rows: the forward decay
+//      product and state from zero (P, S; every chunk but the last, in the
+//      chunk's first two grad_C rows) and the reverse product of dA and value
+//      of c leaving the chunk from c = 0 (Q, G; every chunk but the first, in
+//      the first rows of grad_dA and grad_x);
+//   2. per (batch, channel): the forward state entering each chunk (into the
+//      chunk's first grad_dBx row) and the adjoint carried into each chunk,
+//      c_k = Q_{k+1} c_{k+1} + G_{k+1} (over Q);
+//   3. every chunk: its states recomputed into its grad_C rows, then the
+//      sequential kernel's backward sweep over them (loads 8 steps ahead),
+//      the first step reading the state before the chunk from grad_dBx; the
 //      chunk's sum of gy x goes to its first grad_x row;
-//   7. per (batch, channel): the chunks' partials summed in chunk order (into
-//      the grad_D workspace) and grad_x restored in those rows; then grad_D
-//      as the sum over the batch, in order.
+//   4. per (batch, channel): those partials summed in chunk order (into the
+//      grad_D workspace) and grad_x written back in those rows;
+//   5. grad_D as the sum over the batch, in order.
 // Every chunk but the last is full, so (P, S) fit its first two rows; each
 // lane reads its chunk's scratch rows before it writes them.
+// Both directions' aggregates of a chunk in one pass over its rows: the
+// forward (P, S) into grad_C rows t0, t0 + 1 (every chunk but the last) and
+// the reverse (Q, G) into the first rows of grad_dA and grad_x (every chunk
+// but the first); the second loop reads dA again from L2.
 __global__ void __launch_bounds__(256)
-diag_bwd_fwd_states_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
-                           const float* __restrict__ s_in, float* __restrict__ st, int batch,
-                           int seqlen, int d_inner, int lc, int nchunks) {
+diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                     const float* __restrict__ C, const float* __restrict__ gy,
+                     float* __restrict__ fwd_agg, float* __restrict__ q_out, float* __restrict__ g_out,
+                     int batch, int seqlen, int d_inner, int lc, int nchunks) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_b = (int64_t)nchunks * d_inner;
   if (gid >= (int64_t)batch * per_b) return;
@@ -1199,76 +1202,89 @@ diag_bwd_fwd_states_kernel(const float* __restrict__ dA, const float* __restrict
   const int d = (int)(gid % d_inner);
   const int t0 = k * lc;
   const int n = min(lc, seqlen - t0);
-  int64_t idx = ((int64_t)b * seqlen + t0) * d_inner + d;
-  float s = s_in[idx];
-#pragma unroll 8
-  for (int t = 0; t < n; ++t, idx += d_inner) {
-    s = fmaf(dA[idx], s, dBx[idx]);
-    st[idx] = s;
-  }
-}
-
-__global__ void __launch_bounds__(256)
-diag_bwd_rev_agg_kernel(const float* __restrict__ dA, const float* __restrict__ C,
-                        const float* __restrict__ gy, float* __restrict__ q_out,
-                        float* __restrict__ g_out, int batch, int seqlen, int d_inner, int lc,
-                        int nchunks) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t per_b = (int64_t)(nchunks - 1) * d_inner;
-  if (gid >= (int64_t)batch * per_b) return;
-  const int b = (int)(gid / per_b);
-  const int k = 1 + (int)((gid % per_b) / d_inner);  // chunks 1 .. nchunks - 1
-  const int d = (int)(gid % d_inner);
-  const int t0 = k * lc;
-  const int n = min(lc, seqlen - t0);
   const int64_t first = ((int64_t)b * seqlen + t0) * d_inner + d;
-  int64_t idx = first + (int64_t)(n - 1) * d_inner;
-  float c = 0.0f, Q = 1.0f;
+  if (k + 1 < nchunks) {
+    int64_t idx = first;
+    float P = 1.0f, S = 0.0f;
 #pragma unroll 8
-  for (int t = n - 1; t >= 0; --t, idx -= d_inner) {
-    const float a = dA[idx];
-    const float g = fmaf(gy[idx], C[idx], c);
-    c = g * a;
-    Q *= a;
+    for (int t = 0; t < n; ++t, idx += d_inner) {
+      const float a = dA[idx];
+      S = fmaf(a, S, dBx[idx]);
+      P *= a;
+    }
+    fwd_agg[first] = P;
+    fwd_agg[first + d_inner] = S;
   }
-  q_out[first] = Q;
-  g_out[first] = c;
+  if (k > 0) {
+    int64_t idx = first + (int64_t)(n - 1) * d_inner;
+    float c = 0.0f, Q = 1.0f;
+#pragma unroll 8
+    for (int t = n - 1; t >= 0; --t, idx -= d_inner) {
+      const float a = dA[idx];
+      const float g = fmaf(gy[idx], C[idx], c);
+      c = g * a;
+      Q *= a;
+    }
+    q_out[first] = Q;
+    g_out[first] = c;
+  }
 }
 
+// Both carries per (batch, channel): the forward state entering each chunk
+// (into grad_dBx's first rows) and the adjoint carried into each chunk from
+// the right (over Q in grad_dA's first rows).
 __global__ void __launch_bounds__(256)
-diag_bwd_rev_carry_kernel(float* __restrict__ q_c, const float* __restrict__ g_agg, int batch,
-                          int seqlen, int d_inner, int lc, int nchunks) {
+diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* __restrict__ s_in,
+                        float* __restrict__ q_c, const float* __restrict__ g_agg, int batch,
+                        int seqlen, int d_inner, int lc, int nchunks) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)batch * d_inner) return;
   const int b = (int)(gid / d_inner);
   const int d = (int)(gid % d_inner);
   constexpr int kG = 16;
   const int64_t base = (int64_t)b * seqlen * d_inner + d;
-  const int64_t chunk_stride = (int64_t)lc * d_inner;
-  float c = 0.0f;  // entering the last chunk
-  // chunks nchunks - 1 down to 1: up to 16 aggregates loaded before their rows are overwritten
+  const int64_t cs = (int64_t)lc * d_inner;
+  float s = 0.0f;
+  for (int k0 = 0; k0 + 1 < nchunks; k0 += kG) {
+    float P[kG], S[kG];
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      const int k = min(k0 + i, nchunks - 2);
+      P[i] = fwd_agg[base + k * cs];
+      S[i] = fwd_agg[base + k * cs + d_inner];
+    }
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      if (k0 + i + 1 < nchunks) {
+        s_in[base + (k0 + i) * cs] = s;
+        s = fmaf(P[i], s, S[i]);
+      }
+    }
+  }
+  s_in[base + (int64_t)(nchunks - 1) * cs] = s;
+  float c = 0.0f;
   for (int k0 = nchunks - 1; k0 >= 1; k0 -= kG) {
     float Q[kG], G[kG];
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
       const int k = max(k0 - i, 1);
-      Q[i] = q_c[base + k * chunk_stride];
-      G[i] = g_agg[base + k * chunk_stride];
+      Q[i] = q_c[base + k * cs];
+      G[i] = g_agg[base + k * cs];
     }
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
       if (k0 - i >= 1) {
-        q_c[base + (k0 - i) * chunk_stride] = c;  // the adjoint carried into chunk k0 - i
+        q_c[base + (k0 - i) * cs] = c;
         c = fmaf(Q[i], c, G[i]);
       }
     }
   }
-  q_c[base] = c;  // into chunk 0
+  q_c[base] = c;
 }
 
 __global__ void __launch_bounds__(256)
-diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ C,
-                      const float* __restrict__ D, const float* __restrict__ x,
+diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                      const float* __restrict__ C, const float* __restrict__ D, const float* __restrict__ x,
                       const float* __restrict__ gy, float* __restrict__ g_dA,
                       float* __restrict__ g_dBx, float* g_C, float* __restrict__ g_x, int batch,
                       int seqlen, int d_inner, int lc, int nchunks) {
@@ -1286,6 +1302,17 @@ diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ C,
   const float s_prev0 = g_dBx[first];  // the state before the chunk
   const float dd = D[d];
   float gd = 0.0f;
+  {
+    // the chunk's states, from the state before it, into its grad_C rows
+    // (read back below from L2 by this lane)
+    float sv = s_prev0;
+    int64_t j = first;
+#pragma unroll 8
+    for (int t = 0; t < n; ++t, j += D_) {
+      sv = fmaf(dA[j], sv, dBx[j]);
+      g_C[j] = sv;
+    }
+  }
   // steps t .. t - 7 (chunk-relative) loaded before any of their rows is
   // written: grad_C holds the states and is overwritten with gy * state, so
   // the loads cannot move past the stores otherwise
@@ -2078,8 +2105,8 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const unsigned g3 = (unsigned)((batch * nc * d_inner + 255) / 256);
   ak::diag_scan_chunk_agg_kernel<<<dim3(g1), dim3(256), 0, s>>>(dA, dBx, y, (int)batch, (int)seqlen,
                                                                (int)d_inner, lc, nc);
-  ak::diag_scan_chunk_carry_kernel<<<dim3(g2), dim3(256), 0, s>>>(y, nullptr, (int)batch, (int)seqlen,
-                                                                 (int)d_inner, lc, nc);
+  ak::diag_scan_chunk_carry_kernel<<<dim3(g2), dim3(256), 0, s>>>(y, (int)batch, (int)seqlen, (int)d_inner,
+                                                                 lc, nc);
   ak::diag_scan_chunk_out_kernel<<<dim3(g3), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch,
                                                                (int)seqlen, (int)d_inner, lc, nc);
   return ak_check_launch(name);
@@ -2119,18 +2146,13 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
     const int lc = (int)((seqlen + nc - 1) / nc);
     const int ncs = (int)((seqlen + lc - 1) / lc);
     const int B_ = (int)batch, L_ = (int)seqlen, D_ = (int)d_inner;
-    const unsigned g_agg = (unsigned)((batch * (ncs - 1) * d_inner + 255) / 256);
     const unsigned g_lane = (unsigned)((lanes + 255) / 256);
     const unsigned g_all = (unsigned)((batch * ncs * d_inner + 255) / 256);
-    ak::diag_scan_chunk_agg_kernel<<<dim3(g_agg), dim3(256), 0, s>>>(dA, dBx, grad_C, B_, L_, D_, lc, ncs);
-    ak::diag_scan_chunk_carry_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_C, grad_dBx, B_, L_, D_, lc,
-                                                                       ncs);
-    ak::diag_bwd_fwd_states_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, grad_dBx, grad_C, B_, L_, D_,
-                                                                    lc, ncs);
-    ak::diag_bwd_rev_agg_kernel<<<dim3(g_agg), dim3(256), 0, s>>>(dA, C, grad_y, grad_dA, grad_x, B_, L_,
-                                                                 D_, lc, ncs);
-    ak::diag_bwd_rev_carry_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_dA, grad_x, B_, L_, D_, lc, ncs);
-    ak::diag_bwd_chunk_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, C, D, x, grad_y, grad_dA, grad_dBx,
+    ak::diag_bwd_aggs_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, C, grad_y, grad_C, grad_dA, grad_x,
+                                                              B_, L_, D_, lc, ncs);
+    ak::diag_bwd_carries_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_C, grad_dBx, grad_dA, grad_x, B_, L_,
+                                                                  D_, lc, ncs);
+    ak::diag_bwd_chunk_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx,
                                                                grad_C, grad_x, B_, L_, D_, lc, ncs);
     ak::diag_bwd_gd_chunks_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_y, D, grad_x, part, B_, L_, D_,
                                                                    lc, ncs);
