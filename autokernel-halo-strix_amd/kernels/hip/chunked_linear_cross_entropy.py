@@ -38,8 +38,8 @@ hand-written MFMA GEMMs with fp32 accumulation (``ak_lmhead_grad_hidden``,
 in place, token-major, by both (the transposed operand through gfx950's
 transposing LDS reads). The vocabulary is walked in ranges whose
 ``dlogits`` slice ``[n_rows, width]`` stays under ``GRAD_LOGITS_BUDGET``
-bytes (``ak_lmhead_ce_bwd_range``; the width a multiple of the tile kernel's
-256 vocab rows). Each range's ``grad_W`` rows are one complete GEMM rounded
+bytes (``ak_lmhead_ce_bwd_range``; whole 256-row vocab tiles, the ranges as
+even as whole rounds of the tile kernel allow: ``_vocab_ranges``). Each range's ``grad_W`` rows are one complete GEMM rounded
 once to the weight dtype; ``grad_hidden`` is summed over the ranges in an
 fp32 buffer (the GEMM's add-into-fp32 output) and rounded once at the end.
 The default budget (4 GiB) keeps the C4 shape in one range (8192 x 50304
@@ -60,6 +60,8 @@ everything to fp16).
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 import torch.nn as nn
@@ -141,6 +143,41 @@ _RANGE_PAD = 64
 _VOCAB_TILE = 256
 
 
+def _vocab_ranges(n: int, vocab: int, elem: int, cus: int):
+    """Vocab ranges ``[v0, v1)`` whose dlogits slices (``n x (v1 - v0)``
+    elements of ``elem`` bytes) fit ``GRAD_LOGITS_BUDGET``.
+
+    The fewest ranges that fit, of whole vocab tiles, as even as the tile
+    kernel allows: ranges of ``w`` tiles with the rest in the last one, ``w``
+    a multiple of ``q``, where ``q`` vocab tiles times the ``ceil(n / 256)``
+    token tiles is a multiple of the CU count (each launch then runs whole
+    rounds of the persistent workgroups). ``w`` is the even share rounded
+    down to a multiple of ``q`` if the last range then still fits, else
+    rounded up if that fits, else the even share itself. Measured at C4
+    (whole backward, one process): a 512 MB budget takes 96 + 100.5 tiles,
+    632 MiB and 0-4% faster than 128 + 68.5 at 816 MiB; 256 MB takes
+    48 + 48 + 48 + 52.5, 440 MiB at the same time as 64 + 64 + 64 + 4.5 at
+    488 MiB; at 128 MB the even share of 29 tiles ran 5% slower than 32-tile
+    ranges, which rounding up gives.
+    """
+    tiles = -(-vocab // _VOCAB_TILE)
+    cap = max(1, min(tiles, GRAD_LOGITS_BUDGET // (n * elem * _VOCAB_TILE)))
+    count = -(-tiles // cap)
+    if count == 1:
+        return [(0, vocab)]
+    per = -(-tiles // count)
+    q = cus // math.gcd(cus, -(-n // 256))
+    down, up = per // q * q, -(-per // q) * q
+    if down > 0 and tiles - (count - 1) * down <= cap:
+        per = down
+    elif up <= cap:
+        per = up
+    # count ranges of per tiles, the last one holding the rest: it is not
+    # empty since (count - 1) * per < tiles, and it fits by the choice above
+    cuts = [i * per * _VOCAB_TILE for i in range(count)] + [vocab]
+    return [(cuts[i], cuts[i + 1]) for i in range(count)]
+
+
 def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torch.Tensor,
                        lse: torch.Tensor, denom: torch.Tensor, grad_loss: torch.Tensor,
                        ignore_index: int = -100, need_hidden: bool = True,
@@ -167,10 +204,12 @@ def lmhead_ce_backward(hidden: torch.Tensor, weight: torch.Tensor, targets: torc
     g1 = grad_loss.reshape(1).to(torch.float32).contiguous()
     den1 = denom.reshape(1).to(torch.float32).contiguous()
     lse = lse.contiguous()
-    width = GRAD_LOGITS_BUDGET // (n * hidden.element_size())
-    width = max(_VOCAB_TILE, width - width % _VOCAB_TILE)
-    width = min(width, vocab)
-    ranges = [(v0, min(v0 + width, vocab)) for v0 in range(0, vocab, width)]
+    # the CU count only shapes the plan (a CPU tensor reaches here only from
+    # the tests' fake backend: MI355X's 256)
+    cus = (torch.cuda.get_device_properties(hidden.device).multi_processor_count
+           if hidden.device.type == "cuda" else 256)
+    ranges = _vocab_ranges(n, vocab, hidden.element_size(), cus)
+    width = max(v1 - v0 for v0, v1 in ranges)
     # each range's dlogits slice lives in a buffer whose pitch covers the
     # slice rounded up to 64 columns (the gradient GEMMs read whole 64-column
     # K blocks); a pitch off powers of two keeps the rows from all starting

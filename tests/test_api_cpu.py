@@ -619,3 +619,32 @@ def test_optimized_model_context_swaps_and_restores(fake_backend):
     assert cmp["correctness"] == "PASS"
     bad = verify.compare_outputs(ref, ref.clone().fill_(float("nan")), torch.float32)
     assert bad["correctness"] == "FAIL" and "NaN" in bad["reason"]
+
+
+def test_lmhead_backward_vocab_range_plan(monkeypatch):
+    """The lm-head backward's vocab ranges under a dlogits budget: they tile
+    the vocabulary in order, every range but the last is whole 256-column
+    tiles, none exceeds the budget's width (one tile at least), and their
+    number is the fewest that fit. At the C4 shape the plans are the measured
+    ones: even shares rounded to whole rounds of the tile kernel's 256
+    persistent workgroups (8 vocab tiles x 32 token tiles)."""
+    import random
+    from kernels.hip import chunked_linear_cross_entropy as clce
+    c4 = {512: [96, 96 + 100.5], 256: [48, 96, 144, 196.5], 128: [32, 64, 96, 128, 160, 192, 196.5],
+          4096: [196.5]}
+    for mb, ends in c4.items():
+        monkeypatch.setattr(clce, "GRAD_LOGITS_BUDGET", mb << 20)
+        assert [v1 / 256 for _, v1 in clce._vocab_ranges(8192, 50304, 2, 256)] == ends
+    rng = random.Random(0)
+    for _ in range(3000):
+        n, vocab = rng.randint(1, 20000), rng.randint(1, 300000)
+        elem, cus = rng.choice([2, 4]), rng.choice([256, 304, 80, 1])
+        monkeypatch.setattr(clce, "GRAD_LOGITS_BUDGET", rng.randint(1, 1 << 32))
+        r = clce._vocab_ranges(n, vocab, elem, cus)
+        tiles = -(-vocab // 256)
+        cap = max(1, min(tiles, clce.GRAD_LOGITS_BUDGET // (n * elem * 256)))
+        assert r[0][0] == 0 and r[-1][1] == vocab
+        assert all(a[1] == b[0] for a, b in zip(r, r[1:])) and all(v1 > v0 for v0, v1 in r)
+        assert all((v1 - v0) % 256 == 0 for v0, v1 in r[:-1])
+        assert max(-(-(v1 - v0) // 256) for v0, v1 in r) <= cap
+        assert len(r) == -(-tiles // cap)
