@@ -1163,37 +1163,40 @@ diag_scan_gd_kernel(const float* __restrict__ gD_part, float* __restrict__ grad_
   grad_D[d] = s;
 }
 
-// The backward in chunks (the chunk plan of the chunked forward, lanes
-// (batch, chunk, channel), the gradient buffers as scratch), for shapes whose
-// (batch, channel) lanes are too few for the GPU. The adjoint is carried
-// backward in time as c: g_t = gy_t C_t + c, then c = g_t dA_t is what step t
-// passes to step t - 1, affine in c across a chunk. Five launches:
+// The backward in chunks (lanes (batch, chunk, channel), the gradient
+// buffers as scratch), for shapes whose (batch, channel) lanes are too few
+// for the GPU. The adjoint is carried backward in time as c: g_t = gy_t C_t
+// + c, then c = g_t dA_t is what step t passes to step t - 1, affine in c
+// across a chunk. Four launches:
 //   1. every chunk's aggregates in one pass over its rows: the forward decay
 //      product and state from zero (P, S; every chunk but the last, in the
-//      chunk's first two grad_C rows) and the reverse product of dA and value
-//      of c leaving the chunk from c = 0 (Q, G; every chunk but the first, in
-//      the first rows of grad_dA and grad_x);
-//   2. per (batch, channel): the forward state entering each chunk (into the
-//      chunk's first grad_dBx row) and the adjoint carried into each chunk,
+//      chunk's first two grad_C rows), the reverse product of dA and value of
+//      c leaving the chunk from c = 0 (Q, G; every chunk but the first, in the
+//      first rows of grad_dA and grad_x), and the chunk's sum of gy x (in the
+//      first grad_dBx row);
+//   2. per (batch, channel): the sums of gy x added in chunk order (into the
+//      grad_D workspace), then the forward state entering each chunk (over
+//      the sums) and the adjoint carried into each chunk,
 //      c_k = Q_{k+1} c_{k+1} + G_{k+1} (over Q);
-//   3. every chunk: its states recomputed into its grad_C rows, then the
-//      sequential kernel's backward sweep over them (loads 8 steps ahead),
-//      the first step reading the state before the chunk from grad_dBx; the
-//      chunk's sum of gy x goes to its first grad_x row;
-//   4. per (batch, channel): those partials summed in chunk order (into the
-//      grad_D workspace) and grad_x written back in those rows;
-//   5. grad_D as the sum over the batch, in order.
+//   3. every chunk: its states from the state before it, then the
+//      sequential kernel's backward sweep over them;
+//   4. grad_D as the sum over the batch, in order.
 // Every chunk but the last is full, so (P, S) fit its first two rows; each
-// lane reads its chunk's scratch rows before it writes them.
-// Both directions' aggregates of a chunk in one pass over its rows: the
-// forward (P, S) into grad_C rows t0, t0 + 1 (every chunk but the last) and
-// the reverse (Q, G) into the first rows of grad_dA and grad_x (every chunk
-// but the first); the second loop reads dA again from L2.
+// lane reads its chunk's scratch rows before it writes them. With kLC > 0
+// (chunks of at most kLC steps) a lane holds its chunk's rows in registers:
+// all its loads are issued together and the states never leave registers.
+// With kLC = 0 the rows stream, and pass 3 parks the states in grad_C rows
+// and reads them back from L2. Both do the same arithmetic in the same order
+// (a register lane pads its steps past the chunk's end with dA = 1 and zeros,
+// which leave every aggregate and sum unchanged).
+template <int kLC>
 __global__ void __launch_bounds__(256)
 diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
                      const float* __restrict__ C, const float* __restrict__ gy,
-                     float* __restrict__ fwd_agg, float* __restrict__ q_out, float* __restrict__ g_out,
-                     int batch, int seqlen, int d_inner, int lc, int nchunks) {
+                     const float* __restrict__ x, float* __restrict__ fwd_agg,
+                     float* __restrict__ q_out, float* __restrict__ g_out,
+                     float* __restrict__ gd_out, int batch, int seqlen, int d_inner, int lc,
+                     int nchunks) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_b = (int64_t)nchunks * d_inner;
   if (gid >= (int64_t)batch * per_b) return;
@@ -1202,40 +1205,81 @@ diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx
   const int d = (int)(gid % d_inner);
   const int t0 = k * lc;
   const int n = min(lc, seqlen - t0);
-  const int64_t first = ((int64_t)b * seqlen + t0) * d_inner + d;
-  if (k + 1 < nchunks) {
-    int64_t idx = first;
-    float P = 1.0f, S = 0.0f;
-#pragma unroll 8
-    for (int t = 0; t < n; ++t, idx += d_inner) {
-      const float a = dA[idx];
-      S = fmaf(a, S, dBx[idx]);
-      P *= a;
+  const int64_t D_ = d_inner;
+  const int64_t first = ((int64_t)b * seqlen + t0) * D_ + d;
+  float gd = 0.0f;
+  if constexpr (kLC > 0) {
+    float a[kLC], v[kLC], cv[kLC], yv[kLC], xv[kLC];
+#pragma unroll
+    for (int j = 0; j < kLC; ++j) {
+      const bool in = j < n;
+      const int64_t i = first + (int64_t)(in ? j : 0) * D_;
+      a[j] = in ? dA[i] : 1.0f;
+      v[j] = in ? dBx[i] : 0.0f;
+      cv[j] = in ? C[i] : 0.0f;
+      yv[j] = in ? gy[i] : 0.0f;
+      xv[j] = in ? x[i] : 0.0f;
     }
-    fwd_agg[first] = P;
-    fwd_agg[first + d_inner] = S;
-  }
-  if (k > 0) {
-    int64_t idx = first + (int64_t)(n - 1) * d_inner;
+    if (k + 1 < nchunks) {
+      float P = 1.0f, S = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kLC; ++j) {
+        S = fmaf(a[j], S, v[j]);
+        P *= a[j];
+      }
+      fwd_agg[first] = P;
+      fwd_agg[first + D_] = S;
+    }
+    float c = 0.0f, Q = 1.0f;
+#pragma unroll
+    for (int j = kLC - 1; j >= 0; --j) {
+      c = fmaf(yv[j], cv[j], c) * a[j];
+      Q *= a[j];
+      gd = fmaf(yv[j], xv[j], gd);
+    }
+    if (k > 0) {
+      q_out[first] = Q;
+      g_out[first] = c;
+    }
+  } else {
+    if (k + 1 < nchunks) {
+      int64_t idx = first;
+      float P = 1.0f, S = 0.0f;
+#pragma unroll 8
+      for (int t = 0; t < n; ++t, idx += D_) {
+        const float a = dA[idx];
+        S = fmaf(a, S, dBx[idx]);
+        P *= a;
+      }
+      fwd_agg[first] = P;
+      fwd_agg[first + D_] = S;
+    }
+    int64_t idx = first + (int64_t)(n - 1) * D_;
     float c = 0.0f, Q = 1.0f;
 #pragma unroll 8
-    for (int t = n - 1; t >= 0; --t, idx -= d_inner) {
+    for (int t = n - 1; t >= 0; --t, idx -= D_) {
       const float a = dA[idx];
-      const float g = fmaf(gy[idx], C[idx], c);
-      c = g * a;
+      const float yv = gy[idx];
+      c = fmaf(yv, C[idx], c) * a;
       Q *= a;
+      gd = fmaf(yv, x[idx], gd);
     }
-    q_out[first] = Q;
-    g_out[first] = c;
+    if (k > 0) {
+      q_out[first] = Q;
+      g_out[first] = c;
+    }
   }
+  gd_out[first] = gd;
 }
 
-// Both carries per (batch, channel): the forward state entering each chunk
-// (into grad_dBx's first rows) and the adjoint carried into each chunk from
-// the right (over Q in grad_dA's first rows).
+// Per (batch, channel): the chunks' sums of gy x added in chunk order (into
+// part), then the forward state entering each chunk (over those sums, in
+// grad_dBx's first rows) and the adjoint carried into each chunk from the
+// right (over Q in grad_dA's first rows). sx is read (sums) before it is
+// written (states) through the one pointer.
 __global__ void __launch_bounds__(256)
-diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* __restrict__ s_in,
-                        float* __restrict__ q_c, const float* __restrict__ g_agg, int batch,
+diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* sx, float* __restrict__ q_c,
+                        const float* __restrict__ g_agg, float* __restrict__ part, int batch,
                         int seqlen, int d_inner, int lc, int nchunks) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)batch * d_inner) return;
@@ -1244,6 +1288,16 @@ diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* __restrict__ s
   constexpr int kG = 16;
   const int64_t base = (int64_t)b * seqlen * d_inner + d;
   const int64_t cs = (int64_t)lc * d_inner;
+  float gd = 0.0f;
+  for (int k0 = 0; k0 < nchunks; k0 += kG) {
+    float G[kG];
+#pragma unroll
+    for (int i = 0; i < kG; ++i) G[i] = sx[base + min(k0 + i, nchunks - 1) * cs];
+#pragma unroll
+    for (int i = 0; i < kG; ++i)
+      if (k0 + i < nchunks) gd += G[i];
+  }
+  part[gid] = gd;
   float s = 0.0f;
   for (int k0 = 0; k0 + 1 < nchunks; k0 += kG) {
     float P[kG], S[kG];
@@ -1256,12 +1310,12 @@ diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* __restrict__ s
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
       if (k0 + i + 1 < nchunks) {
-        s_in[base + (k0 + i) * cs] = s;
+        sx[base + (k0 + i) * cs] = s;
         s = fmaf(P[i], s, S[i]);
       }
     }
   }
-  s_in[base + (int64_t)(nchunks - 1) * cs] = s;
+  sx[base + (int64_t)(nchunks - 1) * cs] = s;
   float c = 0.0f;
   for (int k0 = nchunks - 1; k0 >= 1; k0 -= kG) {
     float Q[kG], G[kG];
@@ -1282,9 +1336,10 @@ diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* __restrict__ s
   q_c[base] = c;
 }
 
+template <int kLC>
 __global__ void __launch_bounds__(256)
 diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
-                      const float* __restrict__ C, const float* __restrict__ D, const float* __restrict__ x,
+                      const float* __restrict__ C, const float* __restrict__ D,
                       const float* __restrict__ gy, float* __restrict__ g_dA,
                       float* __restrict__ g_dBx, float* g_C, float* __restrict__ g_x, int batch,
                       int seqlen, int d_inner, int lc, int nchunks) {
@@ -1301,78 +1356,69 @@ diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ dB
   float c = g_dA[first];               // the adjoint carried into the chunk
   const float s_prev0 = g_dBx[first];  // the state before the chunk
   const float dd = D[d];
-  float gd = 0.0f;
-  {
-    // the chunk's states, from the state before it, into its grad_C rows
-    // (read back below from L2 by this lane)
-    float sv = s_prev0;
-    int64_t j = first;
-#pragma unroll 8
-    for (int t = 0; t < n; ++t, j += D_) {
-      sv = fmaf(dA[j], sv, dBx[j]);
-      g_C[j] = sv;
-    }
-  }
-  // steps t .. t - 7 (chunk-relative) loaded before any of their rows is
-  // written: grad_C holds the states and is overwritten with gy * state, so
-  // the loads cannot move past the stores otherwise
-  auto step = [&](int t, float a, float cv, float yv, float xv, float st_t, float st_p) {
+  auto step = [&](int t, float a, float cv, float yv, float st_t, float st_p) {
     const int64_t i = first + (int64_t)t * D_;
     g_C[i] = yv * st_t;
     const float g = fmaf(yv, cv, c);
     g_dA[i] = g * st_p;
     g_dBx[i] = g;
     c = g * a;
-    if (t > 0) g_x[i] = yv * dd;
-    gd = fmaf(yv, xv, gd);
+    g_x[i] = yv * dd;
   };
-  int t = n - 1;
-  for (; t - kDiagU + 1 >= 0; t -= kDiagU) {
-    float a[kDiagU], cv[kDiagU], yv[kDiagU], xv[kDiagU], st[kDiagU + 1];
+  if constexpr (kLC > 0) {
+    float a[kLC], v[kLC], cv[kLC], yv[kLC], st[kLC + 1];
 #pragma unroll
-    for (int j = 0; j < kDiagU; ++j) {
-      const int64_t i = first + (int64_t)(t - j) * D_;
-      a[j] = dA[i];
-      cv[j] = C[i];
-      yv[j] = gy[i];
-      xv[j] = x[i];
-      st[j] = g_C[i];
+    for (int j = 0; j < kLC; ++j) {
+      const bool in = j < n;
+      const int64_t i = first + (int64_t)(in ? j : 0) * D_;
+      a[j] = in ? dA[i] : 1.0f;
+      v[j] = in ? dBx[i] : 0.0f;
+      cv[j] = in ? C[i] : 0.0f;
+      yv[j] = in ? gy[i] : 0.0f;
     }
-    st[kDiagU] = t - kDiagU >= 0 ? g_C[first + (int64_t)(t - kDiagU) * D_] : s_prev0;
+    st[0] = s_prev0;
 #pragma unroll
-    for (int j = 0; j < kDiagU; ++j) step(t - j, a[j], cv[j], yv[j], xv[j], st[j], st[j + 1]);
-  }
-  for (; t >= 0; --t) {
-    const int64_t i = first + (int64_t)t * D_;
-    const float st_t = g_C[i];
-    const float st_p = t > 0 ? g_C[i - D_] : s_prev0;
-    step(t, dA[i], C[i], gy[i], x[i], st_t, st_p);
-  }
-  g_x[first] = gd;  // the chunk's sum of gy x (the row's gy D is written back by the grad_D pass)
-}
-
-// Per (batch, channel): the sum of the chunks' gy x partials in chunk order
-// (into the grad_D workspace, summed over the batch by diag_scan_gd_kernel),
-// and gy D written back into those grad_x rows.
-__global__ void __launch_bounds__(256)
-diag_bwd_gd_chunks_kernel(const float* __restrict__ gy, const float* __restrict__ D,
-                          float* __restrict__ g_x, float* __restrict__ part, int batch,
-                          int seqlen, int d_inner, int lc, int nchunks) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)batch * d_inner) return;
-  const int b = (int)(gid / d_inner);
-  const int d = (int)(gid % d_inner);
-  const int64_t base = (int64_t)b * seqlen * d_inner + d;
-  const int64_t chunk_stride = (int64_t)lc * d_inner;
-  const float dd = D[d];
-  float s = 0.0f;
+    for (int j = 0; j < kLC; ++j) st[j + 1] = fmaf(a[j], st[j], v[j]);
+#pragma unroll
+    for (int j = kLC - 1; j >= 0; --j)
+      if (j < n) step(j, a[j], cv[j], yv[j], st[j + 1], st[j]);
+  } else {
+    {
+      // the chunk's states, from the state before it, into its grad_C rows
+      // (read back below from L2 by this lane)
+      float sv = s_prev0;
+      int64_t j = first;
 #pragma unroll 8
-  for (int k = 0; k < nchunks; ++k) {
-    const int64_t i = base + k * chunk_stride;
-    s += g_x[i];
-    g_x[i] = gy[i] * dd;
+      for (int t = 0; t < n; ++t, j += D_) {
+        sv = fmaf(dA[j], sv, dBx[j]);
+        g_C[j] = sv;
+      }
+    }
+    // steps t .. t - 7 (chunk-relative) loaded before any of their rows is
+    // written: grad_C holds the states and is overwritten with gy * state, so
+    // the loads cannot move past the stores otherwise
+    int t = n - 1;
+    for (; t - kDiagU + 1 >= 0; t -= kDiagU) {
+      float a[kDiagU], cv[kDiagU], yv[kDiagU], st[kDiagU + 1];
+#pragma unroll
+      for (int j = 0; j < kDiagU; ++j) {
+        const int64_t i = first + (int64_t)(t - j) * D_;
+        a[j] = dA[i];
+        cv[j] = C[i];
+        yv[j] = gy[i];
+        st[j] = g_C[i];
+      }
+      st[kDiagU] = t - kDiagU >= 0 ? g_C[first + (int64_t)(t - kDiagU) * D_] : s_prev0;
+#pragma unroll
+      for (int j = 0; j < kDiagU; ++j) step(t - j, a[j], cv[j], yv[j], st[j], st[j + 1]);
+    }
+    for (; t >= 0; --t) {
+      const int64_t i = first + (int64_t)t * D_;
+      const float st_t = g_C[i];
+      const float st_p = t > 0 ? g_C[i - D_] : s_prev0;
+      step(t, dA[i], C[i], gy[i], st_t, st_p);
+    }
   }
-  part[gid] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -2141,21 +2187,32 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
                         workspace_bytes, ak_diag_scan_bwd_workspace_bytes(batch, d_inner));
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
-  const int nc = ak::diag_chunks(batch, seqlen, d_inner, 17);
+  // Chunks of at most 32 steps keep their rows in registers; the plan for
+  // them aims at 2^19 lanes (at AMADEUS's shape 64 chunks of 16 steps),
+  // otherwise at 2^17 with streaming chunks.
+  int nc = ak::diag_chunks(batch, seqlen, d_inner, 19);
+  int lc = nc > 1 ? (int)((seqlen + nc - 1) / nc) : 0;
+  if (nc > 1 && lc > 32) {
+    nc = ak::diag_chunks(batch, seqlen, d_inner, 17);
+    lc = nc > 1 ? (int)((seqlen + nc - 1) / nc) : 0;
+  }
   if (nc > 1) {
-    const int lc = (int)((seqlen + nc - 1) / nc);
     const int ncs = (int)((seqlen + lc - 1) / lc);
     const int B_ = (int)batch, L_ = (int)seqlen, D_ = (int)d_inner;
     const unsigned g_lane = (unsigned)((lanes + 255) / 256);
     const unsigned g_all = (unsigned)((batch * ncs * d_inner + 255) / 256);
-    ak::diag_bwd_aggs_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, C, grad_y, grad_C, grad_dA, grad_x,
-                                                              B_, L_, D_, lc, ncs);
-    ak::diag_bwd_carries_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_C, grad_dBx, grad_dA, grad_x, B_, L_,
-                                                                  D_, lc, ncs);
-    ak::diag_bwd_chunk_kernel<<<dim3(g_all), dim3(256), 0, s>>>(dA, dBx, C, D, x, grad_y, grad_dA, grad_dBx,
-                                                               grad_C, grad_x, B_, L_, D_, lc, ncs);
-    ak::diag_bwd_gd_chunks_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_y, D, grad_x, part, B_, L_, D_,
-                                                                   lc, ncs);
+    auto run = [&](auto lc_tag) {
+      constexpr int kLC = decltype(lc_tag)::value;
+      ak::diag_bwd_aggs_kernel<kLC><<<dim3(g_all), dim3(256), 0, s>>>(
+          dA, dBx, C, grad_y, x, grad_C, grad_dA, grad_x, grad_dBx, B_, L_, D_, lc, ncs);
+      ak::diag_bwd_carries_kernel<<<dim3(g_lane), dim3(256), 0, s>>>(grad_C, grad_dBx, grad_dA, grad_x, part,
+                                                                    B_, L_, D_, lc, ncs);
+      ak::diag_bwd_chunk_kernel<kLC><<<dim3(g_all), dim3(256), 0, s>>>(
+          dA, dBx, C, D, grad_y, grad_dA, grad_dBx, grad_C, grad_x, B_, L_, D_, lc, ncs);
+    };
+    if (lc <= 16) run(std::integral_constant<int, 16>{});
+    else if (lc <= 32) run(std::integral_constant<int, 32>{});
+    else run(std::integral_constant<int, 0>{});
     ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
         part, grad_D, B_, D_);
     return ak_check_launch(name);
