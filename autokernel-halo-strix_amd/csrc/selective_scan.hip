@@ -967,6 +967,7 @@ diag_scan_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
 // 8 bytes per element more than the sequential pass (dA and dBx read twice);
 // the states differ from the sequential ones by rounding only. Chunks: see
 // diag_chunks.
+template <int kLC>
 __global__ void __launch_bounds__(256)
 diag_scan_chunk_agg_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
                            float* __restrict__ y, int batch, int seqlen, int d_inner, int lc,
@@ -980,11 +981,28 @@ diag_scan_chunk_agg_kernel(const float* __restrict__ dA, const float* __restrict
   const int64_t row0 = (int64_t)b * seqlen + (int64_t)k * lc;
   int64_t idx = row0 * d_inner + d;
   float P = 1.0f, S = 0.0f;
+  if constexpr (kLC > 0) {
+    // a full chunk (lc <= kLC steps), its rows loaded together
+    float a[kLC], v[kLC];
+#pragma unroll
+    for (int t = 0; t < kLC; ++t) {
+      const bool in = t < lc;
+      const int64_t i = idx + (int64_t)(in ? t : 0) * d_inner;
+      a[t] = in ? dA[i] : 1.0f;
+      v[t] = in ? dBx[i] : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < kLC; ++t) {
+      S = fmaf(a[t], S, v[t]);
+      P *= a[t];
+    }
+  } else {
 #pragma unroll 8
-  for (int t = 0; t < lc; ++t, idx += d_inner) {
-    const float a = dA[idx];
-    S = fmaf(a, S, dBx[idx]);
-    P *= a;
+    for (int t = 0; t < lc; ++t, idx += d_inner) {
+      const float a = dA[idx];
+      S = fmaf(a, S, dBx[idx]);
+      P *= a;
+    }
   }
   y[row0 * d_inner + d] = P;
   y[(row0 + 1) * d_inner + d] = S;
@@ -1035,6 +1053,7 @@ inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner, int lanes
   return (int)std::max<int64_t>(nchunks, 1);
 }
 
+template <int kLC>
 __global__ void __launch_bounds__(256)
 diag_scan_chunk_out_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
                            const float* __restrict__ C, const float* __restrict__ D,
@@ -1051,10 +1070,29 @@ diag_scan_chunk_out_kernel(const float* __restrict__ dA, const float* __restrict
   int64_t idx = ((int64_t)b * seqlen + t0) * d_inner + d;
   float s = y[idx];  // the entering state, read before this lane writes its rows
   const float dd = D[d];
+  if constexpr (kLC > 0) {
+    // the chunk's rows (at most kLC) loaded together
+    float a[kLC], v[kLC], c[kLC], xv[kLC];
+#pragma unroll
+    for (int t = 0; t < kLC; ++t) {
+      const bool in = t < n;
+      const int64_t i = idx + (int64_t)(in ? t : 0) * d_inner;
+      a[t] = in ? dA[i] : 1.0f;
+      v[t] = in ? dBx[i] : 0.0f;
+      c[t] = in ? C[i] : 0.0f;
+      xv[t] = in ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int t = 0; t < kLC; ++t) {
+      s = fmaf(a[t], s, v[t]);
+      if (t < n) y[idx + (int64_t)t * d_inner] = fmaf(c[t], s, dd * xv[t]);
+    }
+  } else {
 #pragma unroll 8
-  for (int t = 0; t < n; ++t, idx += d_inner) {
-    s = fmaf(dA[idx], s, dBx[idx]);
-    y[idx] = fmaf(C[idx], s, dd * x[idx]);
+    for (int t = 0; t < n; ++t, idx += d_inner) {
+      s = fmaf(dA[idx], s, dBx[idx]);
+      y[idx] = fmaf(C[idx], s, dd * x[idx]);
+    }
   }
 }
 
@@ -1209,6 +1247,8 @@ diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx
   const int64_t first = ((int64_t)b * seqlen + t0) * D_ + d;
   float gd = 0.0f;
   if constexpr (kLC > 0) {
+    // dA and dBx first (the forward aggregate), then C, gy and x (the reverse
+    // one and the sum): at most about 64 loaded values live at once
     float a[kLC], v[kLC], cv[kLC], yv[kLC], xv[kLC];
 #pragma unroll
     for (int j = 0; j < kLC; ++j) {
@@ -1216,9 +1256,6 @@ diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx
       const int64_t i = first + (int64_t)(in ? j : 0) * D_;
       a[j] = in ? dA[i] : 1.0f;
       v[j] = in ? dBx[i] : 0.0f;
-      cv[j] = in ? C[i] : 0.0f;
-      yv[j] = in ? gy[i] : 0.0f;
-      xv[j] = in ? x[i] : 0.0f;
     }
     if (k + 1 < nchunks) {
       float P = 1.0f, S = 0.0f;
@@ -1229,6 +1266,14 @@ diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx
       }
       fwd_agg[first] = P;
       fwd_agg[first + D_] = S;
+    }
+#pragma unroll
+    for (int j = 0; j < kLC; ++j) {
+      const bool in = j < n;
+      const int64_t i = first + (int64_t)(in ? j : 0) * D_;
+      cv[j] = in ? C[i] : 0.0f;
+      yv[j] = in ? gy[i] : 0.0f;
+      xv[j] = in ? x[i] : 0.0f;
     }
     float c = 0.0f, Q = 1.0f;
 #pragma unroll
@@ -1273,10 +1318,13 @@ diag_bwd_aggs_kernel(const float* __restrict__ dA, const float* __restrict__ dBx
 }
 
 // Per (batch, channel): the chunks' sums of gy x added in chunk order (into
-// part), then the forward state entering each chunk (over those sums, in
+// part), the forward state entering each chunk (over those sums, in
 // grad_dBx's first rows) and the adjoint carried into each chunk from the
-// right (over Q in grad_dA's first rows). sx is read (sums) before it is
-// written (states) through the one pointer.
+// right (over Q in grad_dA's first rows). Each round loads 16 chunks' worth
+// of all three walks (the forward ones from the left, the reverse one from
+// the right) before any of their rows is written, so the three dependent
+// chains share their load latency; sx is read (sums) before it is written
+// (states) through the one pointer.
 __global__ void __launch_bounds__(256)
 diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* sx, float* __restrict__ q_c,
                         const float* __restrict__ g_agg, float* __restrict__ part, int batch,
@@ -1288,52 +1336,39 @@ diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* sx, float* __r
   constexpr int kG = 16;
   const int64_t base = (int64_t)b * seqlen * d_inner + d;
   const int64_t cs = (int64_t)lc * d_inner;
-  float gd = 0.0f;
-  for (int k0 = 0; k0 < nchunks; k0 += kG) {
-    float G[kG];
-#pragma unroll
-    for (int i = 0; i < kG; ++i) G[i] = sx[base + min(k0 + i, nchunks - 1) * cs];
-#pragma unroll
-    for (int i = 0; i < kG; ++i)
-      if (k0 + i < nchunks) gd += G[i];
-  }
-  part[gid] = gd;
-  float s = 0.0f;
-  for (int k0 = 0; k0 + 1 < nchunks; k0 += kG) {
-    float P[kG], S[kG];
+  float gd = 0.0f, s = 0.0f, c = 0.0f;
+  for (int r0 = 0; r0 < nchunks; r0 += kG) {
+    // forward walk: chunks r0 .. r0 + 15; reverse walk: chunks
+    // nchunks - 1 - r0 down to nchunks - 16 - r0 (chunk 0 takes no Q / G)
+    float G[kG], P[kG], S[kG], Q[kG], R[kG];
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      const int k = min(k0 + i, nchunks - 2);
-      P[i] = fwd_agg[base + k * cs];
-      S[i] = fwd_agg[base + k * cs + d_inner];
+      const int kf = min(r0 + i, nchunks - 1);
+      const int kp = min(r0 + i, max(nchunks - 2, 0));
+      const int kr = max(nchunks - 1 - r0 - i, 1);
+      G[i] = sx[base + kf * cs];
+      P[i] = fwd_agg[base + kp * cs];
+      S[i] = fwd_agg[base + kp * cs + d_inner];
+      Q[i] = q_c[base + kr * cs];
+      R[i] = g_agg[base + kr * cs];
     }
 #pragma unroll
     for (int i = 0; i < kG; ++i) {
-      if (k0 + i + 1 < nchunks) {
-        sx[base + (k0 + i) * cs] = s;
-        s = fmaf(P[i], s, S[i]);
+      const int kf = r0 + i;
+      if (kf < nchunks) {
+        gd += G[i];
+        sx[base + kf * cs] = s;  // the state entering chunk kf
+        if (kf + 1 < nchunks) s = fmaf(P[i], s, S[i]);
       }
-    }
-  }
-  sx[base + (int64_t)(nchunks - 1) * cs] = s;
-  float c = 0.0f;
-  for (int k0 = nchunks - 1; k0 >= 1; k0 -= kG) {
-    float Q[kG], G[kG];
-#pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      const int k = max(k0 - i, 1);
-      Q[i] = q_c[base + k * cs];
-      G[i] = g_agg[base + k * cs];
-    }
-#pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      if (k0 - i >= 1) {
-        q_c[base + (k0 - i) * cs] = c;
-        c = fmaf(Q[i], c, G[i]);
+      const int kr = nchunks - 1 - r0 - i;
+      if (kr >= 1) {
+        q_c[base + kr * cs] = c;  // the adjoint carried into chunk kr
+        c = fmaf(Q[i], c, R[i]);
       }
     }
   }
   q_c[base] = c;
+  part[gid] = gd;
 }
 
 template <int kLC>
@@ -2137,7 +2172,11 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const int64_t lanes = batch * d_inner;
   hipStream_t s = ak_stream(stream);
   // chunks when (batch, channel) lanes alone leave the GPU idle
-  const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
+  // Chunks of at most 32 steps keep their rows in registers; the plan for
+  // them aims at 2^19 lanes (at AMADEUS's shape 64 chunks of 16 steps),
+  // otherwise at 2^18 with streaming chunks.
+  int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 19);
+  if (nchunks > 1 && (seqlen + nchunks - 1) / nchunks > 32) nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
   if (nchunks <= 1) {
     const unsigned grid = (unsigned)((lanes + 255) / 256);
     ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch, (int)seqlen,
@@ -2149,12 +2188,18 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const unsigned g1 = (unsigned)((batch * (nc - 1) * d_inner + 255) / 256);
   const unsigned g2 = (unsigned)((lanes + 255) / 256);
   const unsigned g3 = (unsigned)((batch * nc * d_inner + 255) / 256);
-  ak::diag_scan_chunk_agg_kernel<<<dim3(g1), dim3(256), 0, s>>>(dA, dBx, y, (int)batch, (int)seqlen,
-                                                               (int)d_inner, lc, nc);
-  ak::diag_scan_chunk_carry_kernel<<<dim3(g2), dim3(256), 0, s>>>(y, (int)batch, (int)seqlen, (int)d_inner,
-                                                                 lc, nc);
-  ak::diag_scan_chunk_out_kernel<<<dim3(g3), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch,
-                                                               (int)seqlen, (int)d_inner, lc, nc);
+  auto run = [&](auto lc_tag) {
+    constexpr int kLC = decltype(lc_tag)::value;
+    ak::diag_scan_chunk_agg_kernel<kLC><<<dim3(g1), dim3(256), 0, s>>>(dA, dBx, y, (int)batch, (int)seqlen,
+                                                                      (int)d_inner, lc, nc);
+    ak::diag_scan_chunk_carry_kernel<<<dim3(g2), dim3(256), 0, s>>>(y, (int)batch, (int)seqlen, (int)d_inner,
+                                                                   lc, nc);
+    ak::diag_scan_chunk_out_kernel<kLC><<<dim3(g3), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch,
+                                                                      (int)seqlen, (int)d_inner, lc, nc);
+  };
+  if (lc <= 16) run(std::integral_constant<int, 16>{});
+  else if (lc <= 32) run(std::integral_constant<int, 32>{});
+  else run(std::integral_constant<int, 0>{});
   return ak_check_launch(name);
 }
 
