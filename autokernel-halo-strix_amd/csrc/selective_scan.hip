@@ -1041,10 +1041,12 @@ diag_scan_chunk_carry_kernel(float* __restrict__ y, int batch, int seqlen, int d
 }
 
 // Chunks for the diagonal scan: enough for about 2^lanes_log2 lanes in all,
-// at most 64, at least 16 steps each; 1 means the sequential kernels. At
-// AMADEUS's shape ([16, 1024, 384]) the forward measured fastest with 2^18
-// lanes (41 against 46 us with 2^17, the same with 2^19) and the backward with
-// 2^17 (124 us, 137 with 2^19).
+// at most 64, at least 16 steps each; 1 means the sequential kernels. Both
+// directions first try 2^19 lanes and take that plan when its chunks have at
+// most 32 steps (they are then held in registers); otherwise the forward
+// streams with 2^18 and the backward with 2^17, the fastest streaming plans
+// at AMADEUS's shape ([16, 1024, 384]: forward 41 against 46 us with 2^17,
+// backward 124 against 137 us with 2^19).
 inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner, int lanes_log2) {
   const int64_t lanes = batch * d_inner;
   const int64_t want = ((int64_t)1 << lanes_log2);
