@@ -1042,11 +1042,11 @@ diag_scan_chunk_carry_kernel(float* __restrict__ y, int batch, int seqlen, int d
 
 // Chunks for the diagonal scan: enough for about 2^lanes_log2 lanes in all,
 // at most 64, at least 16 steps each; 1 means the sequential kernels. Both
-// directions first try 2^19 lanes and take that plan when its chunks have at
-// most 32 steps (they are then held in registers); otherwise the forward
-// streams with 2^18 and the backward with 2^17, the fastest streaming plans
-// at AMADEUS's shape ([16, 1024, 384]: forward 41 against 46 us with 2^17,
-// backward 124 against 137 us with 2^19).
+// directions aim at 2^18 lanes; chunks of at most 32 steps are held in
+// registers. The backward falls back to 2^17 for chunks that stream (at
+// AMADEUS's shape [16, 1024, 384], streaming: backward 124 against 137 us
+// with 2^19; registers: 43 chunks of 24 steps ran 1-2% faster than 64 of 16
+// in both directions).
 inline int diag_chunks(int64_t batch, int64_t seqlen, int64_t d_inner, int lanes_log2) {
   const int64_t lanes = batch * d_inner;
   const int64_t want = ((int64_t)1 << lanes_log2);
@@ -2174,11 +2174,9 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   const int64_t lanes = batch * d_inner;
   hipStream_t s = ak_stream(stream);
   // chunks when (batch, channel) lanes alone leave the GPU idle
-  // Chunks of at most 32 steps keep their rows in registers; the plan for
-  // them aims at 2^19 lanes (at AMADEUS's shape 64 chunks of 16 steps),
-  // otherwise at 2^18 with streaming chunks.
-  int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 19);
-  if (nchunks > 1 && (seqlen + nchunks - 1) / nchunks > 32) nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
+  // about 2^18 lanes (at AMADEUS's shape 43 chunks of 24 steps, held in
+  // registers; chunks of more than 32 steps stream)
+  const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
   if (nchunks <= 1) {
     const unsigned grid = (unsigned)((lanes + 255) / 256);
     ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch, (int)seqlen,
@@ -2235,9 +2233,9 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
   // Chunks of at most 32 steps keep their rows in registers; the plan for
-  // them aims at 2^19 lanes (at AMADEUS's shape 64 chunks of 16 steps),
+  // them aims at 2^18 lanes (at AMADEUS's shape 43 chunks of 24 steps),
   // otherwise at 2^17 with streaming chunks.
-  int nc = ak::diag_chunks(batch, seqlen, d_inner, 19);
+  int nc = ak::diag_chunks(batch, seqlen, d_inner, 18);
   int lc = nc > 1 ? (int)((seqlen + nc - 1) / nc) : 0;
   if (nc > 1 && lc > 32) {
     nc = ak::diag_chunks(batch, seqlen, d_inner, 17);

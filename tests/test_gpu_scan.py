@@ -313,15 +313,17 @@ def test_diag_scan_backward(shp):
 
 
 @pytest.mark.parametrize("shp", [(1, 32, 3), (1, 33, 1), (3, 100, 7), (2, 1000, 33), (1, 5000, 8),
-                                 (16, 1024, 384), (2, 31, 5), (512, 64, 384), (4, 2000, 48)])
+                                 (16, 1024, 384), (2, 31, 5), (512, 64, 384), (4, 2000, 48),
+                                 (8, 256, 64)])
 def test_diag_scan_chunk_plans(shp):
     """The diagonal scan's chunk plans at their edges, forward and backward
     against the float64 oracle: the smallest chunked lengths (32, 33 steps),
     a short last chunk (1000 = 58 x 17 + 14), the 64-chunk cap (5000 steps),
     AMADEUS's width, and shapes that stay sequential (31 steps; 2^17 lanes).
-    The backward keeps chunks of up to 16 steps in registers ((1, 32, 3),
-    AMADEUS), 17-32 steps in the 32-step register kernels (33, 100, 1000 and
-    2000 = 62 x 32 + 16 steps) and streams longer ones (5000 steps)."""
+    Chunks of up to 16 steps are held in the 16-step register kernels
+    ((1, 32, 3), (8, 256, 64)), 17-32 steps in the 32-step ones (33, 100 and
+    1000 steps, AMADEUS's 43 x 24 = 42 x 24 + 16, 2000 = 62 x 32 + 16), and
+    longer chunks stream (5000 steps)."""
     need_gpu()
     from kernels.hip import selective_scan, selective_scan_backward
     g = torch.Generator().manual_seed(sum(shp) + 5)
