@@ -1098,6 +1098,97 @@ diag_scan_chunk_out_kernel(const float* __restrict__ dA, const float* __restrict
   }
 }
 
+// One launch for the whole forward when the sequence has at most 1024 steps
+// and the (batch, channel) lanes are few: a workgroup takes 32 channels of
+// one batch row (128-byte row segments) and cuts the sequence into nck
+// chunks of at most 32 steps, one thread per (chunk, channel). Each thread
+// holds its chunk's dA and dBx in registers and forms the chunk's decay
+// product P and state from zero S; the chunks' (P, S) meet in LDS, where one
+// thread per channel walks them in order (s_k = P_{k-1} s_{k-1} + S_{k-1}),
+// and every thread then runs its rows from its entering state, reading C and
+// x in two halves. (Loading the first half during the carry, or C and x in
+// four groups of 8 rows one group ahead, measured 1 and 17% slower.) Inputs are read once and y written once, with no scratch
+// in HBM; the states differ from the sequential ones by rounding only.
+constexpr int kDiagWgCh = 32;  // channels per workgroup
+// 32-bit byte offsets from an array's base (the workgroup paths require
+// batch * seqlen * d_inner * 4 < 2^32): the base stays in scalar registers
+// and one offset register per row serves every array.
+__device__ __forceinline__ float ld_at(const float* __restrict__ p, uint32_t e) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p) + 4u * e);
+}
+__device__ __forceinline__ void st_at(float* __restrict__ p, uint32_t e, float v) {
+  *reinterpret_cast<float*>(reinterpret_cast<char*>(p) + 4u * e) = v;
+}
+constexpr int kDiagWgLC = 32;  // steps per chunk at most
+
+__global__ void __launch_bounds__(1024)
+diag_scan_wg_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                    const float* __restrict__ C, const float* __restrict__ D,
+                    const float* __restrict__ x, float* __restrict__ y, int batch, int seqlen,
+                    int d_inner, int lc, int nck) {
+  __shared__ float sP[kDiagWgLC][kDiagWgCh + 1], sS[kDiagWgLC][kDiagWgCh + 1];
+  const int c = threadIdx.x % kDiagWgCh;
+  const int k = threadIdx.x / kDiagWgCh;  // chunk (< nck <= 32)
+  const int dblocks = (d_inner + kDiagWgCh - 1) / kDiagWgCh;
+  const int b = blockIdx.x / dblocks;
+  const int d = (blockIdx.x % dblocks) * kDiagWgCh + c;
+  const bool live = d < d_inner;
+  const int t0 = k * lc;
+  const int n = live ? max(0, min(lc, seqlen - t0)) : 0;
+  const uint32_t D_ = (uint32_t)d_inner;
+  const uint32_t base = ((uint32_t)b * (uint32_t)seqlen + (uint32_t)min(t0, seqlen - 1)) * D_ + (uint32_t)(live ? d : 0);
+  float a[kDiagWgLC], v[kDiagWgLC];
+#pragma unroll
+  for (int j = 0; j < kDiagWgLC; ++j) {
+    const bool in = j < n;
+    const uint32_t i = base + (uint32_t)(in ? j : 0) * D_;
+    a[j] = in ? ld_at(dA, i) : 1.0f;
+    v[j] = in ? ld_at(dBx, i) : 0.0f;
+  }
+  {
+    float P = 1.0f, S = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDiagWgLC; ++j) {
+      S = fmaf(a[j], S, v[j]);
+      P *= a[j];
+    }
+    sP[k][c] = P;
+    sS[k][c] = S;
+  }
+  __syncthreads();
+  if (k == 0) {
+    // the state entering each chunk, over its S
+    float s = 0.0f;
+    for (int kk = 0; kk < nck; ++kk) {
+      const float P = sP[kk][c], S = sS[kk][c];
+      sS[kk][c] = s;
+      s = fmaf(P, s, S);
+    }
+  }
+  __syncthreads();
+  float s = sS[k][c];
+  const float dd = live ? D[d] : 0.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    constexpr int kH = kDiagWgLC / 2;
+    float cv[kH], xv[kH];
+#pragma unroll
+    for (int j = 0; j < kH; ++j) {
+      const int jj = h * kH + j;
+      const bool in = jj < n;
+      const uint32_t i = base + (uint32_t)(in ? jj : 0) * D_;
+      cv[j] = in ? ld_at(C, i) : 0.0f;
+      xv[j] = in ? ld_at(x, i) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kH; ++j) {
+      const int jj = h * kH + j;
+      s = fmaf(a[jj], s, v[jj]);
+      if (jj < n) st_at(y, base + (uint32_t)jj * D_, fmaf(cv[j], s, dd * xv[j]));
+    }
+  }
+}
+
 // Backward of the diagonal recurrence (the gradient of the reference's
 // sequential formula, kernels/hip/_torch_ops.py:346-386, and of its HIP
 // kernel kernels/hip/selective_scan_backward.py:72-311), one lane per
@@ -2177,6 +2268,15 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   // about 2^18 lanes (at AMADEUS's shape 43 chunks of 24 steps, held in
   // registers; chunks of more than 32 steps stream)
   const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
+  if (nchunks > 1 && seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && batch * seqlen * d_inner < ((int64_t)1 << 30)) {
+    // one launch: every chunk of 32 channels in one workgroup
+    const int nck = (int)((seqlen + ak::kDiagWgLC - 1) / ak::kDiagWgLC);
+    const int lc = (int)((seqlen + nck - 1) / nck);
+    const unsigned grid = (unsigned)(batch * ((d_inner + ak::kDiagWgCh - 1) / ak::kDiagWgCh));
+    ak::diag_scan_wg_kernel<<<dim3(grid), dim3(ak::kDiagWgCh * nck), 0, s>>>(
+        dA, dBx, C, D, x, y, (int)batch, (int)seqlen, (int)d_inner, lc, nck);
+    return ak_check_launch(name);
+  }
   if (nchunks <= 1) {
     const unsigned grid = (unsigned)((lanes + 255) / 256);
     ak::diag_scan_kernel<<<dim3(grid), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch, (int)seqlen,

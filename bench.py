@@ -325,7 +325,7 @@ def make_case(name):
             launch = lambda st: _lib.diag_scan(st["dA"], st["dBx"], st["C"], st["D"], st["x"], st["y"])
             return Case(name, "Diagonal scan fp32 [16, 1024, 384] (AMADEUS's SSM width)", "hbm", DIAG_BYTES,
                         16 * 1024, launch, sets,
-                        "diag_scan_chunk_agg_kernel + diag_scan_chunk_carry_kernel + diag_scan_chunk_out_kernel")
+                        "diag_scan_wg_kernel (one launch, 32 channels per workgroup)")
         launch = lambda st: _lib.diag_scan_bwd(st["dA"], st["dBx"], st["C"], st["D"], st["x"], st["gy"],
                                                st["grads"][0], st["grads"][1], st["grads"][2], st["grads"][4],
                                                st["grads"][3])

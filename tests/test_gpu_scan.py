@@ -320,10 +320,12 @@ def test_diag_scan_chunk_plans(shp):
     against the float64 oracle: the smallest chunked lengths (32, 33 steps),
     a short last chunk (1000 = 58 x 17 + 14), the 64-chunk cap (5000 steps),
     AMADEUS's width, and shapes that stay sequential (31 steps; 2^17 lanes).
-    Chunks of up to 16 steps are held in the 16-step register kernels
+    The forward takes one launch up to 1024 steps (every chunked shape here
+    but the 2000- and 5000-step ones, which run its chunked passes). The
+    backward holds chunks of up to 16 steps in the 16-step register kernels
     ((1, 32, 3), (8, 256, 64)), 17-32 steps in the 32-step ones (33, 100 and
     1000 steps, AMADEUS's 43 x 24 = 42 x 24 + 16, 2000 = 62 x 32 + 16), and
-    longer chunks stream (5000 steps)."""
+    streams longer chunks (5000 steps)."""
     need_gpu()
     from kernels.hip import selective_scan, selective_scan_backward
     g = torch.Generator().manual_seed(sum(shp) + 5)
