@@ -1464,6 +1464,110 @@ diag_bwd_carries_kernel(const float* __restrict__ fwd_agg, float* sx, float* __r
   part[gid] = gd;
 }
 
+// Both aggregates and all three carries of the chunked backward in one
+// launch, for sequences of at most 1024 steps: the layout of
+// diag_scan_wg_kernel (32 channels of one batch row per workgroup, one thread
+// per (chunk of at most 32 steps, channel)). Per thread, the arithmetic of
+// diag_bwd_aggs_kernel<32> in its order (dA and dBx first; then C, gy and x
+// from the top half down, which continues the reverse walk and the gy x sum
+// across the halves); then in LDS one thread per channel walks the forward
+// states, one the adjoints and one the gy x sums, as diag_bwd_carries_kernel
+// does. The entering state goes to the chunk's first grad_dBx row, the
+// adjoint to its first grad_dA row and the channel's sum of gy x to the
+// grad_D workspace: what diag_bwd_chunk_kernel<32> then reads.
+__global__ void __launch_bounds__(1024)
+diag_bwd_wg_carry_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
+                         const float* __restrict__ C, const float* __restrict__ gy,
+                         const float* __restrict__ x, float* __restrict__ s_in,
+                         float* __restrict__ c_in, float* __restrict__ part, int batch,
+                         int seqlen, int d_inner, int lc, int nck) {
+  constexpr int kW = kDiagWgCh + 1;
+  __shared__ float sP[kDiagWgLC][kW], sS[kDiagWgLC][kW], sQ[kDiagWgLC][kW], sG[kDiagWgLC][kW],
+      sX[kDiagWgLC][kW];
+  constexpr int kH = kDiagWgLC / 2;
+  const int c = threadIdx.x % kDiagWgCh;
+  const int k = threadIdx.x / kDiagWgCh;  // chunk (< nck <= 32)
+  const int dblocks = (d_inner + kDiagWgCh - 1) / kDiagWgCh;
+  const int b = blockIdx.x / dblocks;
+  const int d = (blockIdx.x % dblocks) * kDiagWgCh + c;
+  const bool live = d < d_inner;
+  const int t0 = k * lc;
+  const int n = live ? max(0, min(lc, seqlen - t0)) : 0;
+  const uint32_t D_ = (uint32_t)d_inner;
+  const uint32_t base = ((uint32_t)b * (uint32_t)seqlen + (uint32_t)min(t0, seqlen - 1)) * D_ + (uint32_t)(live ? d : 0);
+  float a[kDiagWgLC];
+  {
+    float v[kDiagWgLC];
+#pragma unroll
+    for (int j = 0; j < kDiagWgLC; ++j) {
+      const bool in = j < n;
+      const uint32_t i = base + (uint32_t)(in ? j : 0) * D_;
+      a[j] = in ? ld_at(dA, i) : 1.0f;
+      v[j] = in ? ld_at(dBx, i) : 0.0f;
+    }
+    float P = 1.0f, S = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDiagWgLC; ++j) {
+      S = fmaf(a[j], S, v[j]);
+      P *= a[j];
+    }
+    sP[k][c] = P;
+    sS[k][c] = S;
+  }
+  float cc = 0.0f, Q = 1.0f, gd = 0.0f;
+  auto rev_half = [&](auto h_tag) {
+    constexpr int h = decltype(h_tag)::value;
+    float cv[kH], yv[kH], xv[kH];
+#pragma unroll
+    for (int j = 0; j < kH; ++j) {
+      const int jj = h * kH + j;
+      const bool in = jj < n;
+      const uint32_t i = base + (uint32_t)(in ? jj : 0) * D_;
+      cv[j] = in ? ld_at(C, i) : 0.0f;
+      yv[j] = in ? ld_at(gy, i) : 0.0f;
+      xv[j] = in ? ld_at(x, i) : 0.0f;
+    }
+#pragma unroll
+    for (int j = kH - 1; j >= 0; --j) {
+      cc = fmaf(yv[j], cv[j], cc) * a[h * kH + j];
+      Q *= a[h * kH + j];
+      gd = fmaf(yv[j], xv[j], gd);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  rev_half(std::integral_constant<int, 1>{});
+  rev_half(std::integral_constant<int, 0>{});
+  sQ[k][c] = Q;
+  sG[k][c] = cc;
+  sX[k][c] = gd;
+  __syncthreads();
+  const uint32_t first = base;  // the chunk's first row (chunks past the end have no rows)
+  if (k == 0) {
+    float s = 0.0f, g = 0.0f;
+    for (int kk = 0; kk < nck; ++kk) {
+      g += sX[kk][c];
+      const float P = sP[kk][c], S = sS[kk][c];
+      sS[kk][c] = s;  // the state entering chunk kk
+      s = fmaf(P, s, S);
+    }
+    if (live) part[(int64_t)b * d_inner + d] = g;
+  }
+  if (k == (nck > 2 ? 2 : 0)) {
+    float ca = 0.0f;
+    for (int kk = nck - 1; kk >= 1; --kk) {
+      const float Qk = sQ[kk][c], Gk = sG[kk][c];
+      sG[kk][c] = ca;  // the adjoint entering chunk kk from the right
+      ca = fmaf(Qk, ca, Gk);
+    }
+    sG[0][c] = ca;
+  }
+  __syncthreads();
+  if (n > 0) {
+    st_at(s_in, first, sS[k][c]);
+    st_at(c_in, first, sG[k][c]);
+  }
+}
+
 template <int kLC>
 __global__ void __launch_bounds__(256)
 diag_bwd_chunk_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
@@ -2346,6 +2450,22 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
     const int B_ = (int)batch, L_ = (int)seqlen, D_ = (int)d_inner;
     const unsigned g_lane = (unsigned)((lanes + 255) / 256);
     const unsigned g_all = (unsigned)((batch * ncs * d_inner + 255) / 256);
+    if (seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && batch * seqlen * d_inner < ((int64_t)1 << 30)) {
+      // aggregates and carries in one launch (its own plan: at most 32 chunks
+      // of at most 32 steps), then the 32-step sweep on the same chunks
+      const int nck = (int)((seqlen + ak::kDiagWgLC - 1) / ak::kDiagWgLC);
+      const int lcw = (int)((seqlen + nck - 1) / nck);
+      const int ncw = (int)((seqlen + lcw - 1) / lcw);
+      const unsigned grid = (unsigned)(batch * ((d_inner + ak::kDiagWgCh - 1) / ak::kDiagWgCh));
+      ak::diag_bwd_wg_carry_kernel<<<dim3(grid), dim3(ak::kDiagWgCh * nck), 0, s>>>(
+          dA, dBx, C, grad_y, x, grad_dBx, grad_dA, part, B_, L_, D_, lcw, nck);
+      const unsigned g_w = (unsigned)((batch * ncw * d_inner + 255) / 256);
+      ak::diag_bwd_chunk_kernel<32><<<dim3(g_w), dim3(256), 0, s>>>(
+          dA, dBx, C, D, grad_y, grad_dA, grad_dBx, grad_C, grad_x, B_, L_, D_, lcw, ncw);
+      ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
+          part, grad_D, B_, D_);
+      return ak_check_launch(name);
+    }
     auto run = [&](auto lc_tag) {
       constexpr int kLC = decltype(lc_tag)::value;
       ak::diag_bwd_aggs_kernel<kLC><<<dim3(g_all), dim3(256), 0, s>>>(

@@ -330,7 +330,7 @@ def make_case(name):
                                                st["grads"][0], st["grads"][1], st["grads"][2], st["grads"][4],
                                                st["grads"][3])
         return Case(name, "Diagonal scan backward fp32 [16, 1024, 384]", "hbm", DIAGB_BYTES, 16 * 1024, launch,
-                    sets, "chunked diagonal-scan backward (4 launches)")
+                    sets, "diag_bwd_wg_carry_kernel + diag_bwd_chunk_kernel<32> + diag_scan_gd_kernel")
     if name == "c5b":
         cpu = gen_c5()
         cpu["dout"] = torch.randn(cpu["u"].shape, generator=torch.Generator().manual_seed(2)).bfloat16()

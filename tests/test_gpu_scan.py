@@ -320,12 +320,12 @@ def test_diag_scan_chunk_plans(shp):
     against the float64 oracle: the smallest chunked lengths (32, 33 steps),
     a short last chunk (1000 = 58 x 17 + 14), the 64-chunk cap (5000 steps),
     AMADEUS's width, and shapes that stay sequential (31 steps; 2^17 lanes).
-    The forward takes one launch up to 1024 steps (every chunked shape here
-    but the 2000- and 5000-step ones, which run its chunked passes). The
-    backward holds chunks of up to 16 steps in the 16-step register kernels
-    ((1, 32, 3), (8, 256, 64)), 17-32 steps in the 32-step ones (33, 100 and
-    1000 steps, AMADEUS's 43 x 24 = 42 x 24 + 16, 2000 = 62 x 32 + 16), and
-    streams longer chunks (5000 steps)."""
+    Up to 1024 steps (every chunked shape here but the 2000- and 5000-step
+    ones) the forward takes one launch and the backward its workgroup carry
+    kernel and the 32-step sweep (AMADEUS: 32 chunks of 32 steps; 1000 = 31 x
+    32 + 8). Longer sequences run the chunked passes: chunks of 17-32 steps in
+    the 32-step register kernels (2000 = 62 x 32 + 16), longer ones streaming
+    (5000 steps)."""
     need_gpu()
     from kernels.hip import selective_scan, selective_scan_backward
     g = torch.Generator().manual_seed(sum(shp) + 5)
