@@ -2401,8 +2401,9 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
     ak::diag_scan_chunk_out_kernel<kLC><<<dim3(g3), dim3(256), 0, s>>>(dA, dBx, C, D, x, y, (int)batch,
                                                                       (int)seqlen, (int)d_inner, lc, nc);
   };
-  if (lc <= 16) run(std::integral_constant<int, 16>{});
-  else if (lc <= 32) run(std::integral_constant<int, 32>{});
+  // (chunks of at most 16 steps arise only for sequences of at most 1024
+  // steps, which take the one-launch kernel)
+  if (lc <= 32) run(std::integral_constant<int, 32>{});
   else run(std::integral_constant<int, 0>{});
   return ak_check_launch(name);
 }
@@ -2475,8 +2476,9 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
       ak::diag_bwd_chunk_kernel<kLC><<<dim3(g_all), dim3(256), 0, s>>>(
           dA, dBx, C, D, grad_y, grad_dA, grad_dBx, grad_C, grad_x, B_, L_, D_, lc, ncs);
     };
-    if (lc <= 16) run(std::integral_constant<int, 16>{});
-    else if (lc <= 32) run(std::integral_constant<int, 32>{});
+    // (chunks of at most 16 steps arise only for sequences of at most 1024
+    // steps, which take the workgroup carry kernel)
+    if (lc <= 32) run(std::integral_constant<int, 32>{});
     else run(std::integral_constant<int, 0>{});
     ak::diag_scan_gd_kernel<<<dim3((unsigned)((d_inner + 255) / 256)), dim3(256), 0, s>>>(
         part, grad_D, B_, D_);
