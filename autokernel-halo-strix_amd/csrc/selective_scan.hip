@@ -1106,10 +1106,13 @@ diag_scan_chunk_out_kernel(const float* __restrict__ dA, const float* __restrict
 // product P and state from zero S; the chunks' (P, S) meet in LDS, where one
 // thread per channel walks them in order (s_k = P_{k-1} s_{k-1} + S_{k-1}),
 // and every thread then runs its rows from its entering state, reading C and
-// x in two halves. (Loading the first half during the carry, or C and x in
-// four groups of 8 rows one group ahead, measured 1 and 17% slower.) Inputs are read once and y written once, with no scratch
+// x in two halves. Inputs are read once and y written once, with no scratch
 // in HBM; the states differ from the sequential ones by rounding only.
+// (Loading the first half during the carry, or C and x in four groups of 8
+// rows one group ahead, measured 1% and 17% slower.)
 constexpr int kDiagWgCh = 32;  // channels per workgroup
+constexpr int kDiagWgLC = 32;  // steps per chunk at most (and chunks at most)
+
 // 32-bit byte offsets from an array's base (the workgroup paths require
 // batch * seqlen * d_inner * 4 < 2^32): the base stays in scalar registers
 // and one offset register per row serves every array.
@@ -1119,7 +1122,6 @@ __device__ __forceinline__ float ld_at(const float* __restrict__ p, uint32_t e) 
 __device__ __forceinline__ void st_at(float* __restrict__ p, uint32_t e, float v) {
   *reinterpret_cast<float*>(reinterpret_cast<char*>(p) + 4u * e) = v;
 }
-constexpr int kDiagWgLC = 32;  // steps per chunk at most
 
 __global__ void __launch_bounds__(1024)
 diag_scan_wg_kernel(const float* __restrict__ dA, const float* __restrict__ dBx,
