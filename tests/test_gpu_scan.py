@@ -314,7 +314,7 @@ def test_diag_scan_backward(shp):
 
 @pytest.mark.parametrize("shp", [(1, 32, 3), (1, 33, 1), (3, 100, 7), (2, 1000, 33), (1, 5000, 8),
                                  (16, 1024, 384), (2, 31, 5), (512, 64, 384), (4, 2000, 48),
-                                 (8, 256, 64)])
+                                 (8, 256, 64), (2, 777, 1000)])
 def test_diag_scan_chunk_plans(shp):
     """The diagonal scan's chunk plans at their edges, forward and backward
     against the float64 oracle: the smallest chunked lengths (32, 33 steps),
@@ -323,7 +323,8 @@ def test_diag_scan_chunk_plans(shp):
     Up to 1024 steps (every chunked shape here but the 2000- and 5000-step
     ones) the forward takes one launch and the backward its workgroup carry
     kernel and the 32-step sweep (AMADEUS: 32 chunks of 32 steps; 1000 = 31 x
-    32 + 8). Longer sequences run the chunked passes: chunks of 17-32 steps in
+    32 + 8; 777 = 24 x 32 + 9 steps over 1000 channels, whose last block of 32
+    holds 8). Longer sequences run the chunked passes: chunks of 17-32 steps in
     the 32-step register kernels (2000 = 62 x 32 + 16), longer ones streaming
     (5000 steps)."""
     need_gpu()
