@@ -2370,9 +2370,10 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   if (batch * seqlen * d_inner >= ((int64_t)1 << 62)) return ak_set_error(AK_ERR_INVALID_ARG, "%s: shape too large", name);
   const int64_t lanes = batch * d_inner;
   hipStream_t s = ak_stream(stream);
-  // chunks when (batch, channel) lanes alone leave the GPU idle
-  // about 2^18 lanes (at AMADEUS's shape 43 chunks of 24 steps, held in
-  // registers; chunks of more than 32 steps stream)
+  // chunks when (batch, channel) lanes alone leave the GPU idle (about 2^18
+  // lanes in all). Up to 1024 steps one workgroup per 32 channels holds all
+  // of a row's chunks (AMADEUS's shape); longer sequences take the chunked
+  // passes, chunks of at most 32 steps in registers, longer ones streaming.
   const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
   if (nchunks > 1 && seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && batch * seqlen * d_inner < ((int64_t)1 << 30)) {
     // one launch: every chunk of 32 channels in one workgroup
@@ -2439,9 +2440,10 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
                         workspace_bytes, ak_diag_scan_bwd_workspace_bytes(batch, d_inner));
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
-  // Chunks of at most 32 steps keep their rows in registers; the plan for
-  // them aims at 2^18 lanes (at AMADEUS's shape 43 chunks of 24 steps),
-  // otherwise at 2^17 with streaming chunks.
+  // Chunks when (batch, channel) lanes alone leave the GPU idle. Up to 1024
+  // steps the workgroup carry kernel and the 32-step sweep (AMADEUS's shape);
+  // longer sequences take the chunked passes, with chunks of at most 32 steps
+  // in registers (a plan for about 2^18 lanes) or else streaming (2^17).
   int nc = ak::diag_chunks(batch, seqlen, d_inner, 18);
   int lc = nc > 1 ? (int)((seqlen + nc - 1) / nc) : 0;
   if (nc > 1 && lc > 32) {
