@@ -2372,10 +2372,12 @@ extern "C" int ak_diag_scan_fwd(const float* dA, const float* dBx, const float* 
   hipStream_t s = ak_stream(stream);
   // chunks when (batch, channel) lanes alone leave the GPU idle (about 2^18
   // lanes in all). Up to 1024 steps one workgroup per 32 channels holds all
-  // of a row's chunks (AMADEUS's shape); longer sequences take the chunked
-  // passes, chunks of at most 32 steps in registers, longer ones streaming.
+  // of a row's chunks (AMADEUS's shape; not below 16 channels, where most of
+  // its threads would idle); otherwise the chunked passes, chunks of at most
+  // 32 steps in registers, longer ones streaming.
   const int nchunks = ak::diag_chunks(batch, seqlen, d_inner, 18);
-  if (nchunks > 1 && seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && batch * seqlen * d_inner < ((int64_t)1 << 30)) {
+  if (nchunks > 1 && seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && d_inner >= ak::kDiagWgCh / 2 &&
+      batch * seqlen * d_inner < ((int64_t)1 << 30)) {
     // one launch: every chunk of 32 channels in one workgroup
     const int nck = (int)((seqlen + ak::kDiagWgLC - 1) / ak::kDiagWgLC);
     const int lc = (int)((seqlen + nck - 1) / nck);
@@ -2441,9 +2443,10 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
   float* part = static_cast<float*>(workspace);
   const int64_t lanes = batch * d_inner;
   // Chunks when (batch, channel) lanes alone leave the GPU idle. Up to 1024
-  // steps the workgroup carry kernel and the 32-step sweep (AMADEUS's shape);
-  // longer sequences take the chunked passes, with chunks of at most 32 steps
-  // in registers (a plan for about 2^18 lanes) or else streaming (2^17).
+  // steps and from 16 channels the workgroup carry kernel and the 32-step
+  // sweep (AMADEUS's shape); otherwise the chunked passes, with chunks of at
+  // most 32 steps in registers (a plan for about 2^18 lanes) or else
+  // streaming (2^17).
   int nc = ak::diag_chunks(batch, seqlen, d_inner, 18);
   int lc = nc > 1 ? (int)((seqlen + nc - 1) / nc) : 0;
   if (nc > 1 && lc > 32) {
@@ -2455,7 +2458,8 @@ extern "C" int ak_diag_scan_bwd(const float* dA, const float* dBx, const float* 
     const int B_ = (int)batch, L_ = (int)seqlen, D_ = (int)d_inner;
     const unsigned g_lane = (unsigned)((lanes + 255) / 256);
     const unsigned g_all = (unsigned)((batch * ncs * d_inner + 255) / 256);
-    if (seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && batch * seqlen * d_inner < ((int64_t)1 << 30)) {
+    if (seqlen <= ak::kDiagWgLC * ak::kDiagWgLC && d_inner >= ak::kDiagWgCh / 2 &&
+        batch * seqlen * d_inner < ((int64_t)1 << 30)) {
       // aggregates and carries in one launch (its own plan: at most 32 chunks
       // of at most 32 steps), then the 32-step sweep on the same chunks
       const int nck = (int)((seqlen + ak::kDiagWgLC - 1) / ak::kDiagWgLC);

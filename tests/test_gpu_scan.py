@@ -320,13 +320,13 @@ def test_diag_scan_chunk_plans(shp):
     against the float64 oracle: the smallest chunked lengths (32, 33 steps),
     a short last chunk (1000 = 58 x 17 + 14), the 64-chunk cap (5000 steps),
     AMADEUS's width, and shapes that stay sequential (31 steps; 2^17 lanes).
-    Up to 1024 steps (every chunked shape here but the 2000- and 5000-step
-    ones) the forward takes one launch and the backward its workgroup carry
-    kernel and the 32-step sweep (AMADEUS: 32 chunks of 32 steps; 1000 = 31 x
-    32 + 8; 777 = 24 x 32 + 9 steps over 1000 channels, whose last block of 32
-    holds 8). Longer sequences run the chunked passes: chunks of 17-32 steps in
-    the 32-step register kernels (2000 = 62 x 32 + 16), longer ones streaming
-    (5000 steps)."""
+    Up to 1024 steps and from 16 channels the forward takes one launch and
+    the backward its workgroup carry kernel and the 32-step sweep (AMADEUS: 32
+    chunks of 32 steps; 1000 = 31 x 32 + 8 over 33 channels; 777 = 24 x 32 + 9
+    steps over 1000 channels, whose last block of 32 holds 8; 256 and 64
+    steps). Fewer channels or longer sequences run the chunked passes: chunks
+    of up to 32 steps in the register kernels (1, 3 and 7 channels; 2000 = 62
+    x 32 + 16 steps), longer ones streaming (5000 steps)."""
     need_gpu()
     from kernels.hip import selective_scan, selective_scan_backward
     g = torch.Generator().manual_seed(sum(shp) + 5)
